@@ -1,0 +1,231 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so). Test infrastructure: the checker only."""
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+LIB_PATH = ROOT / "oracle" / "liboracle.so"
+
+F32, F16, BF16, FP8, INT4 = 0, 1, 2, 3, 4
+SWIGLU, SIGMOID_GATE, GATED_ADD, ADD_BIAS, GELU_TANH, ADD, SILU = range(7)
+
+
+class Params(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("m", "n", "k")] + [("scale", ctypes.c_float)] + [
+        (n, ctypes.c_uint32) for n in ("x_stride", "w_stride", "y_stride", "x_offset", "w_offset", "y_offset", "width",
+                                       "cin", "k_split")]
+
+
+def _load():
+    if not LIB_PATH.exists():
+        subprocess.run(["make", "-C", str(LIB_PATH.parent)], check=True, capture_output=True)
+    lib = ctypes.CDLL(str(LIB_PATH))
+    P = ctypes.c_void_p
+    u8, u16, u32, i64, f, d, sz = (ctypes.c_uint8, ctypes.c_uint16, ctypes.c_uint32, ctypes.c_int64, ctypes.c_float,
+                                   ctypes.c_double, ctypes.c_size_t)
+    sig = {
+        "or_e4m3": (d, [u8]), "or_e4m3_gpu": (f, [u8]), "or_e5m2": (d, [u8]), "or_f16": (d, [u16]),
+        "or_bf16": (f, [u16]), "or_f32_to_bf16": (u16, [f]), "or_f32_to_f16": (u16, [f]),
+        "or_unpack_fp8": (None, [P, sz, f, P]), "or_int4_value": (f, [u32, ctypes.c_int, u16]),
+        "or_dequant_int4": (None, [P, P, sz, sz, sz, P]),
+        "or_lcg_next": (u32, [P]), "or_lcg_uniform": (d, [P]),
+        "or_matmul_test_data": (None, [u32, u32, u32, u32, P, P]),
+        "or_mt_seed": (None, [P, ctypes.c_uint64]), "or_mt_next": (u32, [P]),
+        "or_torch_randn": (None, [sz, ctypes.c_uint64, P]),
+        "or_matmul_params_make": (ctypes.c_int, [u32, u32, u32, f, i64, i64, i64, i64, i64, i64, i64, P, P, sz]),
+        "or_ksplit_for": (u32, [u32, u32, u32]), "or_ksplit_chunk": (u32, [u32, u32]),
+        "or_matmul_f64": (None, [P, ctypes.c_int, P, ctypes.c_int, P, P, u32, ctypes.c_int, P]),
+        "or_matmul_f64_rows": (None, [P, ctypes.c_int, P, ctypes.c_int, P, P, u32, u32, u32, P]),
+        "or_layer_sum": (None, [u32, u32, u32, P, P, P]),
+        "or_rmsnorm_f64": (None, [sz, sz, d, d, P, P, P, P, P]),
+        "or_rope_positions": (None, [u32, u32, u32, u32, P]),
+        "or_rope_tables": (ctypes.c_int, [P, u32, P, u32, d, P, P]),
+        "or_rope_rotate_f64": (None, [u32, u32, u32, ctypes.c_int, P, P, P, P]),
+        "or_gelu_tanh": (d, [d]), "or_gelu_tanh_shader": (f, [f]), "or_sigmoid": (d, [d]),
+        "or_elementwise_f64": (None, [ctypes.c_int, sz, sz, P, P, P, P]),
+        "or_rel_error": (d, [P, P, sz]), "or_compare": (None, [P, P, sz, P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def c_contig(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def e4m3(b):
+    return lib.or_e4m3(b)
+
+
+def e4m3_table():
+    return np.array([lib.or_e4m3(b) for b in range(256)])
+
+
+def e4m3_gpu_table():
+    return np.array([lib.or_e4m3_gpu(b) for b in range(256)], dtype=np.float32)
+
+
+def unpack_fp8(data, scale):
+    data = c_contig(data, np.uint8)
+    out = np.empty(data.size, np.float32)
+    lib.or_unpack_fp8(ptr(data), data.size, scale, ptr(out))
+    return out
+
+
+def to_bf16(a):
+    a = c_contig(a, np.float32).ravel()
+    return np.array([lib.or_f32_to_bf16(float(v)) for v in a], dtype=np.uint16)
+
+
+def to_f16(a):
+    a = c_contig(a, np.float32).ravel()
+    return np.array([lib.or_f32_to_f16(float(v)) for v in a], dtype=np.uint16)
+
+
+def bf16_to_f32(h):
+    h = np.asarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def matmul_test_data(m, n, k, seed=1):
+    x = np.empty(m * k, np.float32)
+    w = np.empty(n * k, np.uint8)
+    lib.or_matmul_test_data(m, n, k, seed, ptr(x), ptr(w))
+    return x, w
+
+
+def lcg(seed, count):
+    s = ctypes.c_uint32(seed)
+    return np.array([lib.or_lcg_uniform(ctypes.byref(s)) for _ in range(count)])
+
+
+def torch_randn(n, seed):
+    out = np.empty(n, np.float32)
+    lib.or_torch_randn(n, seed, ptr(out))
+    return out
+
+
+def matmul_params(m, n, k, scale, x_stride=-1, w_stride=-1, y_stride=-1, x_offset=-1, w_offset=-1, y_offset=-1,
+                  k_split=1):
+    p = Params()
+    msg = ctypes.create_string_buffer(256)
+    rc = lib.or_matmul_params_make(m, n, k, scale, x_stride, w_stride, y_stride, x_offset, w_offset, y_offset,
+                                   k_split, ctypes.byref(p), msg, 256)
+    if rc:
+        raise ValueError(msg.value.decode())
+    return p
+
+
+def matmul(p, x_dtype, x, w_dtype, w, scales=None, group=0, split=False, accumulate=False, y=None, out_len=None):
+    """Float64 oracle matmul; returns the whole y buffer (size out_len, default rows * y_stride + y_offset)."""
+    rows = p.m * (p.k_split if split else 1)
+    if y is None:
+        y = np.zeros(out_len if out_len is not None else rows * p.y_stride + p.y_offset, np.float64)
+    else:
+        y = c_contig(y, np.float64).copy()
+    flags = (1 if split else 0) | (2 if accumulate else 0)
+    lib.or_matmul_f64(ctypes.byref(p), x_dtype, ptr(x), w_dtype, ptr(w), ptr(scales), group, flags, ptr(y))
+    return y
+
+
+def matmul_rows(p, x_dtype, x, w_dtype, w, row_begin, row_end, scales=None, group=0):
+    y = np.zeros(p.m * p.y_stride + p.y_offset, np.float64)
+    lib.or_matmul_f64_rows(ctypes.byref(p), x_dtype, ptr(x), w_dtype, ptr(w), ptr(scales), group, row_begin, row_end,
+                           ptr(y))
+    return y
+
+
+def ksplit_for(m, n, k):
+    return lib.or_ksplit_for(m, n, k)
+
+
+def ksplit_chunk(k, split):
+    return lib.or_ksplit_chunk(k, split)
+
+
+def layer_sum(tokens, layers, dim, x, w):
+    out = np.empty(tokens * dim, np.float64)
+    lib.or_layer_sum(tokens, layers, dim, ptr(c_contig(x, np.float32)), ptr(c_contig(w, np.float32)), ptr(out))
+    return out
+
+
+def rmsnorm(x, weight, eps=1e-5, offset=1.0, scale=None, shift=None):
+    x = c_contig(x, np.float32)
+    weight = c_contig(weight, np.float32)
+    d = weight.size
+    rows = x.size // d
+    out = np.empty(x.size, np.float64)
+    sc = None if scale is None else c_contig(scale, np.float32)
+    sh = None if shift is None else c_contig(shift, np.float32)
+    lib.or_rmsnorm_f64(rows, d, eps, offset, ptr(x), ptr(weight), ptr(sc), ptr(sh), ptr(out))
+    return out
+
+
+def rope_positions(text_tokens, rows, columns, axes):
+    pos = np.empty((text_tokens + rows * columns) * axes, np.float64)
+    lib.or_rope_positions(text_tokens, rows, columns, axes, ptr(pos))
+    return pos.reshape(-1, axes)
+
+
+def rope_tables(pos, axes, theta):
+    pos = c_contig(pos, np.float64)
+    tokens = pos.shape[0]
+    ax = np.array(axes, dtype=np.uint32)
+    pairs = int(sum(axes) // 2)
+    cos = np.empty(tokens * pairs, np.float32)
+    sin = np.empty(tokens * pairs, np.float32)
+    rc = lib.or_rope_tables(ptr(pos), tokens, ptr(ax), len(axes), theta, ptr(cos), ptr(sin))
+    if rc < 0:
+        raise ValueError("Every RoPE axis needs an even number of dims")
+    return cos, sin, pairs
+
+
+def rope_rotate(x, tokens, heads, pairs, cos, sin, half=False):
+    x = c_contig(x, np.float32)
+    out = np.empty(x.size, np.float64)
+    lib.or_rope_rotate_f64(tokens, heads, pairs, 1 if half else 0, ptr(x), ptr(c_contig(cos, np.float32)),
+                           ptr(c_contig(sin, np.float32)), ptr(out))
+    return out
+
+
+def elementwise(op, a, b=None, c=None, d=1):
+    a = c_contig(a, np.float32)
+    bb = None if b is None else c_contig(b, np.float32)
+    cc = None if c is None else c_contig(c, np.float32)
+    out = np.empty(a.size, np.float64)
+    lib.or_elementwise_f64(op, a.size, d, ptr(a), ptr(bb), ptr(cc), ptr(out))
+    return out
+
+
+def dequant_int4(words, scales, rows, k, group):
+    words = c_contig(words, np.uint32)
+    scales = c_contig(scales, np.uint16)
+    out = np.empty(rows * k, np.float32)
+    lib.or_dequant_int4(ptr(words), ptr(scales), rows, k, group, ptr(out))
+    return out
+
+
+def rel_error(got, ref):
+    got = c_contig(got, np.float64)
+    ref = c_contig(ref, np.float64)
+    return lib.or_rel_error(ptr(got), ptr(ref), ref.size)
+
+
+def compare(result, reference):
+    a = c_contig(result, np.float64)
+    b = c_contig(reference, np.float64)
+    cs, mx, rel = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    lib.or_compare(ptr(a), ptr(b), a.size, ctypes.byref(cs), ctypes.byref(mx), ctypes.byref(rel))
+    return {"cosine": cs.value, "maxError": mx.value, "relativeError": rel.value}

@@ -1,0 +1,377 @@
+"""Pins the CPU oracle before it is trusted as the checker of the HIP path.
+
+Sources of truth, none of them the oracle itself:
+  * known-answer values from the reference's own tests (tests/fp8.test.ts, tests/noise.test.ts,
+    tests/rope.test.ts, tests/gpu/fp8.test.ts, tests/gpu/matmul.test.ts, tests/gpu/rmsnorm.test.ts);
+  * the reference's fixture tests/fixtures/torch-randn.json (copied to tests/golden/);
+  * torch's float8_e4m3fn / bfloat16 / float16 / tanh-GELU (tests/golden/*.json, see make_golden.py);
+  * numpy float64 library routines (matmul, einsum, complex rotation, scipy's expit) on the same inputs.
+Each "plausible mistake" check shows that a dropped term, a transposed operand or a wrong index would
+fail the same comparison.
+"""
+import json
+import math
+import pathlib
+
+import numpy as np
+import pytest
+from scipy.special import expit
+
+import oracle_lib as O
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def load(name):
+    return json.loads((GOLDEN / name).read_text())
+
+
+E4M3_TORCH = np.array([float("nan") if v == "nan" else float(v) for v in load("e4m3fn.json")["decode"]])
+
+
+# ---------------------------------------------------------------------------------------------- decoders
+
+@pytest.mark.parametrize("byte,value", [(0x00, 0.0), (0x38, 1.0), (0xC0, -2.0), (0x7E, 448.0), (0x01, 2.0 ** -9),
+                                        (0x08, 2.0 ** -6), (0x3C, 1.5)])
+def test_e4m3_known_answers(byte, value):  # tests/fp8.test.ts:5-19
+    assert O.e4m3(byte) == value
+
+
+def test_e4m3_negative_zero_nan_no_infinity():  # tests/fp8.test.ts:21-25
+    assert O.e4m3(0x80) == 0.0 and math.copysign(1.0, O.e4m3(0x80)) < 0
+    assert math.isnan(O.e4m3(0x7F)) and math.isnan(O.e4m3(0xFF))
+
+
+def test_e4m3_all_codes_match_torch():
+    ours = O.e4m3_table()
+    nan = np.isnan(E4M3_TORCH)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan], E4M3_TORCH[~nan])
+    assert np.array_equal(np.signbit(ours[~nan]), np.signbit(E4M3_TORCH[~nan]))
+
+
+def test_shader_decoder_equals_cpu_decoder_and_has_no_nan_branch():  # tests/gpu/fp8.test.ts:21-28, kernels/fp8.ts:12-20
+    gpu = O.e4m3_gpu_table().astype(np.float64)
+    ref = E4M3_TORCH
+    ok = ~np.isnan(ref)
+    assert np.array_equal(gpu[ok], ref[ok])
+    assert np.array_equal(np.signbit(gpu[ok]), np.signbit(ref[ok]))
+    assert gpu[0x7F] == 480.0 and gpu[0xFF] == -480.0
+
+
+@pytest.mark.parametrize("byte,value", [(0x00, 0.0), (0x3C, 1.0), (0x7B, 57344.0), (0x01, 2.0 ** -16), (0xC0, -2.0),
+                                        (0x7C, math.inf), (0xFC, -math.inf)])
+def test_e5m2_known_answers(byte, value):  # tests/fp8.test.ts:27-41
+    assert O.lib.or_e5m2(byte) == value
+    assert math.isnan(O.lib.or_e5m2(0x7E))
+
+
+def test_f16_and_bf16_known_answers():  # tests/fp8.test.ts:44-50
+    assert [O.lib.or_bf16(h) for h in (0x3F80, 0xC000)] == [1.0, -2.0]
+    assert [O.lib.or_f16(h) for h in (0x3C00, 0xC000, 0x0001, 0x7C00)] == [1.0, -2.0, 2.0 ** -24, math.inf]
+    every = np.arange(65536, dtype=np.uint16)
+    ours = np.array([O.lib.or_f16(int(h)) for h in every])
+    lib = every.view(np.float16).astype(np.float64)
+    ok = ~np.isnan(lib)
+    assert np.array_equal(np.isnan(ours), ~ok) and np.array_equal(ours[ok], lib[ok])
+
+
+def test_unpack_fp8_scale_and_odd_length():  # tests/gpu/fp8.test.ts:30-37
+    s = 0.0018833705689758062
+    got = O.unpack_fp8(np.array([0x38, 0xC0, 0x7E], np.uint8), s)
+    want = np.array([1.0, -2.0, 448.0], np.float32) * np.float32(s)
+    assert np.array_equal(got, want)
+    assert O.unpack_fp8(np.array([0x38, 0x38, 0x38, 0x38, 0x40], np.uint8), 1.0).tolist() == [1, 1, 1, 1, 2]
+
+
+def test_float_conversions_match_torch():
+    g = load("convert.json")
+    f = np.array(g["f32_bits"], np.uint32).view(np.float32)
+    assert O.to_bf16(f).tolist() == g["bf16"]
+    assert O.to_f16(f).tolist() == g["f16"]
+    # numpy's own float16 rounding agrees as a second library
+    with np.errstate(over="ignore"):
+        assert np.array_equal(O.to_f16(f), f.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------------- generators
+
+def test_lcg_sequence():  # tests/gpu/matmul.test.ts:10-12
+    s, want = 1, []
+    for _ in range(5):
+        s = (s * 1664525 + 1013904223) % 2 ** 32
+        want.append(s / 2 ** 32)
+    assert O.lcg(1, 5).tolist() == want
+
+
+def test_matmul_test_data_layout():  # tests/gpu/matmul.test.ts:14-23: x first, then w; no NaN codes
+    m, n, k = 37, 70, 100
+    x, w = O.matmul_test_data(m, n, k, 1)
+    u = O.lcg(1, m * k + n * k)
+    assert np.array_equal(x, (u[: m * k] * 2 - 1).astype(np.float32))
+    b = np.floor(u[m * k:] * 256).astype(np.int64)
+    b = np.where((b & 0x7F) == 0x7F, b - 1, b)
+    assert np.array_equal(w, b.astype(np.uint8))
+    assert not np.any((w & 0x7F) == 0x7F)
+
+
+def test_mt19937_known_answers():  # tests/noise.test.ts:11-20
+    import ctypes
+    mt = (ctypes.c_uint32 * 625)()
+    O.lib.or_mt_seed(mt, 5489)
+    last = 0
+    for _ in range(10000):
+        last = O.lib.or_mt_next(mt)
+    assert last == 4123659995
+    a, b = (ctypes.c_uint32 * 625)(), (ctypes.c_uint32 * 625)()
+    O.lib.or_mt_seed(a, 2 ** 32 + 7)
+    O.lib.or_mt_seed(b, 7)
+    assert O.lib.or_mt_next(a) == O.lib.or_mt_next(b)
+
+
+def test_torch_randn_known_answers_and_fixture():  # tests/noise.test.ts:25-45
+    r4 = lambda a: [round(float(v), 4) for v in a]
+    assert r4(O.torch_randn(6, 0)) == [1.541, -0.2934, -2.1788, 0.5684, -1.0845, -1.3986]
+    assert r4(O.torch_randn(3, 42)) == [0.3367, 0.1288, 0.2345]
+    assert r4(O.torch_randn(16, 0)) == [-1.1258, -1.1524, -0.2506, -0.4339, 0.8487, 0.692, -0.316, -2.1152, 0.3223,
+                                        -1.2633, 0.35, 0.3081, 0.1198, 1.2377, 1.1168, -0.2473]
+    for case in load("torch-randn.json")["cases"]:
+        a = O.torch_randn(case["n"], case["seed"])
+        for i, v in case["values"].items():
+            assert abs(a[int(i)] - v) < 5e-7, (case["n"], case["seed"], i)
+
+
+# ---------------------------------------------------------------------------------------------- matmul
+
+def np_matmul(x, wdec, m, n, k, scale):
+    return (x.astype(np.float64).reshape(m, k) @ wdec.astype(np.float64).reshape(n, k).T * scale).ravel()
+
+
+@pytest.mark.parametrize("m,n,k,scale,seed", [(1, 1, 4, 0.002, 1), (37, 70, 100, 0.002, 1), (64, 64, 64, 0.002, 1),
+                                              (130, 65, 36, 0.002, 1), (200, 260, 84, 0.002, 1),
+                                              (8, 1536, 512, 0.0018833705689758062, 7)])
+def test_fp8_matmul_oracle_matches_numpy(m, n, k, scale, seed):  # tests/gpu/matmul.test.ts:49-66
+    x, w = O.matmul_test_data(m, n, k, seed)
+    p = O.matmul_params(m, n, k, scale)
+    got = O.matmul(p, O.F32, x, O.FP8, w)
+    want = np_matmul(x, E4M3_TORCH[w], m, n, k, np.float32(scale))
+    assert O.rel_error(got, want) < 1e-12
+    if min(n, k) > 1 and n != k:  # a transposed W cannot pass
+        wrong = np_matmul(x, E4M3_TORCH[w].reshape(n, k).T.copy().ravel()[: n * k], m, n, k, np.float32(scale))
+        assert O.rel_error(got, wrong) > 1e-3
+    if k > 4:  # a dropped last k term cannot pass
+        wd = E4M3_TORCH[w].reshape(n, k).copy()
+        wd[:, -1] = 0
+        assert O.rel_error(got, np_matmul(x, wd.ravel(), m, n, k, np.float32(scale))) > 1e-6
+
+
+def test_matmul_params_validation():  # tests/gpu/matmul.test.ts:68-72, kernels/matmul.ts:205-207
+    with pytest.raises(ValueError, match="K must be a multiple of 4, got 6"):
+        O.matmul_params(1, 1, 6, 1.0)
+    with pytest.raises(ValueError, match="xStride"):
+        O.matmul_params(1, 1, 4, 1.0, x_stride=6)
+    with pytest.raises(ValueError, match="wOffset"):
+        O.matmul_params(1, 1, 4, 1.0, w_offset=2)
+    p = O.matmul_params(3, 5, 8, 0.5)
+    assert (p.x_stride, p.w_stride, p.y_stride, p.k_split) == (8, 8, 5, 1)
+
+
+def test_ksplit_known_answers():  # tests/gpu/matmul.test.ts:151-156
+    assert O.ksplit_for(1088, 64, 6144) == 24
+    assert O.ksplit_for(4160, 64, 16384) == 8
+    assert O.ksplit_for(4160, 6144, 6144) == 1
+    assert O.ksplit_for(5, 12, 16) == 1
+    assert O.ksplit_chunk(200, 3) == 80  # slices of 80, 80, 40 (tests/gpu/matmul.test.ts:133)
+
+
+def test_split_k_partials_sum_to_the_full_product():  # tests/gpu/matmul.test.ts:131-149
+    m, n, k, split, scale = 5, 12, 200, 3, 0.5
+    x, w = O.matmul_test_data(m, n, k, 3)
+    p = O.matmul_params(m, n, k, scale, k_split=split)
+    parts = O.matmul(p, O.F32, x, O.FP8, w, split=True).reshape(split, m * n)
+    want = np_matmul(x, E4M3_TORCH[w], m, n, k, scale)
+    assert np.allclose(parts.sum(0), want, rtol=0, atol=1e-9)
+    assert abs(parts[0, 0] - want[0]) > 1e-3
+    wd = E4M3_TORCH[w].reshape(n, k)
+    assert np.allclose(parts[2], np_matmul(x.reshape(m, k)[:, 160:].ravel(), wd[:, 160:].ravel(), m, n, 40, scale))
+
+
+def test_accumulate_adds_to_y():  # tests/gpu/matmul.test.ts:159-175
+    m, n, k, scale = 3, 6, 8, 0.25
+    x = (np.arange(m * k) % 5 - 2).astype(np.float32)
+    w = ((np.arange(n * k) * 3) % 7 - 3).astype(np.float32)
+    start = np.arange(m * n, dtype=np.float64)
+    p = O.matmul_params(m, n, k, scale)
+    plain = O.matmul(p, O.F32, x, O.F32, w)
+    got = O.matmul(p, O.F32, x, O.F32, w, accumulate=True, y=start)
+    assert np.array_equal(got, plain + start)
+
+
+def test_strided_head_pick():  # tests/gpu/matmul.test.ts:93-109
+    tokens, heads, kv, dim = 20, 4, 2, 128
+    rng = np.random.default_rng(3)
+    q = rng.uniform(-1, 1, tokens * heads * dim).astype(np.float32)
+    kk = rng.uniform(-1, 1, tokens * kv * dim).astype(np.float32)
+    h, g = 2, 1
+    p = O.matmul_params(tokens, tokens, dim, 1.0, x_stride=heads * dim, x_offset=h * dim, w_stride=kv * dim,
+                        w_offset=g * dim, y_stride=24)
+    got = O.matmul(p, O.F32, q, O.F32, kk, out_len=tokens * 24).reshape(tokens, 24)[:, :tokens]
+    want = q.reshape(tokens, heads, dim)[:, h].astype(np.float64) @ kk.reshape(tokens, kv, dim)[:, g].astype(np.float64).T
+    assert np.abs(got - want).max() < 1e-9
+
+
+def test_bf16_and_half_activation_matmul():  # tests/gpu/matmul.test.ts:112-127
+    m, n, k = 37, 70, 100
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-1, 1, m * k).astype(np.float32)
+    wf = rng.uniform(-1, 1, n * k).astype(np.float32)
+    wb = (wf.view(np.uint32) >> 16).astype(np.uint16)  # truncation, as the reference test does
+    p = O.matmul_params(m, n, k, 0.5)
+    got = O.matmul(p, O.F32, x, O.BF16, wb)
+    assert O.rel_error(got, np_matmul(x, O.bf16_to_f32(wb), m, n, k, 0.5)) < 1e-12
+    xh = x.astype(np.float16)
+    got = O.matmul(p, O.F16, xh.view(np.uint16), O.BF16, wb)
+    assert O.rel_error(got, np_matmul(xh.astype(np.float32), O.bf16_to_f32(wb), m, n, k, 0.5)) < 1e-12
+    xb = O.to_bf16(x)
+    got = O.matmul(p, O.BF16, xb, O.FP8, np.zeros(n * k, np.uint8) + 0x38)
+    assert O.rel_error(got, np_matmul(O.bf16_to_f32(xb), np.ones(n * k), m, n, k, 0.5)) < 1e-12
+
+
+def np_int4_dequant(words, scales, rows, k, group):
+    nib = (words[:, None] >> (4 * np.arange(8, dtype=np.uint32))[None, :]) & 0xF
+    q = np.where(nib >= 8, nib.astype(np.int64) - 16, nib.astype(np.int64)).reshape(rows, k)
+    s = scales.view(np.float16).astype(np.float64).reshape(rows, k // group)
+    return q * np.repeat(s, group, axis=1)
+
+
+def test_int4_every_code_and_scale():
+    scales = np.array([0x3C00, 0x2E66, 0x1400, 0x8001, 0xBC00, 0x0000], np.uint16)
+    for s in scales:
+        for code in range(16):
+            word = code << 12  # nibble 3
+            q = code - 16 if code >= 8 else code
+            v = O.lib.or_int4_value(word, 3, int(s))
+            assert v == np.float32(q * float(np.array([s], np.uint16).view(np.float16)[0]))
+
+
+@pytest.mark.parametrize("m,n,k,group", [(1, 40, 128, 64), (8, 33, 256, 64), (16, 17, 192, 64), (3, 9, 96, 32)])
+def test_int4_gemv_oracle_matches_numpy(m, n, k, group):
+    rng = np.random.default_rng(m * 100 + n)
+    words = rng.integers(0, 2 ** 32, n * k // 8, dtype=np.uint64).astype(np.uint32)
+    scales = np.abs(rng.normal(0, 0.01, n * k // group)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(m * k).astype(np.float16)
+    p = O.matmul_params(m, n, k, 1.0)
+    got = O.matmul(p, O.F16, x.view(np.uint16), O.INT4, words, scales=scales, group=group)
+    wd = np_int4_dequant(words, scales, n, k, group)
+    want = (x.astype(np.float64).reshape(m, k) @ wd.T).ravel()
+    assert O.rel_error(got, want) < 1e-12
+    assert np.array_equal(O.dequant_int4(words, scales, n, k, group), wd.astype(np.float32).ravel())
+    # a wrong nibble order (high nibble first) cannot pass
+    swapped = ((words & 0x0F0F0F0F) << 4) | ((words >> 4) & 0x0F0F0F0F)
+    wrong = (x.astype(np.float64).reshape(m, k) @ np_int4_dequant(swapped, scales, n, k, group).T).ravel()
+    assert O.rel_error(got, wrong) > 1e-3
+
+
+def test_layer_sum_matches_einsum():  # src/kernels/text.ts:67-84
+    t, layers, dim = 7, 3, 11
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(t * layers * dim).astype(np.float32)
+    w = np.array([1.0, 0.5, -2.0], np.float32)
+    want = np.einsum("tld,l->td", x.reshape(t, layers, dim).astype(np.float64), w.astype(np.float64)).ravel()
+    assert np.abs(O.layer_sum(t, layers, dim, x, w) - want).max() < 1e-12
+
+
+# ---------------------------------------------------------------------------------------------- rmsnorm / rope / elementwise
+
+def np_rmsnorm(x, w, d, eps, offset, scale, shift):
+    xr = x.astype(np.float64).reshape(-1, d)
+    inv = 1.0 / np.sqrt((xr * xr).mean(1, keepdims=True) + eps)
+    return (xr * inv * (offset + w.astype(np.float64)) * (1 + scale.astype(np.float64)) + shift).ravel()
+
+
+@pytest.mark.parametrize("rows,d,offset,mod", [(3, 6144, 1.0, True), (100, 128, 0.0, False), (5, 37, 1.0, False)])
+def test_rmsnorm_oracle(rows, d, offset, mod):  # tests/gpu/rmsnorm.test.ts:25-48
+    rng = np.random.default_rng(d)
+    x = rng.uniform(-4, 4, rows * d).astype(np.float32)
+    w = rng.uniform(-0.1, 0.1, d).astype(np.float32)
+    sc = rng.uniform(-1, 1, d).astype(np.float32) if mod else np.zeros(d, np.float32)
+    sh = rng.uniform(-1, 1, d).astype(np.float32) if mod else np.zeros(d, np.float32)
+    got = O.rmsnorm(x, w, 1e-5, offset, sc if mod else None, sh if mod else None)
+    want = np_rmsnorm(x, w, d, 1e-5, offset, sc, sh)
+    assert np.abs(got - want).max() < 1e-12
+    assert np.abs(got - np_rmsnorm(x, w, d, 1e-5, 1.0 - offset, sc, sh)).max() > 1e-3  # offset matters
+
+
+def test_rope_positions_known_answer():  # tests/rope.test.ts:4-17
+    assert O.rope_positions(2, 2, 3, 3).tolist() == [[0, 0, 0], [0, 0, 0], [0, 0, 0], [0, 0, 1], [0, 0, 2], [0, 1, 0],
+                                                    [0, 1, 1], [0, 1, 2]]
+
+
+def test_rope_tables_known_answers():  # tests/rope.test.ts:19-39
+    cos, sin, pairs = O.rope_tables(np.zeros((1, 3)), [32, 48, 48], 1000.0)
+    assert pairs == 64 and cos.tolist() == [1.0] * 64 and sin.tolist() == [0.0] * 64
+    cos, sin, _ = O.rope_tables(np.array([[0.0, 3.0, 5.0]]), [32, 48, 48], 1000.0)
+    ang = lambda pos, j, dim: pos * 1000.0 ** (-(2 * j) / dim)
+    assert sin[0] == 0
+    assert abs(cos[16] - math.cos(ang(3, 0, 48))) < 5e-7
+    assert abs(sin[16 + 5] - math.sin(ang(3, 5, 48))) < 5e-7
+    assert abs(sin[40 + 23] - math.sin(ang(5, 23, 48))) < 5e-7
+    with pytest.raises(ValueError, match="even"):
+        O.rope_tables(np.zeros((1, 3)), [31, 48, 49], 1000.0)
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_rope_rotation_matches_complex_multiply(half):  # tests/gpu/rope.test.ts:5-42
+    pos = O.rope_positions(2, 3, 4, 3)
+    tokens, heads = pos.shape[0], 3
+    cos, sin, pairs = O.rope_tables(pos, [32, 48, 48], 1000.0)
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-1, 1, tokens * heads * pairs * 2).astype(np.float32)
+    got = O.rope_rotate(x, tokens, heads, pairs, cos, sin, half)
+    xr = x.astype(np.float64).reshape(tokens, heads, 2, pairs) if half else x.astype(np.float64).reshape(
+        tokens, heads, pairs, 2)
+    z = xr[:, :, 0, :] + 1j * xr[:, :, 1, :] if half else xr[..., 0] + 1j * xr[..., 1]
+    e = (cos.astype(np.float64) + 1j * sin.astype(np.float64)).reshape(tokens, 1, pairs)
+    r = z * e
+    want = np.stack([r.real, r.imag], axis=2 if half else 3).ravel()
+    assert np.abs(got - want).max() < 1e-12
+    assert np.array_equal(got[: 2 * heads * pairs * 2], x[: 2 * heads * pairs * 2])  # text tokens unchanged
+    wrong = np.stack([r.real, -r.imag], axis=2 if half else 3).ravel()  # the opposite rotation cannot pass
+    assert np.abs(got - wrong).max() > 1e-3
+
+
+def test_gelu_matches_torch_and_shader_form():  # tests/gpu/text.test.ts:56-60, kernels/elementwise.ts:25-29
+    g = load("gelu.json")
+    ours = np.array([O.lib.or_gelu_tanh(v) for v in g["x"]])
+    assert np.abs(ours - np.array(g["gelu"])).max() < 1e-12
+    shader = np.array([O.lib.or_gelu_tanh_shader(v) for v in g["x"]], np.float64)
+    assert np.abs(shader - np.array(g["gelu"])).max() < 1e-5
+
+
+def test_elementwise_ops_match_scipy():  # src/kernels/elementwise.ts:38-84, tests/gpu/elementwise.test.ts:15-40
+    n, d = 1000, 40
+    rng = np.random.default_rng(1)
+    a, b = (rng.uniform(-8, 8, n).astype(np.float32) for _ in range(2))
+    g = rng.uniform(-1, 1, d).astype(np.float32)
+    A, B, G = a.astype(np.float64), b.astype(np.float64), g.astype(np.float64)
+    cases = {
+        O.SWIGLU: (A * expit(A) * B, dict(b=b)),
+        O.SIGMOID_GATE: (A * expit(B), dict(b=b)),
+        O.GATED_ADD: (A + np.tile(G, n // d) * B, dict(b=b, c=g, d=d)),
+        O.ADD_BIAS: (A + np.tile(G, n // d), dict(b=g, d=d)),
+        O.ADD: (A + B, dict(b=b)),
+        O.SILU: (A * expit(A), {}),
+    }
+    for op, (want, kw) in cases.items():
+        assert np.abs(O.elementwise(op, a, **kw) - want).max() < 1e-12, op
+
+
+def test_compare_known_answers():  # src/model/compare.ts:2-17
+    a = np.array([1.0, 2.0, 3.0])
+    r = O.compare(a, a)
+    assert r["cosine"] == pytest.approx(1.0) and r["maxError"] == 0 and r["relativeError"] == 0
+    r = O.compare(2 * a, a)
+    assert r["cosine"] == pytest.approx(1.0) and r["maxError"] == 3 and r["relativeError"] == pytest.approx(1.0)
+    r = O.compare(np.array([1.0, 0.0]), np.array([0.0, 1.0]))
+    assert r["cosine"] == 0 and r["relativeError"] == pytest.approx(math.sqrt(2))
+    assert O.rel_error(np.array([1.0, 2.5]), np.array([1.0, 2.0])) == pytest.approx(0.25)
