@@ -1,0 +1,141 @@
+/*
+ * we.h — C ABI of the MI355X (gfx950) quantized-weight matmul path.
+ *
+ * Plain C: pointers, sizes and integer status codes; no PyTorch or HIP types in any signature.
+ * Every entry point returns WE_OK (0) or an error code and leaves a message in we_last_error(ctx).
+ * Device buffers are plain device pointers owned by the context (like the reference's Graph owns its
+ * GPUBuffers). All work is queued in order on the context's compute stream; results are visible to
+ * the host after we_buf_download or we_sync.
+ *
+ * Each declaration names the reference interface it replaces (paths in the dotstories/web-engine tree).
+ */
+#ifndef WE_H
+#define WE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define WE_OK 0
+#define WE_EINVAL 1       /* bad shape / stride / alignment / argument; message = the reference's text */
+#define WE_ENOMEM 2       /* device or pinned-host allocation failed */
+#define WE_EHIP 3         /* a HIP runtime call failed; message carries hipGetErrorString */
+#define WE_EUNSUPPORTED 4 /* a dtype combination or mode this build does not implement */
+
+/* dtype tags (activations, weights, outputs) */
+#define WE_F32 0
+#define WE_F16 1
+#define WE_BF16 2
+#define WE_FP8_E4M3 3 /* OCP float8_e4m3fn, one byte per value, K contiguous */
+#define WE_INT4 4     /* 8 two's-complement nibbles per LE u32 along K, low nibble first; f16 scale per group */
+
+/* matmul epilogue flags (combinable; applied in this order: scale, bias, gelu, accumulate) */
+#define WE_EPI_ACCUMULATE 1u /* y += ... (src/kernels/matmul.ts:145) */
+#define WE_EPI_SPLIT_K 2u    /* slice z of K into rows z*M.. of y (src/kernels/matmul.ts:155-159) */
+#define WE_EPI_BIAS 4u       /* + bias[col] (f32), the addBias pass of src/model/ops.ts:65 fused */
+#define WE_EPI_GELU_TANH 8u  /* tanh GELU of the result (src/kernels/elementwise.ts:25-29) fused */
+
+/* elementwise ops (src/kernels/elementwise.ts:38-84) */
+#define WE_OP_SWIGLU 0       /* out = silu(a) * b */
+#define WE_OP_SIGMOID_GATE 1 /* out = a * sigmoid(b) */
+#define WE_OP_GATED_ADD 2    /* out = a + c[i % d] * b */
+#define WE_OP_ADD_BIAS 3     /* out = a + b[i % d] */
+#define WE_OP_GELU_TANH 4    /* out = gelu_tanh(a) */
+#define WE_OP_ADD 5          /* out = a + b */
+#define WE_OP_SILU 6         /* out = a * sigmoid(a) */
+
+typedef struct we_ctx we_ctx;
+
+/* Binary image of the reference's matmul Params buffer: 13 x u32, scale stored as f32
+ * (src/kernels/matmul.ts:120-126). Strides and offsets are in values, not bytes. */
+typedef struct we_matmul_params {
+  uint32_t m, n, k;
+  float scale;
+  uint32_t x_stride, w_stride, y_stride;
+  uint32_t x_offset, w_offset, y_offset;
+  uint32_t width, cin; /* conv3x3 only in the reference; must be 0 here */
+  uint32_t k_split;
+} we_matmul_params;
+
+/* ---- context: replaces getDevice (src/gpu/compute.ts:6-20) and the Graph object (src/gpu/graph.ts:26-35) ---- */
+int we_ctx_create(int device, we_ctx** out);
+int we_ctx_destroy(we_ctx* ctx);
+const char* we_last_error(const we_ctx* ctx);
+/* device name, compute-unit count, LDS bytes per workgroup (for reports) */
+int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units, int* lds_bytes);
+
+/* ---- buffers: Graph.buffer / free / release / mark / copy / read / stats (src/gpu/graph.ts:38-139) ---- */
+int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out);  /* zeroed, size-keyed pool */
+int we_buf_free(we_ctx* ctx, void* buf);                   /* back to the pool; later use is stream-ordered */
+int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t bytes); /* queue.writeBuffer */
+int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size_t bytes); /* Graph.read */
+int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes);
+int we_mark(we_ctx* ctx, size_t* mark);                                         /* Graph.mark */
+int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep);     /* Graph.release */
+int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes); /* Graph.stats */
+int we_sync(we_ctx* ctx); /* device.queue.onSubmittedWorkDone(), called from src/model/weights.ts:128 */
+
+/* ---- pinned host memory and weight streaming: replaces the per-block upload pacing of
+ * loadTransformer (src/model/weights.ts:124-129) and runAhead (src/gpu/run-ahead.ts:7-21) ---- */
+int we_host_alloc(we_ctx* ctx, size_t bytes, void** out); /* pinned (hipHostMalloc) */
+int we_host_free(we_ctx* ctx, void* ptr);
+/* enqueue dst <- pinned src on the copy stream after the compute work recorded by `after` (0 = none);
+ * returns a ticket that compute can wait on */
+int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket);
+int we_wait_ticket(we_ctx* ctx, uint64_t ticket);   /* compute stream waits for a copy ticket */
+int we_record_compute(we_ctx* ctx, uint64_t* ticket); /* ticket for the compute work queued so far */
+int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done);
+
+/* ---- timing on the compute stream (hipEvents) ---- */
+int we_timer_start(we_ctx* ctx);
+int we_timer_stop(we_ctx* ctx, float* ms);
+
+/* ---- matmul: matmulParams (src/kernels/matmul.ts:198-212) and kSplitFor (src/model/ops.ts:42-45) ---- */
+/* negative stride/offset = the reference's default; fails with "<name> must be a multiple of 4, got v" */
+int we_matmul_params_make(we_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, float scale, int64_t x_stride,
+                          int64_t w_stride, int64_t y_stride, int64_t x_offset, int64_t w_offset, int64_t y_offset,
+                          int64_t k_split, we_matmul_params* out);
+uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
+
+/* y = x . W^T * scale with W [N, K] as stored (fp8 / bf16 / f16 / f32 / int4). Replaces matmulWgsl
+ * (src/kernels/matmul.ts:118-178) dispatched by linear() (src/model/ops.ts:61-73).
+ * x: x_dtype in {F32, F16, BF16}; y: y_dtype in {F32, F16, BF16}; w_scales: int4 only, f16 [N, K/group];
+ * bias: f32 [N] with WE_EPI_BIAS. Accumulation is fp32 on bf16/f16 MFMA (f32 inputs are split into
+ * two bf16 terms, keeping ~16 mantissa bits). */
+int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+              const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
+
+/* ---- norms and rotary: rmsnormWgsl (src/kernels/rmsnorm.ts:13-48) / norm() (src/model/ops.ts:78-82),
+ * ropeKernel (src/kernels/rope.ts:59-77) / rotate() (src/model/ops.ts:89-93) ---- */
+/* out = x / sqrt(mean(x^2) + eps) * (offset + weight) * (1 + scale) + shift; scale/shift may be NULL */
+int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+               const float* weight, const float* scale, const float* shift, void* out);
+/* x [tokens, heads, 2*pairs]; cos/sin f32 [tokens, pairs]; half = 0 interleaved pairs, 1 (j, j+pairs) */
+int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
+            const float* cos_t, const float* sin_t, void* out);
+/* the q/k path of attend() (src/model/block.ts:53-56) in one pass: per-head RMSNorm (offset, eps) of
+ * x [tokens, heads, head_dim], then RoPE on tokens >= rope_from (earlier tokens are only normalized);
+ * cos/sin rows are indexed by token. */
+int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
+                    const float* weight, uint32_t rope_from, int half, const float* cos_t, const float* sin_t,
+                    int dtype, const void* x, void* out);
+
+/* ---- elementwise and reductions (src/kernels/elementwise.ts:38-84, src/kernels/text.ts:67-84) ---- */
+int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,
+                   void* out);
+int we_layer_sum(we_ctx* ctx, uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w,
+                 float* out);
+
+/* ---- dequantization test kernels: unpackFp8 (src/kernels/fp8.ts:24-36) and the int4 format ---- */
+int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale, float* out);
+int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, uint32_t rows, uint32_t k,
+                    uint32_t group, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

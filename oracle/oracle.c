@@ -131,6 +131,12 @@ uint32_t or_lcg_next(uint32_t* state) {
 }
 double or_lcg_uniform(uint32_t* state) { return or_lcg_next(state) / 4294967296.0; }
 
+/* n consecutive draws of the generator above, as doubles in [0, 1). */
+void or_lcg_fill(uint32_t seed, size_t n, double* out) {
+  uint32_t s = seed;
+  for (size_t i = 0; i < n; i++) out[i] = or_lcg_uniform(&s);
+}
+
 /* tests/gpu/matmul.test.ts:14-23 — x (f32) first, uniform in [-1, 1); then fp8 bytes, NaN codes moved
  * down by one. */
 void or_matmul_test_data(uint32_t m, uint32_t n, uint32_t k, uint32_t seed, float* x, uint8_t* w) {

@@ -40,6 +40,7 @@ void or_dequant_int4(const uint32_t* words, const uint16_t* scales, size_t rows,
 /* ---- seeded generators ---- */
 uint32_t or_lcg_next(uint32_t* state);
 double or_lcg_uniform(uint32_t* state);
+void or_lcg_fill(uint32_t seed, size_t n, double* out);
 void or_matmul_test_data(uint32_t m, uint32_t n, uint32_t k, uint32_t seed, float* x, uint8_t* w);
 typedef struct { uint32_t state[624]; int index; } or_mt19937;
 void or_mt_seed(or_mt19937* mt, uint64_t seed);

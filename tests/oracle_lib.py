@@ -30,7 +30,7 @@ def _load():
         "or_bf16": (f, [u16]), "or_f32_to_bf16": (u16, [f]), "or_f32_to_f16": (u16, [f]),
         "or_unpack_fp8": (None, [P, sz, f, P]), "or_int4_value": (f, [u32, ctypes.c_int, u16]),
         "or_dequant_int4": (None, [P, P, sz, sz, sz, P]),
-        "or_lcg_next": (u32, [P]), "or_lcg_uniform": (d, [P]),
+        "or_lcg_next": (u32, [P]), "or_lcg_uniform": (d, [P]), "or_lcg_fill": (None, [u32, sz, P]),
         "or_matmul_test_data": (None, [u32, u32, u32, u32, P, P]),
         "or_mt_seed": (None, [P, ctypes.c_uint64]), "or_mt_next": (u32, [P]),
         "or_torch_randn": (None, [sz, ctypes.c_uint64, P]),
@@ -107,8 +107,17 @@ def matmul_test_data(m, n, k, seed=1):
 
 
 def lcg(seed, count):
-    s = ctypes.c_uint32(seed)
-    return np.array([lib.or_lcg_uniform(ctypes.byref(s)) for _ in range(count)])
+    out = np.empty(count, np.float64)
+    lib.or_lcg_fill(seed, count, ptr(out))
+    return out
+
+
+def bf16_rne(a):
+    """Vectorised f32 -> bf16 bits, round to nearest even (checked against or_f32_to_bf16 in test_oracle)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
 
 
 def torch_randn(n, seed):

@@ -1,0 +1,269 @@
+"""GEMM parity on the GPU through the C-ABI, against the float64 oracle.
+Mirrors tests/gpu/matmul.test.ts (shapes, LCG inputs, error definition) and adds the dtype matrix,
+every tile configuration, the fused epilogues and full-size shapes (sampled rows + exact properties).
+
+Tolerances (max|y - ref| / max|ref|, tests/gpu/matmul.test.ts:38-46):
+  * f32 / f16 / bf16 inputs with an f32 output: 1e-5, the reference's own bar (f32 operands are split
+    into three bf16 terms, exact; every other operand is exact in the MFMA type; only the f32
+    accumulation rounds);
+  * f16 output: 2e-3 (one f16 rounding is 2^-11 of the value);  bf16 output: 1e-2 (2^-8 of the value).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import we
+
+pytestmark = pytest.mark.gpu
+TOL_F32_OUT = 1e-5
+TOL = {we.F32: TOL_F32_OUT, we.F16: 2e-3, we.BF16: 1e-2}
+
+
+def decode(arr, dt):
+    if dt == we.F32:
+        return arr.view(np.float32).astype(np.float64)
+    if dt == we.F16:
+        return arr.view(np.float16).astype(np.float64)
+    return O.bf16_to_f32(arr.view(np.uint16)).astype(np.float64)
+
+
+def encode_act(x32, dt):
+    """f32 values -> storage for dtype dt, and the exact values the kernel sees (for the oracle)."""
+    if dt == we.F32:
+        return x32.astype(np.float32), x32.astype(np.float32), O.F32
+    if dt == we.F16:
+        h = x32.astype(np.float16)
+        return h, h.view(np.uint16), O.F16
+    b = O.bf16_rne(x32)
+    return b, b, O.BF16
+
+
+def run(graph, p, x, x_dt, w, w_dt, y_dt=we.F32, flags=0, bias=None, y_init=None, rows=None):
+    rows = rows if rows is not None else p.m * (p.k_split if flags & we.EPI_SPLIT_K else 1)
+    ylen = (rows - 1) * p.y_stride + p.n + p.y_offset
+    esz = we.ELEM_BYTES[y_dt]
+    mark = graph.mark()
+    xb, wb = graph.buffer(x), graph.buffer(w)
+    yb = graph.buffer(y_init) if y_init is not None else graph.buffer(ylen * esz)
+    bb = graph.buffer(np.asarray(bias, np.float32)) if bias is not None else None
+    graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=flags)
+    out = graph.read(yb, nbytes=ylen * esz)
+    graph.release(mark)
+    return decode(out, y_dt)
+
+
+REF_SHAPES = [(1, 1, 4), (37, 70, 100), (64, 64, 64), (130, 65, 36), (200, 260, 84)]
+
+
+@pytest.mark.parametrize("m,n,k", REF_SHAPES)
+def test_fp8_matches_reference_test_shapes(graph, m, n, k):  # tests/gpu/matmul.test.ts:49-59
+    x, w = O.matmul_test_data(m, n, k, 1)
+    got = we.matmul_fp8(graph, x, w, 0.002, m, n, k)
+    want = O.matmul(O.matmul_params(m, n, k, 0.002), O.F32, x, O.FP8, w)
+    assert O.rel_error(got.astype(np.float64), want) < TOL_F32_OUT
+
+
+def test_fp8_krea_layer_shape(graph):  # tests/gpu/matmul.test.ts:61-66
+    m, n, k, s = 8, 1536, 6144, 0.0018833705689758062
+    x, w = O.matmul_test_data(m, n, k, 7)
+    got = we.matmul_fp8(graph, x, w, s, m, n, k)
+    want = O.matmul(O.matmul_params(m, n, k, s), O.F32, x, O.FP8, w)
+    assert O.rel_error(got.astype(np.float64), want) < TOL_F32_OUT
+
+
+def test_refuses_bad_params_and_short_buffers(graph):  # tests/gpu/matmul.test.ts:68-72
+    p = we.MatmulParams(1, 1, 6, 1.0, 6, 6, 1, 0, 0, 0, 0, 0, 1)
+    x, w, y = graph.buffer(64), graph.buffer(64), graph.buffer(64)
+    with pytest.raises(we.WeError, match="K must be a multiple of 4, got 6"):
+        graph.matmul(p, we.F32, x, we.FP8, w, we.F32, y)
+    p = we.matmul_params(4, 4, 8, 1.0)
+    with pytest.raises(we.WeError, match="y is too small"):
+        graph.matmul(p, we.F32, graph.buffer(4 * 8 * 4), we.FP8, graph.buffer(32), we.F32, graph.buffer(8))
+    with pytest.raises(we.WeError, match="not a buffer of this context"):
+        graph.matmul(p, we.F32, we.Buffer(16, 128), we.FP8, w, we.F32, y)
+
+
+def test_f32_head_pick_with_strides_and_offsets(graph):  # tests/gpu/matmul.test.ts:93-109
+    tokens, heads, kv, dim = 20, 4, 2, 128
+    u = O.lcg(3, tokens * heads * dim)
+    q = (u * 2 - 1).astype(np.float32)
+    kk = (O.lcg(4, tokens * kv * dim) * 2 - 1).astype(np.float32)
+    h, g = 2, 1
+    got = we.matmul_f32(graph, q, kk, 1.0, tokens, tokens, dim, output_length=tokens * 24, x_stride=heads * dim,
+                        x_offset=h * dim, w_stride=kv * dim, w_offset=g * dim, y_stride=24).reshape(tokens, 24)
+    want = q.reshape(tokens, heads, dim)[:, h].astype(np.float64) @ kk.reshape(tokens, kv, dim)[:, g].astype(
+        np.float64).T
+    assert np.abs(got[:, :tokens] - want).max() < 1e-4
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 70, 100), (8, 1536, 6144)])
+def test_bf16_weights(graph, m, n, k):  # tests/gpu/matmul.test.ts:112-127
+    u = O.lcg(9, m * k + n * k)
+    x = (u[: m * k] * 2 - 1).astype(np.float32)
+    wf = (u[m * k:] * 2 - 1).astype(np.float32)
+    wb = (wf.view(np.uint32) >> 16).astype(np.uint16)
+    got = we.matmul_bf16(graph, x, wb, 0.5, m, n, k)
+    want = O.matmul(O.matmul_params(m, n, k, 0.5), O.F32, x, O.BF16, wb)
+    assert O.rel_error(got.astype(np.float64), want) < TOL_F32_OUT
+
+
+def test_split_k_partials(graph):  # tests/gpu/matmul.test.ts:131-149
+    m, n, k, split, scale = 5, 12, 200, 3, 0.5
+    x, w = O.matmul_test_data(m, n, k, 3)
+    p = we.matmul_params(m, n, k, scale, k_split=split, graph=graph)
+    parts = run(graph, p, x, we.F32, w, we.FP8, flags=we.EPI_SPLIT_K).reshape(split, m * n)
+    op = O.matmul_params(m, n, k, scale, k_split=split)
+    want_parts = O.matmul(op, O.F32, x, O.FP8, w, split=True).reshape(split, m * n)
+    want = O.matmul(O.matmul_params(m, n, k, scale), O.F32, x, O.FP8, w)
+    assert np.abs(parts - want_parts).max() < 1e-5 * np.abs(want).max()
+    assert np.abs(parts.sum(0) - want).max() < 5e-4  # toBeCloseTo(want, 3)
+    assert abs(parts[0, 0] - want[0]) > 1e-3
+
+
+def test_accumulate_adds_exactly(graph):  # tests/gpu/matmul.test.ts:159-175
+    m, n, k, scale = 3, 6, 8, 0.25
+    x = (np.arange(m * k) % 5 - 2).astype(np.float32)
+    w = ((np.arange(n * k) * 3) % 7 - 3).astype(np.float32)
+    start = np.arange(m * n, dtype=np.float32)
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    plain = run(graph, p, x, we.F32, w, we.F32)
+    got = run(graph, p, x, we.F32, w, we.F32, flags=we.EPI_ACCUMULATE, y_init=start)
+    assert np.array_equal(got.astype(np.float32), (plain.astype(np.float32) + start))
+
+
+W_KINDS = [we.FP8, we.BF16, we.F16, we.F32]
+
+
+def make_weights(rng, n, k, w_dt):
+    if w_dt == we.FP8:
+        b = rng.integers(0, 256, n * k).astype(np.uint8)
+        b[(b & 0x7F) == 0x7F] -= 1
+        return b, b, O.FP8
+    vals = rng.normal(0, 0.05, n * k).astype(np.float32)
+    if w_dt == we.BF16:
+        h = O.bf16_rne(vals)
+        return h, h, O.BF16
+    if w_dt == we.F16:
+        h = vals.astype(np.float16).view(np.uint16)
+        return h, h, O.F16
+    return vals, vals, O.F32
+
+
+@pytest.mark.parametrize("x_dt", [we.F32, we.F16, we.BF16])
+@pytest.mark.parametrize("w_dt", W_KINDS)
+@pytest.mark.parametrize("y_dt", [we.F32, we.BF16, we.F16])
+def test_dtype_matrix(graph, x_dt, w_dt, y_dt):
+    m, n, k = 130, 200, 320
+    rng = np.random.default_rng(x_dt * 100 + w_dt * 10 + y_dt)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    scale = 0.02 if w_dt == we.FP8 else 1.0
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    got = run(graph, p, x_store, x_dt, w_store, w_dt, y_dt)
+    want = O.matmul(O.matmul_params(m, n, k, scale), ox, x_oracle, ow, w_oracle)
+    err = O.rel_error(got, want)
+    assert err < TOL[y_dt], err
+
+
+@pytest.mark.parametrize("path", ["fast", "generic"])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("x_dt,w_dt", [(we.BF16, we.FP8), (we.BF16, we.BF16), (we.F16, we.FP8), (we.F16, we.F16)])
+def test_every_tile_config_with_ragged_edges(graph, cfg, x_dt, w_dt, path):
+    """Both kernels (the straight-line fast path and the general one) in every tile shape, with partial
+    tiles in M and N and a partial last K block (K = 208 = 3 * 64 + 16)."""
+    m, n, k = 300, 520, 208
+    rng = np.random.default_rng(cfg)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    p = we.matmul_params(m, n, k, 0.5, graph=graph)
+    os.environ["WE_GEMM_CFG"] = str(cfg)
+    os.environ["WE_GEMM_PATH"] = path
+    try:
+        got = run(graph, p, x_store, x_dt, w_store, w_dt, we.F32)
+    finally:
+        del os.environ["WE_GEMM_CFG"]
+        del os.environ["WE_GEMM_PATH"]
+    want = O.matmul(O.matmul_params(m, n, k, 0.5), ox, x_oracle, ow, w_oracle)
+    assert O.rel_error(got, want) < TOL_F32_OUT
+
+
+def test_unaligned_offsets_and_strides(graph):
+    # multiples of 4 (the reference's only rule) but not of 16 bytes: the element-wise loader path
+    m, n, k = 33, 47, 68
+    rng = np.random.default_rng(5)
+    xs, ws, ys = k + 4, k + 12, n + 3
+    x = rng.standard_normal(4 + m * xs).astype(np.float32)
+    w = rng.integers(0, 256, 4 + n * ws).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] -= 1
+    p = we.matmul_params(m, n, k, 0.1, x_stride=xs, w_stride=ws, y_stride=ys, x_offset=4, w_offset=4, y_offset=2,
+                         graph=graph)
+    got = run(graph, p, x, we.F32, w, we.FP8)
+    op = O.matmul_params(m, n, k, 0.1, x_stride=xs, w_stride=ws, y_stride=ys, x_offset=4, w_offset=4, y_offset=2)
+    want = O.matmul(op, O.F32, x, O.FP8, w, out_len=got.size)
+    assert O.rel_error(got, want) < TOL_F32_OUT
+
+
+def test_bias_and_gelu_epilogue(graph):  # src/model/ops.ts:65 + src/kernels/elementwise.ts:25-29, fused
+    m, n, k = 96, 160, 256
+    rng = np.random.default_rng(7)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), we.BF16)
+    w = rng.integers(0, 256, n * k).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] -= 1
+    bias = rng.normal(0, 1, n).astype(np.float32)
+    p = we.matmul_params(m, n, k, 0.02, graph=graph)
+    got = run(graph, p, x_store, we.BF16, w, we.FP8, we.F32, flags=we.EPI_BIAS | we.EPI_GELU, bias=bias)
+    lin = O.matmul(O.matmul_params(m, n, k, 0.02), ox, x_oracle, O.FP8, w) + np.tile(bias.astype(np.float64), m)
+    want = np.array([O.lib.or_gelu_tanh(v) for v in lin])
+    assert np.abs(got - want).max() < 1e-4 * np.abs(want).max()
+
+
+def test_scale_is_linear_exactly(graph):
+    m, n, k = 64, 128, 192
+    rng = np.random.default_rng(11)
+    x = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
+    w = rng.integers(0, 0x7E, n * k).astype(np.uint8)
+    a = run(graph, we.matmul_params(m, n, k, 0.25, graph=graph), x, we.BF16, w, we.FP8, we.F32)
+    b = run(graph, we.matmul_params(m, n, k, 0.5, graph=graph), x, we.BF16, w, we.FP8, we.F32)
+    assert np.array_equal(2 * a, b)
+
+
+def test_nan_codes_decode_like_the_shader(graph):
+    # the reference shader has no NaN branch: 0x7f / 0xff weigh +-480 (src/kernels/fp8.ts:12-20)
+    m, n, k = 4, 8, 64
+    x = np.ones(m * k, np.float32)
+    w = np.full(n * k, 0x38, np.uint8)  # 1.0
+    w[0] = 0x7F
+    w[k + 5] = 0xFF
+    got = run(graph, we.matmul_params(m, n, k, 1.0, graph=graph), x, we.F32, w, we.FP8).reshape(m, n)
+    assert got[0, 0] == 63 + 480 and got[0, 1] == 63 - 480 and got[0, 2] == 64
+
+
+@pytest.mark.parametrize("name,m,n,k,w_dt", [("C3 up", 4096, 12288, 3072, we.FP8), ("C3 down", 4096, 3072, 12288, we.FP8),
+                                             ("C2 qkv", 4096, 9216, 3072, we.BF16)])
+def test_full_size_sampled_rows(graph, name, m, n, k, w_dt):
+    """Full-size GEMMs: every output is computed, 6 whole rows (incl. the first and last) are checked
+    against the f64 oracle, and the row sums of y equal x @ rowsum(W) (a checksum over all outputs)."""
+    rng = np.random.default_rng(m + n + k)
+    x = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
+    if w_dt == we.FP8:
+        w = rng.integers(0, 256, n * k, dtype=np.uint8)
+        w[(w & 0x7F) == 0x7F] -= 1
+        ow = O.FP8
+    else:
+        w = O.bf16_rne(rng.normal(0, 0.02, n * k).astype(np.float32))
+        ow = O.BF16
+    scale = 0.02 if w_dt == we.FP8 else 1.0
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    got = run(graph, p, x, we.BF16, w, w_dt, we.F32).reshape(m, n)
+    op = O.matmul_params(m, n, k, scale)
+    rows = [0, 1, 777, 2049, m - 2, m - 1]
+    for r in rows:
+        want = O.matmul_rows(op, O.BF16, x, ow, w, r, r + 1).reshape(m, n)[r]
+        assert O.rel_error(got[r], want) < TOL_F32_OUT, (name, r)
+    # checksum of checksums: y @ 1 = x @ (W^T 1) * scale, for every row
+    wdec = (O.e4m3_table()[w] if w_dt == we.FP8 else O.bf16_to_f32(w).astype(np.float64)).reshape(n, k)
+    xs = O.bf16_to_f32(x).astype(np.float64).reshape(m, k)
+    want_sum = xs @ wdec.sum(0) * scale
+    assert np.abs(got.sum(1) - want_sum).max() < 1e-4 * np.abs(want_sum).max() + 1e-3

@@ -1,0 +1,109 @@
+"""RMSNorm, RoPE and the fused per-head norm + RoPE on the GPU against the float64 oracle.
+Mirrors tests/gpu/rmsnorm.test.ts:25-53 and tests/gpu/rope.test.ts:5-42 (tolerances 1e-5 / 1e-6 abs
+for f32; bf16 storage adds one bf16 rounding, 2^-8 of the value)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import we
+
+pytestmark = pytest.mark.gpu
+
+
+def lcg_centered(seed, n, size):
+    """rng(seed) of tests/gpu/rmsnorm.test.ts:5-8: (lcg - 0.5) * size, as f32."""
+    return ((O.lcg(seed, n) - 0.5) * size).astype(np.float32)
+
+
+def test_rmsnorm_krea_rows_with_modulation(graph):  # tests/gpu/rmsnorm.test.ts:25-31
+    d = 6144
+    u = O.lcg(1, 3 * d + 3 * d)
+    x = ((u[: 3 * d] - 0.5) * 8).astype(np.float32)
+    w = ((u[3 * d: 4 * d] - 0.5) * 0.2).astype(np.float32)
+    sc = ((u[4 * d: 5 * d] - 0.5) * 2).astype(np.float32)
+    sh = ((u[5 * d:] - 0.5) * 2).astype(np.float32)
+    out = we.norm(graph, graph.buffer(x), graph.buffer(w), 3, d, we.Mod(graph.buffer(sc), graph.buffer(sh)))
+    got = graph.read(out, dtype=np.float32, count=3 * d)
+    assert np.abs(got - O.rmsnorm(x, w, 1e-5, 1.0, sc, sh)).max() < 1e-5
+
+
+def test_rmsnorm_per_head_plain(graph):  # tests/gpu/rmsnorm.test.ts:33-40
+    d = 128
+    u = O.lcg(2, 101 * d)
+    x = ((u[: 100 * d] - 0.5) * 2).astype(np.float32)
+    w = ((u[100 * d:] - 0.5) * 2).astype(np.float32)
+    out = we.norm(graph, graph.buffer(x), graph.buffer(w), 100, d, we.no_mod(graph, d), offset=0.0)
+    got = graph.read(out, dtype=np.float32, count=100 * d)
+    assert np.abs(got - O.rmsnorm(x, w, 1e-5, 0.0)).max() < 1e-5
+
+
+def test_rmsnorm_short_odd_rows(graph):  # tests/gpu/rmsnorm.test.ts:42-48
+    u = O.lcg(3, 6 * 37)
+    x = ((u[: 5 * 37] - 0.5) * 2).astype(np.float32)
+    w = ((u[5 * 37:] - 0.5) * 2).astype(np.float32)
+    out = we.norm(graph, graph.buffer(x), graph.buffer(w), 5, 37, None)
+    got = graph.read(out, dtype=np.float32, count=5 * 37)
+    assert np.abs(got - O.rmsnorm(x, w, 1e-5, 1.0)).max() < 1e-5
+
+
+@pytest.mark.parametrize("rows,d", [(4608, 3072), (110592 // 8, 128), (7, 2000)])
+def test_rmsnorm_bf16_storage(graph, rows, d):
+    rng = np.random.default_rng(d)
+    x = O.bf16_rne(rng.standard_normal(rows * d).astype(np.float32) * 3)
+    w = rng.uniform(-0.2, 0.2, d).astype(np.float32)
+    out = we.norm(graph, graph.buffer(x), graph.buffer(w), rows, d, None, eps=1e-6, dtype=we.BF16)
+    got = O.bf16_to_f32(graph.read(out, dtype=np.uint16, count=rows * d)).astype(np.float64)
+    want = O.rmsnorm(O.bf16_to_f32(x), w, 1e-6, 1.0)
+    assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 1e-6)
+
+
+def test_rope_interleaved_three_axes(graph):  # tests/gpu/rope.test.ts:5-22
+    heads = 3
+    pos = O.rope_positions(2, 3, 4, 3)
+    cos, sin, pairs = O.rope_tables(pos, [32, 48, 48], 1000.0)
+    tokens = pos.shape[0]
+    x = (O.lcg(1, tokens * heads * 128) * 2 - 1).astype(np.float32)
+    r = we.Rope(graph.buffer(cos), graph.buffer(sin), pairs, tokens)
+    got = graph.read(we.rotate(graph, graph.buffer(x), heads, r), dtype=np.float32, count=x.size)
+    want = O.rope_rotate(x, tokens, heads, pairs, cos, sin)
+    assert np.abs(got - want).max() < 1e-6
+    assert np.array_equal(got[: 2 * heads * 128], x[: 2 * heads * 128])  # text tokens unchanged
+
+
+def test_rope_half_pairs(graph):  # tests/gpu/rope.test.ts:24-42
+    heads = 2
+    pos = np.array([[0.0], [1.0], [5.0], [40.0]])
+    cos, sin, pairs = O.rope_tables(pos, [128], 5e6)
+    x = (O.lcg(7, 4 * heads * 128) * 2 - 1).astype(np.float32)
+    r = we.Rope(graph.buffer(cos), graph.buffer(sin), pairs, 4)
+    got = graph.read(we.rotate(graph, graph.buffer(x), heads, r, "half"), dtype=np.float32, count=x.size)
+    want = O.rope_rotate(x, 4, heads, pairs, cos, sin, half=True)
+    assert np.abs(got - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("dtype", [we.F32, we.BF16])
+def test_fused_qk_norm_rope(graph, half, dtype):
+    """RMSNorm per head (offset 1, eps 1e-6) then 2D-axial RoPE (theta 10000) on the image tokens only,
+    as the q/k path of attend() (src/model/block.ts:53-56) composes it."""
+    text, rows, cols, heads, hd = 8, 6, 10, 4, 128
+    tokens = text + rows * cols
+    pos = O.rope_positions(0, rows, cols, 2)
+    cos, sin, pairs = O.rope_tables(pos, [64, 64], 10000.0)
+    rng = np.random.default_rng(3)
+    x32 = rng.standard_normal(tokens * heads * hd).astype(np.float32) * 2
+    w = rng.uniform(-0.3, 0.3, hd).astype(np.float32)
+    x = x32 if dtype == we.F32 else O.bf16_rne(x32)
+    xs = x32 if dtype == we.F32 else O.bf16_to_f32(x)
+    out = graph.buffer(x.nbytes)
+    graph.qk_norm_rope(tokens, heads, hd, 1e-6, 1.0, graph.buffer(w), text, half, graph.buffer(cos),
+                       graph.buffer(sin), dtype, graph.buffer(x), out)
+    raw = graph.read(out)
+    got = raw.view(np.float32).astype(np.float64) if dtype == we.F32 else O.bf16_to_f32(raw.view(np.uint16)).astype(
+        np.float64)
+    normed = O.rmsnorm(xs, w, 1e-6, 1.0).astype(np.float32)  # [tokens * heads, hd]
+    img = normed.reshape(tokens, heads * hd)[text:].ravel()
+    rot = O.rope_rotate(img, rows * cols, heads, pairs, cos, sin, half=half)
+    want = np.concatenate([normed.reshape(tokens, heads * hd)[:text].ravel().astype(np.float64), rot])
+    tol = 2e-5 if dtype == we.F32 else 2 ** -8
+    assert np.all(np.abs(got - want) <= tol * np.maximum(np.abs(want), 1.0))

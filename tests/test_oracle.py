@@ -88,6 +88,7 @@ def test_float_conversions_match_torch():
     g = load("convert.json")
     f = np.array(g["f32_bits"], np.uint32).view(np.float32)
     assert O.to_bf16(f).tolist() == g["bf16"]
+    assert O.bf16_rne(f).tolist() == g["bf16"]
     assert O.to_f16(f).tolist() == g["f16"]
     # numpy's own float16 rounding agrees as a second library
     with np.errstate(over="ignore"):
@@ -102,6 +103,8 @@ def test_lcg_sequence():  # tests/gpu/matmul.test.ts:10-12
         s = (s * 1664525 + 1013904223) % 2 ** 32
         want.append(s / 2 ** 32)
     assert O.lcg(1, 5).tolist() == want
+    st = __import__("ctypes").c_uint32(1)
+    assert [O.lib.or_lcg_uniform(__import__("ctypes").byref(st)) for _ in range(5)] == want
 
 
 def test_matmul_test_data_layout():  # tests/gpu/matmul.test.ts:14-23: x first, then w; no NaN codes

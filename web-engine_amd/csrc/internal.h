@@ -1,0 +1,65 @@
+// Internal interface between the C-ABI runtime (runtime.cpp) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define WE_EPI_ACCUMULATE_BIT 1u
+#define WE_EPI_SPLIT_K_BIT 2u
+#define WE_EPI_BIAS_BIT 4u
+#define WE_EPI_GELU_BIT 8u
+
+namespace we {
+
+enum GemmCfgId { GEMM_CFG_256x256 = 0, GEMM_CFG_256x128 = 1, GEMM_CFG_128x128 = 2, GEMM_CFG_64x64 = 3, GEMM_CFG_32x64 = 4 };
+
+struct GemmLaunch {
+  const void* x;
+  const void* w;
+  void* y;
+  const float* bias;
+  int x_dtype, w_dtype, y_dtype;
+  uint32_t m, n, k;
+  float scale;
+  uint32_t x_stride, w_stride, y_stride, x_offset, w_offset, y_offset;
+  uint32_t splits, kc;
+  uint32_t flags;
+  int cfg;      // -1: pick by shape
+  int generic;  // 1: skip the fast path (tests of the general kernel)
+};
+hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream);
+// The straight-line fast path; hipErrorNotSupported when the operands do not qualify.
+hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream);
+int pick_gemm_cfg(uint32_t m, uint32_t n, uint32_t splits);
+
+struct Int4Launch {
+  const void* x;
+  const uint32_t* w;
+  const uint16_t* scales;
+  void* y;
+  const float* bias;
+  int x_dtype, y_dtype;
+  uint32_t m, n, k, group;
+  float scale;
+  uint32_t x_stride, y_stride, x_offset, y_offset;
+  uint32_t flags;
+};
+hipError_t int4_launch(const Int4Launch& L, hipStream_t stream);
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
+hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
+                               float* out, hipStream_t s);
+hipError_t launch_elementwise(int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,
+                              void* out, hipStream_t s);
+hipError_t launch_layer_sum(uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w, float* out,
+                            hipStream_t s);
+hipError_t launch_rmsnorm(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                          const float* weight, const float* scale, const float* shift, void* out, hipStream_t s);
+hipError_t launch_rope(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
+                       const float* c, const float* sn, void* out, hipStream_t s);
+hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
+                               const float* weight, uint32_t rope_from, int half, const float* c, const float* sn,
+                               int dtype, const void* x, void* out, hipStream_t s);
+
+}  // namespace we

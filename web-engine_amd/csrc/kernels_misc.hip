@@ -1,0 +1,310 @@
+// Memory-bound kernels around the matmul: buffer zeroing, the dequantization test kernels, the
+// elementwise ops, the split-K layer sum, RMSNorm, RoPE and the fused per-head RMSNorm + RoPE of q/k.
+// All math is f32; activations may be stored as f32, f16 or bf16.
+#include "common.h"
+#include "internal.h"
+
+namespace we {
+
+static inline unsigned grid_for(size_t n, unsigned threads, unsigned cap = 1u << 20) {
+  size_t g = (n + threads - 1) / threads;
+  if (g > cap) g = cap;
+  return (unsigned)(g ? g : 1);
+}
+
+// ------------------------------------------------------------------ zero fill (Graph's zero shader, src/gpu/graph.ts:14-21)
+__global__ void zero_kernel(u32x4* p16, size_t n16, uint8_t* tail, size_t ntail) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) p16[i] = u32x4{0, 0, 0, 0};
+  if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  const size_t n16 = bytes / 16, tail = bytes % 16;
+  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n16 ? n16 : 1, 256, 4096)), dim3(256), 0, s, (u32x4*)p, n16,
+                     (uint8_t*)p + n16 * 16, tail);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ unpackFp8 (src/kernels/fp8.ts:24-36)
+__global__ void unpack_fp8_kernel(const uint8_t* packed, size_t n, const float* scale, float* out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const float sc = scale[0];
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = e4m3_shader(packed[i]) * sc;
+}
+
+hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(unpack_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, (const uint8_t*)packed, n, scale, out);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ int4 dequant (q * s in f32, exact)
+__global__ void dequant_int4_kernel(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
+                                    float* out) {
+  const size_t total = (size_t)rows * k;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const uint32_t gpr = k / group;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint32_t r = (uint32_t)(i / k), kk = (uint32_t)(i % k);
+    const int q = ((int)(w[i / 8] << (28 - 4 * (i % 8)))) >> 28;
+    out[i] = (float)q * f16_to_f32(sc[(size_t)r * gpr + kk / group]);
+  }
+}
+
+hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
+                               float* out, hipStream_t s) {
+  const size_t n = (size_t)rows * k;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(dequant_int4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, w, sc, rows, k, group, out);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ elementwise (src/kernels/elementwise.ts:38-84)
+// a, b, out: activations of dtype DT; per-column vectors (add_bias: b, gated_add: c) are f32.
+template <int DT>
+__global__ void elementwise_kernel(int op, size_t n, size_t d, const void* a, const void* b, const void* c, void* out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float x = load_as_f32<DT>(a, i);
+    float r;
+    switch (op) {
+      case 0: r = x * sigmoid(x) * load_as_f32<DT>(b, i); break;         // swiglu
+      case 1: r = x * sigmoid(load_as_f32<DT>(b, i)); break;             // sigmoidGate
+      case 2: r = x + ((const float*)c)[i % d] * load_as_f32<DT>(b, i); break;  // gatedAdd
+      case 3: r = x + ((const float*)b)[i % d]; break;                   // addBias
+      case 4: r = gelu_tanh(x); break;                                   // geluTanh
+      case 5: r = x + load_as_f32<DT>(b, i); break;                      // add
+      default: r = x * sigmoid(x); break;                                // silu
+    }
+    store_from_f32<DT>(out, i, r);
+  }
+}
+
+hipError_t launch_elementwise(int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,
+                              void* out, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const dim3 g(grid_for(n, 256)), t(256);
+  switch (dtype) {
+    case F16: hipLaunchKernelGGL(elementwise_kernel<F16>, g, t, 0, s, op, n, d, a, b, c, out); break;
+    case BF16: hipLaunchKernelGGL(elementwise_kernel<BF16>, g, t, 0, s, op, n, d, a, b, c, out); break;
+    default: hipLaunchKernelGGL(elementwise_kernel<F32>, g, t, 0, s, op, n, d, a, b, c, out); break;
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ layerSum (src/kernels/text.ts:67-84)
+__global__ void layer_sum_kernel(uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w,
+                                 float* out) {
+  const size_t n = (size_t)tokens * dim;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const size_t t = i / dim, d = i % dim;
+    float sum = 0.0f;
+    for (uint32_t l = 0; l < layers; l++) sum += w[l] * x[(t * layers + l) * dim + d];
+    out[i] = sum;
+  }
+}
+
+hipError_t launch_layer_sum(uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w, float* out,
+                            hipStream_t s) {
+  const size_t n = (size_t)tokens * dim;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(layer_sum_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, tokens, layers, dim, x, w, out);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ RMSNorm (src/kernels/rmsnorm.ts:13-48)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// one wave per row (d <= 1024), several rows per block
+template <int DT>
+__global__ void __launch_bounds__(256) rmsnorm_wave_kernel(uint32_t rows, uint32_t d, float eps, float offset,
+                                                          const void* x, const float* weight, const float* scale,
+                                                          const float* shift, void* out) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const size_t base = (size_t)row * d;
+  float v[16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const uint32_t i = lane + 64 * j;
+    v[j] = i < d ? load_as_f32<DT>(x, base + i) : 0.0f;
+    ss += v[j] * v[j];
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const uint32_t i = lane + 64 * j;
+    if (i < d) {
+      const float sc = scale ? scale[i] : 0.0f, sh = shift ? shift[i] : 0.0f;
+      store_from_f32<DT>(out, base + i, v[j] * inv * (offset + weight[i]) * (1.0f + sc) + sh);
+    }
+  }
+}
+
+// one 256-thread block per row (any d)
+template <int DT>
+__global__ void __launch_bounds__(256) rmsnorm_block_kernel(uint32_t rows, uint32_t d, float eps, float offset,
+                                                           const void* x, const float* weight, const float* scale,
+                                                           const float* shift, void* out) {
+  __shared__ float part[4];
+  const uint32_t row = blockIdx.x;
+  const size_t base = (size_t)row * d;
+  float ss = 0.0f;
+  for (uint32_t i = threadIdx.x; i < d; i += 256) {
+    const float v = load_as_f32<DT>(x, base + i);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+  for (uint32_t i = threadIdx.x; i < d; i += 256) {
+    const float sc = scale ? scale[i] : 0.0f, sh = shift ? shift[i] : 0.0f;
+    store_from_f32<DT>(out, base + i, load_as_f32<DT>(x, base + i) * inv * (offset + weight[i]) * (1.0f + sc) + sh);
+  }
+}
+
+template <int DT>
+static void rmsnorm_dt(uint32_t rows, uint32_t d, float eps, float offset, const void* x, const float* w,
+                       const float* sc, const float* sh, void* out, hipStream_t s) {
+  if (d <= 1024)
+    hipLaunchKernelGGL(rmsnorm_wave_kernel<DT>, dim3((rows + 3) / 4), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh,
+                       out);
+  else
+    hipLaunchKernelGGL(rmsnorm_block_kernel<DT>, dim3(rows), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh, out);
+}
+
+hipError_t launch_rmsnorm(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                          const float* weight, const float* scale, const float* shift, void* out, hipStream_t s) {
+  if (rows == 0 || d == 0) return hipSuccess;
+  switch (dtype) {
+    case F16: rmsnorm_dt<F16>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
+    case BF16: rmsnorm_dt<BF16>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
+    default: rmsnorm_dt<F32>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ RoPE (src/kernels/rope.ts:45-77)
+template <int DT>
+__global__ void rope_kernel(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, const void* x, const float* cs,
+                            const float* sn, void* out) {
+  const size_t total = (size_t)tokens * heads * pairs;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const size_t j = i % pairs, th = i / pairs, t = th / heads;
+    const float c = cs[t * pairs + j], s = sn[t * pairs + j];
+    size_t ia, ib;
+    if (!half) {
+      ia = 2 * i;
+      ib = 2 * i + 1;
+    } else {
+      ia = th * pairs * 2 + j;
+      ib = ia + pairs;
+    }
+    const float a = load_as_f32<DT>(x, ia), b = load_as_f32<DT>(x, ib);
+    store_from_f32<DT>(out, ia, a * c - b * s);
+    store_from_f32<DT>(out, ib, b * c + a * s);
+  }
+}
+
+hipError_t launch_rope(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
+                       const float* c, const float* sn, void* out, hipStream_t s) {
+  const size_t n = (size_t)tokens * heads * pairs;
+  if (n == 0) return hipSuccess;
+  const dim3 g(grid_for(n, 256)), t(256);
+  switch (dtype) {
+    case F16: hipLaunchKernelGGL(rope_kernel<F16>, g, t, 0, s, tokens, heads, pairs, half, x, c, sn, out); break;
+    case BF16: hipLaunchKernelGGL(rope_kernel<BF16>, g, t, 0, s, tokens, heads, pairs, half, x, c, sn, out); break;
+    default: hipLaunchKernelGGL(rope_kernel<F32>, g, t, 0, s, tokens, heads, pairs, half, x, c, sn, out); break;
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ fused per-head RMSNorm + RoPE
+// One wave per (token, head) row of head_dim = 2 * pairs values (pairs <= 256): lane l owns pairs
+// l, l + 64, ..., so both values of each of its pairs are in its registers (interleaved: 2j, 2j+1;
+// half: j, j + pairs). Tokens below rope_from are only normalized; cos/sin row = token - rope_from.
+template <int DT>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                                                          float eps, float offset, const float* weight,
+                                                          uint32_t rope_from, int half, const float* cs,
+                                                          const float* sn, const void* x, void* out) {
+  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= (size_t)tokens * heads) return;
+  const uint32_t t = (uint32_t)(row / heads);
+  const uint32_t pairs = head_dim / 2;
+  const size_t base = row * head_dim;
+  float va[4], vb[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t j = lane + 64 * q;
+    if (j < pairs) {
+      const uint32_t ia = half ? j : 2 * j, ib = half ? j + pairs : 2 * j + 1;
+      va[q] = load_as_f32<DT>(x, base + ia);
+      vb[q] = load_as_f32<DT>(x, base + ib);
+    } else {
+      va[q] = vb[q] = 0.0f;
+    }
+    ss += va[q] * va[q] + vb[q] * vb[q];
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)head_dim + eps);
+  const bool rot = t >= rope_from;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t j = lane + 64 * q;
+    if (j >= pairs) continue;
+    const uint32_t ia = half ? j : 2 * j, ib = half ? j + pairs : 2 * j + 1;
+    const float a = va[q] * inv * (offset + weight[ia]);
+    const float b = vb[q] * inv * (offset + weight[ib]);
+    float ra = a, rb = b;
+    if (rot) {
+      const size_t ti = (size_t)(t - rope_from) * pairs + j;
+      const float c = cs[ti], s = sn[ti];
+      ra = a * c - b * s;
+      rb = b * c + a * s;
+    }
+    store_from_f32<DT>(out, base + ia, ra);
+    store_from_f32<DT>(out, base + ib, rb);
+  }
+}
+
+hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
+                               const float* weight, uint32_t rope_from, int half, const float* c, const float* sn,
+                               int dtype, const void* x, void* out, hipStream_t s) {
+  const size_t rows = (size_t)tokens * heads;
+  if (rows == 0) return hipSuccess;
+  const dim3 g((unsigned)((rows + 3) / 4)), t(256);
+  switch (dtype) {
+    case F16:
+      hipLaunchKernelGGL(qk_norm_rope_kernel<F16>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
+                         half, c, sn, x, out);
+      break;
+    case BF16:
+      hipLaunchKernelGGL(qk_norm_rope_kernel<BF16>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
+                         half, c, sn, x, out);
+      break;
+    default:
+      hipLaunchKernelGGL(qk_norm_rope_kernel<F32>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
+                         half, c, sn, x, out);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace we

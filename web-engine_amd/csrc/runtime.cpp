@@ -1,0 +1,594 @@
+// C-ABI runtime of the gfx950 matmul path: context (device, compute + copy streams, events), a pooled
+// device-buffer allocator with zero-on-alloc (the semantics of the reference's Graph, src/gpu/graph.ts),
+// pinned host memory and ticketed copies for weight streaming, argument validation, and the op entry
+// points that hand off to the kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/we.h"
+#include "internal.h"
+
+namespace {
+
+constexpr size_t kTicketRing = 1024;
+
+struct Alloc {
+  size_t size;  // bytes allocated (a multiple of 256)
+  size_t req;   // bytes the caller asked for, rounded up to 4 like the reference's Graph.buffer
+};
+
+}  // namespace
+
+struct we_ctx {
+  int device = 0;
+  hipStream_t compute = nullptr, copy = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  std::string err;
+  std::map<uintptr_t, Alloc> allocs;                      // every device allocation, by base address
+  std::unordered_map<size_t, std::vector<void*>> pool;    // freed buffers by rounded size
+  std::vector<void*> owned;                               // live buffers, in creation order (for mark/release)
+  std::map<uintptr_t, size_t> pinned;                     // pinned host allocations
+  uint64_t created = 0, reused = 0, created_bytes = 0;
+  std::vector<hipEvent_t> tickets;
+  uint64_t next_ticket = 1;
+  hipDeviceProp_t prop{};
+};
+
+namespace {
+
+int fail(we_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = buf;
+  return code;
+}
+
+int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, WE_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_OK(ctx, call, what)                     \
+  do {                                              \
+    hipError_t e_ = (call);                         \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
+  } while (0)
+
+size_t round_size(size_t bytes) { return ((bytes < 4 ? 4 : bytes) + 255) / 256 * 256; }
+
+// Is [p, p + bytes) inside one device allocation of this context?
+int check_span(we_ctx* ctx, const void* p, size_t bytes, const char* name) {
+  if (bytes == 0) return WE_OK;
+  if (!p) return fail(ctx, WE_EINVAL, "%s is null", name);
+  const uintptr_t a = (uintptr_t)p;
+  auto it = ctx->allocs.upper_bound(a);
+  if (it == ctx->allocs.begin()) return fail(ctx, WE_EINVAL, "%s is not a buffer of this context", name);
+  --it;
+  const uintptr_t base = it->first, end = base + it->second.req;
+  if (a >= base + it->second.size) return fail(ctx, WE_EINVAL, "%s is not a buffer of this context", name);
+  if (a >= end || bytes > end - a)
+    return fail(ctx, WE_EINVAL, "%s is too small: needs %zu bytes at offset %zu of a %zu-byte buffer", name, bytes,
+                (size_t)(a - base), it->second.req);
+  return WE_OK;
+}
+
+int elem_bytes(int dt) {
+  switch (dt) {
+    case WE_F32: return 4;
+    case WE_F16:
+    case WE_BF16: return 2;
+    case WE_FP8_E4M3: return 1;
+    default: return 0;
+  }
+}
+
+bool is_act(int dt) { return dt == WE_F32 || dt == WE_F16 || dt == WE_BF16; }
+
+hipEvent_t& ticket_event(we_ctx* ctx, uint64_t t) { return ctx->tickets[t % kTicketRing]; }
+
+int new_ticket(we_ctx* ctx, hipStream_t s, uint64_t* out) {
+  const uint64_t t = ctx->next_ticket++;
+  hipEvent_t& ev = ticket_event(ctx, t);
+  HIP_OK(ctx, hipEventRecord(ev, s), "hipEventRecord");
+  *out = t;
+  return WE_OK;
+}
+
+int ticket_valid(we_ctx* ctx, uint64_t t) {
+  if (t == 0 || t >= ctx->next_ticket) return fail(ctx, WE_EINVAL, "unknown ticket %llu", (unsigned long long)t);
+  if (t + kTicketRing < ctx->next_ticket)
+    return fail(ctx, WE_EINVAL, "ticket %llu expired (more than %zu tickets since)", (unsigned long long)t, kTicketRing);
+  return WE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int we_ctx_create(int device, we_ctx** out) {
+  if (!out) return WE_EINVAL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return WE_EHIP;
+  if (device < 0 || device >= count) return WE_EINVAL;
+  we_ctx* ctx = new we_ctx();
+  ctx->device = device;
+  auto cleanup = [&](int code) {
+    we_ctx_destroy(ctx);
+    return code;
+  };
+  if (hipSetDevice(device) != hipSuccess) return cleanup(WE_EHIP);
+  if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return cleanup(WE_EHIP);
+  if (hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
+  if (hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
+  if (hipEventCreate(&ctx->t0) != hipSuccess || hipEventCreate(&ctx->t1) != hipSuccess) return cleanup(WE_EHIP);
+  ctx->tickets.resize(kTicketRing, nullptr);
+  for (auto& e : ctx->tickets)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return cleanup(WE_EHIP);
+  *out = ctx;
+  return WE_OK;
+}
+
+int we_ctx_destroy(we_ctx* ctx) {
+  if (!ctx) return WE_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
+  if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+  for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
+  for (auto& kv : ctx->pinned) (void)hipHostFree((void*)kv.first);
+  for (auto& e : ctx->tickets)
+    if (e) (void)hipEventDestroy(e);
+  if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+  if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+  if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
+  if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+  delete ctx;
+  return WE_OK;
+}
+
+const char* we_last_error(const we_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units, int* lds_bytes) {
+  if (!ctx) return WE_EINVAL;
+  if (name && name_len) snprintf(name, name_len, "%s", ctx->prop.gcnArchName);
+  if (compute_units) *compute_units = ctx->prop.multiProcessorCount;
+  if (lds_bytes) *lds_bytes = (int)ctx->prop.sharedMemPerBlock;
+  return WE_OK;
+}
+
+// ------------------------------------------------------------------------------------------ buffers
+
+int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return WE_EINVAL;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  const size_t size = round_size(bytes);
+  void* p = nullptr;
+  const size_t req = (bytes < 4 ? 4 : (bytes + 3) / 4 * 4);
+  auto& list = ctx->pool[size];
+  if (!list.empty()) {
+    p = list.back();
+    list.pop_back();
+    ctx->allocs[(uintptr_t)p].req = req;
+    ctx->reused++;
+  } else {
+    hipError_t e = hipMalloc(&p, size);
+    if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "hipMalloc(%zu): %s", size, hipGetErrorString(e));
+    ctx->allocs[(uintptr_t)p] = Alloc{size, req};
+    ctx->created++;
+    ctx->created_bytes += size;
+  }
+  // zeroed like a new WebGPU buffer; a fill kernel rather than a memset node (graph-capture safe)
+  hipError_t e = we::launch_zero(p, size, ctx->compute);
+  if (e != hipSuccess) return hip_fail(ctx, e, "zero fill");
+  ctx->owned.push_back(p);
+  *out = p;
+  return WE_OK;
+}
+
+int we_buf_free(we_ctx* ctx, void* buf) {
+  if (!ctx) return WE_EINVAL;
+  auto it = ctx->allocs.find((uintptr_t)buf);
+  if (it == ctx->allocs.end()) return fail(ctx, WE_EINVAL, "we_buf_free: not a buffer of this context");
+  for (size_t i = 0; i < ctx->owned.size(); i++)
+    if (ctx->owned[i] == buf) {
+      ctx->owned.erase(ctx->owned.begin() + (long)i);
+      ctx->pool[it->second.size].push_back(buf);
+      return WE_OK;
+    }
+  return fail(ctx, WE_EINVAL, "we_buf_free: buffer already freed");
+}
+
+int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t bytes) {
+  if (!ctx) return WE_EINVAL;
+  if (bytes == 0) return WE_OK;
+  if (!src) return fail(ctx, WE_EINVAL, "upload source is null");
+  int rc = check_span(ctx, (char*)buf + offset, bytes, "upload destination");
+  if (rc) return rc;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipMemcpyAsync((char*)buf + offset, src, bytes, hipMemcpyHostToDevice, ctx->compute), "upload");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "upload sync");  // the host copy may be reused on return
+  return WE_OK;
+}
+
+int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size_t bytes) {
+  if (!ctx) return WE_EINVAL;
+  if (bytes == 0) return WE_OK;
+  if (!dst) return fail(ctx, WE_EINVAL, "download destination is null");
+  int rc = check_span(ctx, (const char*)buf + offset, bytes, "download source");
+  if (rc) return rc;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipMemcpyAsync(dst, (const char*)buf + offset, bytes, hipMemcpyDeviceToHost, ctx->compute), "download");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "download sync");
+  return WE_OK;
+}
+
+int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes) {
+  if (!ctx) return WE_EINVAL;
+  if (bytes == 0) return WE_OK;
+  int rc = check_span(ctx, (const char*)src + src_offset, bytes, "copy source");
+  if (!rc) rc = check_span(ctx, (char*)dst + dst_offset, bytes, "copy destination");
+  if (rc) return rc;
+  HIP_OK(ctx, hipMemcpyAsync((char*)dst + dst_offset, (const char*)src + src_offset, bytes, hipMemcpyDeviceToDevice,
+                             ctx->compute),
+         "copy");
+  return WE_OK;
+}
+
+int we_mark(we_ctx* ctx, size_t* mark) {
+  if (!ctx || !mark) return WE_EINVAL;
+  *mark = ctx->owned.size();
+  return WE_OK;
+}
+
+int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep) {
+  if (!ctx) return WE_EINVAL;
+  if (mark > ctx->owned.size()) return fail(ctx, WE_EINVAL, "mark %zu is past the %zu live buffers", mark, ctx->owned.size());
+  std::vector<void*> later(ctx->owned.begin() + (long)mark, ctx->owned.end());
+  ctx->owned.resize(mark);
+  for (void* b : later) {
+    bool kept = false;
+    for (size_t i = 0; i < n_keep && !kept; i++) kept = keep[i] == b;
+    if (kept) ctx->owned.push_back(b);
+    else ctx->pool[ctx->allocs[(uintptr_t)b].size].push_back(b);
+  }
+  return WE_OK;
+}
+
+int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes) {
+  if (!ctx) return WE_EINVAL;
+  if (created) *created = ctx->created;
+  if (reused) *reused = ctx->reused;
+  if (created_bytes) *created_bytes = ctx->created_bytes;
+  return WE_OK;
+}
+
+int we_sync(we_ctx* ctx) {
+  if (!ctx) return WE_EINVAL;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "compute stream");
+  return WE_OK;
+}
+
+// ------------------------------------------------------------------------------------------ pinned host / streaming
+
+int we_host_alloc(we_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return WE_EINVAL;
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  ctx->pinned[(uintptr_t)p] = bytes;
+  *out = p;
+  return WE_OK;
+}
+
+int we_host_free(we_ctx* ctx, void* ptr) {
+  if (!ctx) return WE_EINVAL;
+  auto it = ctx->pinned.find((uintptr_t)ptr);
+  if (it == ctx->pinned.end()) return fail(ctx, WE_EINVAL, "we_host_free: not pinned memory of this context");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
+  HIP_OK(ctx, hipHostFree(ptr), "hipHostFree");
+  ctx->pinned.erase(it);
+  return WE_OK;
+}
+
+int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket) {
+  if (!ctx || !ticket) return WE_EINVAL;
+  int rc = check_span(ctx, dst, bytes, "stream destination");
+  if (rc) return rc;
+  auto it = ctx->pinned.upper_bound((uintptr_t)pinned_src);
+  if (it == ctx->pinned.begin()) return fail(ctx, WE_EINVAL, "stream source is not pinned memory of this context");
+  --it;
+  if ((uintptr_t)pinned_src + bytes > it->first + it->second)
+    return fail(ctx, WE_EINVAL, "stream source is not pinned memory of this context");
+  if (after) {
+    rc = ticket_valid(ctx, after);
+    if (rc) return rc;
+    HIP_OK(ctx, hipStreamWaitEvent(ctx->copy, ticket_event(ctx, after), 0), "hipStreamWaitEvent");
+  }
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipMemcpyAsync(dst, pinned_src, bytes, hipMemcpyHostToDevice, ctx->copy), "stream copy");
+  return new_ticket(ctx, ctx->copy, ticket);
+}
+
+int we_wait_ticket(we_ctx* ctx, uint64_t ticket) {
+  if (!ctx) return WE_EINVAL;
+  int rc = ticket_valid(ctx, ticket);
+  if (rc) return rc;
+  HIP_OK(ctx, hipStreamWaitEvent(ctx->compute, ticket_event(ctx, ticket), 0), "hipStreamWaitEvent");
+  return WE_OK;
+}
+
+int we_record_compute(we_ctx* ctx, uint64_t* ticket) {
+  if (!ctx || !ticket) return WE_EINVAL;
+  return new_ticket(ctx, ctx->compute, ticket);
+}
+
+int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
+  if (!ctx || !done) return WE_EINVAL;
+  int rc = ticket_valid(ctx, ticket);
+  if (rc) return rc;
+  hipError_t e = hipEventQuery(ticket_event(ctx, ticket));
+  if (e == hipSuccess) *done = 1;
+  else if (e == hipErrorNotReady) *done = 0;
+  else return hip_fail(ctx, e, "hipEventQuery");
+  return WE_OK;
+}
+
+int we_timer_start(we_ctx* ctx) {
+  if (!ctx) return WE_EINVAL;
+  HIP_OK(ctx, hipEventRecord(ctx->t0, ctx->compute), "hipEventRecord");
+  return WE_OK;
+}
+
+int we_timer_stop(we_ctx* ctx, float* ms) {
+  if (!ctx || !ms) return WE_EINVAL;
+  HIP_OK(ctx, hipEventRecord(ctx->t1, ctx->compute), "hipEventRecord");
+  HIP_OK(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");
+  HIP_OK(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1), "hipEventElapsedTime");
+  return WE_OK;
+}
+
+// ------------------------------------------------------------------------------------------ matmul
+
+int we_matmul_params_make(we_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, float scale, int64_t x_stride,
+                          int64_t w_stride, int64_t y_stride, int64_t x_offset, int64_t w_offset, int64_t y_offset,
+                          int64_t k_split, we_matmul_params* out) {
+  if (!out) return fail(ctx, WE_EINVAL, "params output is null");
+  const int64_t xs = x_stride < 0 ? k : x_stride, ws = w_stride < 0 ? k : w_stride, ys = y_stride < 0 ? n : y_stride;
+  const int64_t xo = x_offset < 0 ? 0 : x_offset, wo = w_offset < 0 ? 0 : w_offset, yo = y_offset < 0 ? 0 : y_offset;
+  const char* names[5] = {"K", "xStride", "wStride", "xOffset", "wOffset"};
+  const int64_t vals[5] = {(int64_t)k, xs, ws, xo, wo};
+  for (int i = 0; i < 5; i++)
+    if (vals[i] % 4) return fail(ctx, WE_EINVAL, "%s must be a multiple of 4, got %lld", names[i], (long long)vals[i]);
+  *out = we_matmul_params{m, n, k, scale, (uint32_t)xs, (uint32_t)ws, (uint32_t)ys, (uint32_t)xo, (uint32_t)wo,
+                          (uint32_t)yo, 0, 0, (uint32_t)(k_split < 1 ? 1 : k_split)};
+  return WE_OK;
+}
+
+uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
+  const uint32_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  const uint32_t want = (256 + tiles - 1) / tiles, cap = k / 256;
+  const uint32_t s = want < cap ? want : cap;
+  return s < 1 ? 1 : s;
+}
+
+int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+              const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags) {
+  if (!ctx) return WE_EINVAL;
+  if (!p) return fail(ctx, WE_EINVAL, "params is null");
+  if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
+  {
+    const char* names[5] = {"K", "xStride", "wStride", "xOffset", "wOffset"};
+    const uint32_t vals[5] = {p->k, p->x_stride, p->w_stride, p->x_offset, p->w_offset};
+    for (int i = 0; i < 5; i++)
+      if (vals[i] % 4) return fail(ctx, WE_EINVAL, "%s must be a multiple of 4, got %u", names[i], vals[i]);
+  }
+  if (!is_act(x_dtype)) return fail(ctx, WE_EINVAL, "x dtype %d is not f32 / f16 / bf16", x_dtype);
+  if (!is_act(y_dtype)) return fail(ctx, WE_EINVAL, "y dtype %d is not f32 / f16 / bf16", y_dtype);
+  if (!(is_act(w_dtype) || w_dtype == WE_FP8_E4M3 || w_dtype == WE_INT4))
+    return fail(ctx, WE_EINVAL, "weight dtype %d is not fp8 / bf16 / f16 / f32 / int4", w_dtype);
+  if (flags & ~(WE_EPI_ACCUMULATE | WE_EPI_SPLIT_K | WE_EPI_BIAS | WE_EPI_GELU_TANH))
+    return fail(ctx, WE_EINVAL, "unknown epilogue flags 0x%x", flags);
+  const bool split = (flags & WE_EPI_SPLIT_K) != 0;
+  const uint32_t splits = split ? (p->k_split < 1 ? 1 : p->k_split) : 1;
+  if (p->m == 0 || p->n == 0) return WE_OK;
+  const uint32_t kc = split ? ((p->k + splits - 1) / splits + 15) / 16 * 16 : p->k;
+
+  // extents of every operand (in bytes), so that no launch can read or write outside its buffers
+  const uint64_t xb = elem_bytes(x_dtype), yb = elem_bytes(y_dtype);
+  const uint64_t x_need = p->k ? ((uint64_t)p->x_offset + (uint64_t)(p->m - 1) * p->x_stride + p->k) * xb : 0;
+  const uint64_t y_rows = (uint64_t)p->m * splits;
+  const uint64_t y_need = ((uint64_t)p->y_offset + (y_rows - 1) * p->y_stride + p->n) * yb;
+  int rc = check_span(ctx, x, x_need, "x");
+  if (!rc) rc = check_span(ctx, y, y_need, "y");
+  if (!rc && (flags & WE_EPI_BIAS)) rc = check_span(ctx, bias, (uint64_t)p->n * 4, "bias");
+  if (rc) return rc;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+
+  if (w_dtype == WE_INT4) {
+    if (split) return fail(ctx, WE_EUNSUPPORTED, "int4 weights have no split-K mode (the kernel splits K itself)");
+    if (group == 0 || group % 64 || p->k % group)
+      return fail(ctx, WE_EUNSUPPORTED, "int4 needs a group size that is a multiple of 64 and divides K (group %u, K %u)",
+                  group, p->k);
+    if (p->w_stride != p->k || p->w_offset != 0)
+      return fail(ctx, WE_EUNSUPPORTED, "int4 weights must be contiguous [N, K/8] words (wStride = K, wOffset = 0)");
+    const uint32_t align = x_dtype == WE_F32 ? 4 : 8;
+    if (p->x_stride % align || p->x_offset % align || ((uintptr_t)x % 16))
+      return fail(ctx, WE_EUNSUPPORTED, "int4 path needs 16-byte aligned x rows (xStride and xOffset multiples of %u)",
+                  align);
+    rc = check_span(ctx, w, (uint64_t)p->n * p->k / 2, "w");
+    if (!rc) rc = check_span(ctx, w_scales, (uint64_t)p->n * (p->k / group) * 2, "w_scales");
+    if (rc) return rc;
+    we::Int4Launch L{};
+    L.x = x;
+    L.w = (const uint32_t*)w;
+    L.scales = (const uint16_t*)w_scales;
+    L.y = y;
+    L.bias = bias;
+    L.x_dtype = x_dtype;
+    L.y_dtype = y_dtype;
+    L.m = p->m;
+    L.n = p->n;
+    L.k = p->k;
+    L.group = group;
+    L.scale = p->scale;
+    L.x_stride = p->x_stride;
+    L.y_stride = p->y_stride;
+    L.x_offset = p->x_offset;
+    L.y_offset = p->y_offset;
+    L.flags = flags;
+    hipError_t e = we::int4_launch(L, ctx->compute);
+    if (e != hipSuccess) return hip_fail(ctx, e, "int4 launch");
+    return WE_OK;
+  }
+
+  const uint64_t wb = elem_bytes(w_dtype);
+  const uint64_t w_need = p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0;
+  rc = check_span(ctx, w, w_need, "w");
+  if (rc) return rc;
+  we::GemmLaunch L{};
+  L.x = x;
+  L.w = w;
+  L.y = y;
+  L.bias = bias;
+  L.x_dtype = x_dtype;
+  L.w_dtype = w_dtype;
+  L.y_dtype = y_dtype;
+  L.m = p->m;
+  L.n = p->n;
+  L.k = p->k;
+  L.scale = p->scale;
+  L.x_stride = p->x_stride;
+  L.w_stride = p->w_stride;
+  L.y_stride = p->y_stride;
+  L.x_offset = p->x_offset;
+  L.w_offset = p->w_offset;
+  L.y_offset = p->y_offset;
+  L.splits = splits;
+  L.kc = kc;
+  L.flags = flags;
+  L.cfg = -1;
+  const char* force = getenv("WE_GEMM_CFG");
+  if (force && *force) L.cfg = atoi(force);
+  const char* path = getenv("WE_GEMM_PATH");
+  L.generic = (path && strcmp(path, "generic") == 0) ? 1 : 0;
+  hipError_t e = we::gemm_launch(L, ctx->compute);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+  return WE_OK;
+}
+
+// ------------------------------------------------------------------------------------------ norms, rope, elementwise
+
+int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+               const float* weight, const float* scale, const float* shift, void* out) {
+  if (!ctx) return WE_EINVAL;
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "rmsnorm dtype %d is not f32 / f16 / bf16", dtype);
+  const uint64_t n = (uint64_t)rows * d * elem_bytes(dtype);
+  int rc = check_span(ctx, x, n, "x");
+  if (!rc) rc = check_span(ctx, out, n, "out");
+  if (!rc) rc = check_span(ctx, weight, (uint64_t)d * 4, "weight");
+  if (!rc && scale) rc = check_span(ctx, scale, (uint64_t)d * 4, "scale");
+  if (!rc && shift) rc = check_span(ctx, shift, (uint64_t)d * 4, "shift");
+  if (rc) return rc;
+  hipError_t e = we::launch_rmsnorm(rows, d, eps, offset, dtype, x, weight, scale, shift, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "rmsnorm launch");
+}
+
+int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
+            const float* cos_t, const float* sin_t, void* out) {
+  if (!ctx) return WE_EINVAL;
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "rope dtype %d is not f32 / f16 / bf16", dtype);
+  const uint64_t n = (uint64_t)tokens * heads * pairs * 2 * elem_bytes(dtype);
+  int rc = check_span(ctx, x, n, "x");
+  if (!rc) rc = check_span(ctx, out, n, "out");
+  if (!rc) rc = check_span(ctx, cos_t, (uint64_t)tokens * pairs * 4, "cos");
+  if (!rc) rc = check_span(ctx, sin_t, (uint64_t)tokens * pairs * 4, "sin");
+  if (rc) return rc;
+  hipError_t e = we::launch_rope(tokens, heads, pairs, half ? 1 : 0, dtype, x, cos_t, sin_t, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "rope launch");
+}
+
+int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
+                    const float* weight, uint32_t rope_from, int half, const float* cos_t, const float* sin_t,
+                    int dtype, const void* x, void* out) {
+  if (!ctx) return WE_EINVAL;
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "dtype %d is not f32 / f16 / bf16", dtype);
+  if (head_dim % 2 || head_dim == 0 || head_dim > 512)
+    return fail(ctx, WE_EINVAL, "head_dim must be even and at most 512, got %u", head_dim);
+  const uint64_t n = (uint64_t)tokens * heads * head_dim * elem_bytes(dtype);
+  const uint64_t rot_tokens = tokens > rope_from ? tokens - rope_from : 0;
+  int rc = check_span(ctx, x, n, "x");
+  if (!rc) rc = check_span(ctx, out, n, "out");
+  if (!rc) rc = check_span(ctx, weight, (uint64_t)head_dim * 4, "weight");
+  if (!rc) rc = check_span(ctx, cos_t, rot_tokens * (head_dim / 2) * 4, "cos");
+  if (!rc) rc = check_span(ctx, sin_t, rot_tokens * (head_dim / 2) * 4, "sin");
+  if (rc) return rc;
+  hipError_t e = we::launch_qk_norm_rope(tokens, heads, head_dim, eps, offset, weight, rope_from, half ? 1 : 0, cos_t,
+                                         sin_t, dtype, x, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "qk norm rope launch");
+}
+
+int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,
+                   void* out) {
+  if (!ctx) return WE_EINVAL;
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "elementwise dtype %d is not f32 / f16 / bf16", dtype);
+  if (op < WE_OP_SWIGLU || op > WE_OP_SILU) return fail(ctx, WE_EINVAL, "unknown elementwise op %d", op);
+  const uint64_t bytes = (uint64_t)n * elem_bytes(dtype);
+  if ((op == WE_OP_GATED_ADD || op == WE_OP_ADD_BIAS) && d == 0) return fail(ctx, WE_EINVAL, "d must be positive");
+  int rc = check_span(ctx, a, bytes, "a");
+  if (!rc) rc = check_span(ctx, out, bytes, "out");
+  if (!rc) {
+    if (op == WE_OP_ADD_BIAS) rc = check_span(ctx, b, (uint64_t)(n < d ? n : d) * 4, "bias");
+    else if (op != WE_OP_GELU_TANH && op != WE_OP_SILU) rc = check_span(ctx, b, bytes, "b");
+  }
+  if (!rc && op == WE_OP_GATED_ADD) rc = check_span(ctx, c, (uint64_t)(n < d ? n : d) * 4, "gate");
+  if (rc) return rc;
+  hipError_t e = we::launch_elementwise(op, n, d ? d : 1, dtype, a, b, c, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "elementwise launch");
+}
+
+int we_layer_sum(we_ctx* ctx, uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w,
+                 float* out) {
+  if (!ctx) return WE_EINVAL;
+  int rc = check_span(ctx, x, (uint64_t)tokens * layers * dim * 4, "x");
+  if (!rc) rc = check_span(ctx, w, (uint64_t)layers * 4, "w");
+  if (!rc) rc = check_span(ctx, out, (uint64_t)tokens * dim * 4, "out");
+  if (rc) return rc;
+  hipError_t e = we::launch_layer_sum(tokens, layers, dim, x, w, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "layer sum launch");
+}
+
+int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale, float* out) {
+  if (!ctx) return WE_EINVAL;
+  int rc = check_span(ctx, packed, n, "packed");
+  if (!rc) rc = check_span(ctx, scale, 4, "scale");
+  if (!rc) rc = check_span(ctx, out, (uint64_t)n * 4, "out");
+  if (rc) return rc;
+  hipError_t e = we::launch_unpack_fp8(packed, n, scale, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "unpack launch");
+}
+
+int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, uint32_t rows, uint32_t k,
+                    uint32_t group, float* out) {
+  if (!ctx) return WE_EINVAL;
+  if (k % 8 || group == 0 || k % group) return fail(ctx, WE_EINVAL, "K must be a multiple of 8 and of the group size");
+  int rc = check_span(ctx, words, (uint64_t)rows * k / 2, "words");
+  if (!rc) rc = check_span(ctx, scales, (uint64_t)rows * (k / group) * 2, "scales");
+  if (!rc) rc = check_span(ctx, out, (uint64_t)rows * k * 4, "out");
+  if (rc) return rc;
+  hipError_t e = we::launch_dequant_int4(words, scales, rows, k, group, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "dequant launch");
+}
+
+}  // extern "C"

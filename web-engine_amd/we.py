@@ -1,0 +1,483 @@
+"""Python host side of the MI355X matmul path: a ctypes binding of libwe.so (include/we.h) and a
+mirror of the reference's operator API over it.
+
+  Graph                 src/gpu/graph.ts:26-155   (buffer / read / free / mark / release / copy / destroy / stats)
+  matmul_params         src/kernels/matmul.ts:198-212
+  k_split_for           src/model/ops.ts:42-45
+  Linear, linear        src/model/ops.ts:24-32, 48-73 (bias fused in the GEMM epilogue; LoRA via split-K + accumulate)
+  norm, no_mod          src/model/ops.ts:78-85
+  rotate                src/model/ops.ts:89-93
+  swiglu, sigmoid_gate, gated_add, add, gelu, silu      src/model/ops.ts:101-113
+  matmul_fp8 / matmul_bf16 / matmul_f32 one-shots        src/kernels/matmul.ts:223-265
+  unpack_fp8 one-shot   src/kernels/fp8.ts:24-36
+
+Every op runs the hand-written gfx950 kernels in libwe.so; there is no CPU fallback. Importing works
+without a GPU (the symbol checks use that); creating a Graph needs the library and a GPU and raises
+otherwise.
+"""
+import ctypes
+import os
+import pathlib
+import re
+
+import numpy as np
+
+PKG = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PKG / "libwe.so"
+HEADER = PKG.parent / "include" / "we.h"
+
+F32, F16, BF16, FP8, INT4 = 0, 1, 2, 3, 4
+DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
+ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
+EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
+OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
+ERRORS = {1: "WE_EINVAL", 2: "WE_ENOMEM", 3: "WE_EHIP", 4: "WE_EUNSUPPORTED"}
+TILE = 128  # the reference's matmul tile (src/kernels/matmul.ts:33), used by k_split_for
+
+
+class WeError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+        self.name = ERRORS.get(code, str(code))
+
+
+class MatmulParams(ctypes.Structure):
+    """Binary image of the reference's 13 x u32 matmul Params (src/kernels/matmul.ts:120-126)."""
+    _fields_ = [("m", ctypes.c_uint32), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32), ("scale", ctypes.c_float),
+                ("x_stride", ctypes.c_uint32), ("w_stride", ctypes.c_uint32), ("y_stride", ctypes.c_uint32),
+                ("x_offset", ctypes.c_uint32), ("w_offset", ctypes.c_uint32), ("y_offset", ctypes.c_uint32),
+                ("width", ctypes.c_uint32), ("cin", ctypes.c_uint32), ("k_split", ctypes.c_uint32)]
+
+
+_P, _I, _U32, _U64, _SZ, _F, _I64 = (ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t,
+                                     ctypes.c_float, ctypes.c_int64)
+SIGNATURES = {
+    "we_ctx_create": (_I, [_I, _P]),
+    "we_ctx_destroy": (_I, [_P]),
+    "we_last_error": (ctypes.c_char_p, [_P]),
+    "we_device_info": (_I, [_P, ctypes.c_char_p, _SZ, _P, _P]),
+    "we_buf_alloc": (_I, [_P, _SZ, _P]),
+    "we_buf_free": (_I, [_P, _P]),
+    "we_buf_upload": (_I, [_P, _P, _SZ, _P, _SZ]),
+    "we_buf_download": (_I, [_P, _P, _SZ, _P, _SZ]),
+    "we_buf_copy": (_I, [_P, _P, _SZ, _P, _SZ, _SZ]),
+    "we_mark": (_I, [_P, _P]),
+    "we_release": (_I, [_P, _SZ, _P, _SZ]),
+    "we_stats": (_I, [_P, _P, _P, _P]),
+    "we_sync": (_I, [_P]),
+    "we_host_alloc": (_I, [_P, _SZ, _P]),
+    "we_host_free": (_I, [_P, _P]),
+    "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
+    "we_wait_ticket": (_I, [_P, _U64]),
+    "we_record_compute": (_I, [_P, _P]),
+    "we_ticket_done": (_I, [_P, _U64, _P]),
+    "we_timer_start": (_I, [_P]),
+    "we_timer_stop": (_I, [_P, _P]),
+    "we_matmul_params_make": (_I, [_P, _U32, _U32, _U32, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "we_ksplit_for": (_U32, [_U32, _U32, _U32]),
+    "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
+    "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
+    "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
+    "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _P]),
+    "we_elementwise": (_I, [_P, _I, _SZ, _SZ, _I, _P, _P, _P, _P]),
+    "we_layer_sum": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
+    "we_unpack_fp8": (_I, [_P, _P, _SZ, _P, _P]),
+    "we_dequant_int4": (_I, [_P, _P, _P, _U32, _U32, _U32, _P]),
+}
+
+_lib = None
+
+
+def header_functions():
+    """Names of every function declared in include/we.h."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|uint32_t|const char\*)\s+(we_\w+)\s*\(", text, re.M)))
+
+
+def load_library(path=None):
+    """Loads libwe.so (raising if it is missing) and declares every entry point's signature."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = pathlib.Path(path or os.environ.get("WE_LIB", LIB_PATH))
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+class Buffer:
+    """A device buffer (or a slice of one, like Graph.slice): address and size in bytes."""
+    __slots__ = ("ptr", "size", "base")
+
+    def __init__(self, ptr, size, base=None):
+        self.ptr, self.size, self.base = ptr, size, base
+
+    def __int__(self):
+        return self.ptr
+
+    def __repr__(self):
+        return f"Buffer(0x{self.ptr:x}, {self.size})"
+
+
+def _addr(b):
+    if b is None:
+        return None
+    if isinstance(b, Buffer):
+        return ctypes.c_void_p(b.ptr)
+    return ctypes.c_void_p(int(b))
+
+
+class Graph:
+    """Mirror of the reference's Graph (src/gpu/graph.ts:26-155) over one we_ctx: buffers stay on the GPU,
+    work is queued in order on one compute stream, freed buffers are pooled by size and come back zeroed."""
+
+    def __init__(self, device=0):
+        self.lib = load_library()
+        ctx = ctypes.c_void_p()
+        rc = self.lib.we_ctx_create(device, ctypes.byref(ctx))
+        if rc:
+            raise WeError(rc, f"we_ctx_create(device={device}) failed with {ERRORS.get(rc, rc)}: no usable gfx950 GPU")
+        self.ctx = ctx
+
+    # ---- errors
+    def check(self, rc):
+        if rc:
+            raise WeError(rc, self.lib.we_last_error(self.ctx).decode())
+
+    # ---- Graph API
+    def buffer(self, data=None, nbytes=None):
+        """A zeroed buffer of `nbytes` bytes, or one holding `data` (a numpy array or bytes)."""
+        arr = None
+        if data is not None and not isinstance(data, int):
+            arr = np.ascontiguousarray(data)
+            nbytes = arr.nbytes
+        elif isinstance(data, int):
+            nbytes = data
+        p = ctypes.c_void_p()
+        self.check(self.lib.we_buf_alloc(self.ctx, nbytes, ctypes.byref(p)))
+        buf = Buffer(p.value, nbytes)
+        if arr is not None and nbytes:
+            self.check(self.lib.we_buf_upload(self.ctx, _addr(buf), 0, arr.ctypes.data_as(ctypes.c_void_p), nbytes))
+        return buf
+
+    upload = buffer
+
+    def write(self, buf, data, offset=0):
+        arr = np.ascontiguousarray(data)
+        self.check(self.lib.we_buf_upload(self.ctx, _addr(buf), offset, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
+
+    @staticmethod
+    def slice(buf, offset, size):
+        return Buffer(buf.ptr + offset, size, base=buf)
+
+    def read(self, buf, nbytes=None, dtype=np.uint8, count=None):
+        nbytes = buf.size if nbytes is None else nbytes
+        if count is not None:
+            nbytes = count * np.dtype(dtype).itemsize
+        out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)
+        self.check(self.lib.we_buf_download(self.ctx, _addr(buf), 0, out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
+        return out
+
+    def copy(self, src, src_offset, dst, dst_offset, size):
+        self.check(self.lib.we_buf_copy(self.ctx, _addr(src), src_offset, _addr(dst), dst_offset, size))
+
+    def free(self, buf):
+        self.check(self.lib.we_buf_free(self.ctx, _addr(buf)))
+
+    def mark(self):
+        m = ctypes.c_size_t()
+        self.check(self.lib.we_mark(self.ctx, ctypes.byref(m)))
+        return m.value
+
+    def release(self, mark, keep=()):
+        arr = (ctypes.c_void_p * max(1, len(keep)))(*[b.ptr for b in keep])
+        self.check(self.lib.we_release(self.ctx, mark, arr, len(keep)))
+
+    @property
+    def stats(self):
+        c, r, b = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        self.check(self.lib.we_stats(self.ctx, ctypes.byref(c), ctypes.byref(r), ctypes.byref(b)))
+        return {"created": c.value, "reused": r.value, "createdBytes": b.value}
+
+    def sync(self):
+        self.check(self.lib.we_sync(self.ctx))
+
+    on_submitted_work_done = sync
+
+    def device_info(self):
+        name = ctypes.create_string_buffer(64)
+        cu, lds = ctypes.c_int(), ctypes.c_int()
+        self.check(self.lib.we_device_info(self.ctx, name, 64, ctypes.byref(cu), ctypes.byref(lds)))
+        return {"arch": name.value.decode(), "compute_units": cu.value, "lds_bytes": lds.value}
+
+    def destroy(self):
+        if getattr(self, "ctx", None):
+            self.lib.we_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
+
+    # ---- pinned host memory and streaming
+    def host_alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.check(self.lib.we_host_alloc(self.ctx, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def host_free(self, ptr):
+        self.check(self.lib.we_host_free(self.ctx, ctypes.c_void_p(ptr)))
+
+    def stream_copy(self, dst, pinned_src, nbytes, after=0):
+        t = ctypes.c_uint64()
+        self.check(self.lib.we_stream_copy(self.ctx, _addr(dst), ctypes.c_void_p(pinned_src), nbytes, after,
+                                           ctypes.byref(t)))
+        return t.value
+
+    def wait_ticket(self, ticket):
+        self.check(self.lib.we_wait_ticket(self.ctx, ticket))
+
+    def record_compute(self):
+        t = ctypes.c_uint64()
+        self.check(self.lib.we_record_compute(self.ctx, ctypes.byref(t)))
+        return t.value
+
+    def ticket_done(self, ticket):
+        d = ctypes.c_int()
+        self.check(self.lib.we_ticket_done(self.ctx, ticket, ctypes.byref(d)))
+        return bool(d.value)
+
+    # ---- timing
+    def timer_start(self):
+        self.check(self.lib.we_timer_start(self.ctx))
+
+    def timer_stop(self):
+        ms = ctypes.c_float()
+        self.check(self.lib.we_timer_stop(self.ctx, ctypes.byref(ms)))
+        return ms.value
+
+    # ---- raw ops (one dispatch each)
+    def matmul(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0):
+        self.check(self.lib.we_matmul(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                      _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags))
+
+    def rmsnorm(self, rows, d, eps, offset, dtype, x, weight, scale, shift, out):
+        self.check(self.lib.we_rmsnorm(self.ctx, rows, d, eps, offset, dtype, _addr(x), _addr(weight), _addr(scale),
+                                       _addr(shift), _addr(out)))
+
+    def rope(self, tokens, heads, pairs, half, dtype, x, cos, sin, out):
+        self.check(self.lib.we_rope(self.ctx, tokens, heads, pairs, 1 if half else 0, dtype, _addr(x), _addr(cos),
+                                    _addr(sin), _addr(out)))
+
+    def qk_norm_rope(self, tokens, heads, head_dim, eps, offset, weight, rope_from, half, cos, sin, dtype, x, out):
+        self.check(self.lib.we_qk_norm_rope(self.ctx, tokens, heads, head_dim, eps, offset, _addr(weight), rope_from,
+                                            1 if half else 0, _addr(cos), _addr(sin), dtype, _addr(x), _addr(out)))
+
+    def elementwise(self, op, n, d, dtype, a, b, c, out):
+        self.check(self.lib.we_elementwise(self.ctx, op, n, d, dtype, _addr(a), _addr(b), _addr(c), _addr(out)))
+
+    def layer_sum(self, tokens, layers, dim, x, w, out):
+        self.check(self.lib.we_layer_sum(self.ctx, tokens, layers, dim, _addr(x), _addr(w), _addr(out)))
+
+    def unpack_fp8_raw(self, packed, n, scale, out):
+        self.check(self.lib.we_unpack_fp8(self.ctx, _addr(packed), n, _addr(scale), _addr(out)))
+
+    def dequant_int4_raw(self, words, scales, rows, k, group, out):
+        self.check(self.lib.we_dequant_int4(self.ctx, _addr(words), _addr(scales), rows, k, group, _addr(out)))
+
+
+# ------------------------------------------------------------------------------------------ operator API
+
+def matmul_params(m, n, k, scale, x_stride=None, w_stride=None, y_stride=None, x_offset=None, w_offset=None,
+                  y_offset=None, k_split=1, graph=None):
+    """src/kernels/matmul.ts:198-212, with its validation messages."""
+    lib = load_library()
+    p = MatmulParams()
+    d = lambda v: -1 if v is None else v
+    ctx = graph.ctx if graph is not None else None
+    rc = lib.we_matmul_params_make(ctx, m, n, k, scale, d(x_stride), d(w_stride), d(y_stride), d(x_offset),
+                                   d(w_offset), d(y_offset), k_split, ctypes.byref(p))
+    if rc:
+        msg = lib.we_last_error(ctx).decode() if ctx is not None else _params_message(k, x_stride, w_stride, x_offset,
+                                                                                       w_offset)
+        raise WeError(rc, msg)
+    return p
+
+
+def _params_message(k, xs, ws, xo, wo):
+    vals = {"K": k, "xStride": k if xs is None else xs, "wStride": k if ws is None else ws,
+            "xOffset": xo or 0, "wOffset": wo or 0}
+    for name, v in vals.items():
+        if v % 4:
+            return f"{name} must be a multiple of 4, got {v}"
+    return "invalid matmul parameters"
+
+
+def k_split_for(m, n, k):
+    """src/model/ops.ts:42-45"""
+    return load_library().we_ksplit_for(m, n, k)
+
+
+class Linear:
+    """src/model/ops.ts:24-32, plus the additive int4 dtype (scales f16 [n, k / group])."""
+
+    def __init__(self, buffer, dtype, scale, n, k, bias=None, lora=None, scales=None, group=64):
+        self.buffer, self.dtype, self.scale, self.n, self.k = buffer, dtype, scale, n, k
+        self.bias, self.lora, self.scales, self.group = bias, lora, scales, group
+
+
+def _wdt(dtype):
+    return DTYPES[dtype] if isinstance(dtype, str) else dtype
+
+
+def linear(graph, x, w, m, x_dtype=F32, y_dtype=F32, gelu_tanh=False):
+    """y[m, n] = x[m, k] . W^T (+ bias) (+ lora up.scale * (x . down^T) . up^T, added in place): src/model/ops.ts:61-73.
+    The bias (and optional tanh GELU) run in the GEMM epilogue instead of separate passes."""
+    y = graph.buffer(m * w.n * ELEM_BYTES[y_dtype])
+    flags = (EPI_BIAS if w.bias is not None else 0) | (EPI_GELU if gelu_tanh else 0)
+    graph.matmul(matmul_params(m, w.n, w.k, w.scale, graph=graph), x_dtype, x, _wdt(w.dtype), w.buffer, y_dtype, y,
+                 scales=w.scales, group=w.group if _wdt(w.dtype) == INT4 else 0, bias=w.bias, flags=flags)
+    if w.lora is None:
+        return y
+    down, up = w.lora
+    if down.k != w.k or up.n != w.n or up.k != down.n or down.n % 4:
+        raise WeError(1, "LoRA shapes do not fit the linear layer")
+    t = _narrow_linear(graph, x, down, m, x_dtype)
+    graph.matmul(matmul_params(m, up.n, up.k, up.scale, graph=graph), F32, t, _wdt(up.dtype), up.buffer, y_dtype, y,
+                 flags=EPI_ACCUMULATE)
+    return y
+
+
+def _narrow_linear(graph, x, w, m, x_dtype):
+    """src/model/ops.ts:48-58: split-K partials, then layerSum over them."""
+    split = k_split_for(m, w.n, w.k)
+    if split == 1:
+        return linear(graph, x, w, m, x_dtype, F32)
+    partials = graph.buffer(split * m * w.n * 4)
+    graph.matmul(matmul_params(m, w.n, w.k, w.scale, k_split=split, graph=graph), x_dtype, x, _wdt(w.dtype), w.buffer,
+                 F32, partials, flags=EPI_SPLIT_K)
+    y = graph.buffer(m * w.n * 4)
+    ones = graph.buffer(np.ones(split, np.float32))
+    graph.layer_sum(1, split, m * w.n, partials, ones, y)
+    return y
+
+
+class Mod:
+    def __init__(self, scale, shift):
+        self.scale, self.shift = scale, shift
+
+
+def no_mod(graph, d):
+    """src/model/ops.ts:85"""
+    return Mod(graph.buffer(d * 4), graph.buffer(d * 4))
+
+
+def norm(graph, x, weight, rows, d, mod, eps=1e-5, offset=1.0, dtype=F32):
+    """src/model/ops.ts:78-82"""
+    out = graph.buffer(rows * d * ELEM_BYTES[dtype])
+    graph.rmsnorm(rows, d, eps, offset, dtype, x, weight, mod.scale if mod else None, mod.shift if mod else None, out)
+    return out
+
+
+class Rope:
+    def __init__(self, cos, sin, pairs, tokens):
+        self.cos, self.sin, self.pairs, self.tokens = cos, sin, pairs, tokens
+
+
+def rotate(graph, x, heads, rope, pairing="interleaved", dtype=F32):
+    """src/model/ops.ts:89-93"""
+    out = graph.buffer(rope.tokens * heads * rope.pairs * 2 * ELEM_BYTES[dtype])
+    graph.rope(rope.tokens, heads, rope.pairs, pairing == "half", dtype, x, rope.cos, rope.sin, out)
+    return out
+
+
+def _elementwise(graph, op, a, b, c, n, d=1, dtype=F32):
+    out = graph.buffer(n * ELEM_BYTES[dtype])
+    graph.elementwise(op, n, d, dtype, a, b, c, out)
+    return out
+
+
+def swiglu(graph, gate, up, n, dtype=F32):
+    return _elementwise(graph, OP_SWIGLU, gate, up, None, n, 1, dtype)
+
+
+def sigmoid_gate(graph, a, gate, n, dtype=F32):
+    return _elementwise(graph, OP_SIGMOID_GATE, a, gate, None, n, 1, dtype)
+
+
+def gated_add(graph, x, h, g, n, d, dtype=F32):
+    return _elementwise(graph, OP_GATED_ADD, x, h, g, n, d, dtype)
+
+
+def add_bias(graph, x, b, n, d, dtype=F32):
+    return _elementwise(graph, OP_ADD_BIAS, x, b, None, n, d, dtype)
+
+
+def add(graph, x, h, n, dtype=F32):
+    return _elementwise(graph, OP_ADD, x, h, None, n, 1, dtype)
+
+
+def gelu(graph, x, n, dtype=F32):
+    return _elementwise(graph, OP_GELU_TANH, x, None, None, n, 1, dtype)
+
+
+def silu(graph, x, n, dtype=F32):
+    return _elementwise(graph, OP_SILU, x, None, None, n, 1, dtype)
+
+
+# ------------------------------------------------------------------------------------------ one-shots (tests)
+
+def _oneshot(graph, x, w_bytes, w_dtype, scale, m, n, k, x_dtype=F32, y_dtype=F32, **layout):
+    p = matmul_params(m, n, k, scale, graph=graph, **layout)
+    xb = graph.buffer(x)
+    wb = graph.buffer(w_bytes)
+    rows = m * (p.k_split if layout.get("k_split", 1) > 1 else 1)
+    y = graph.buffer(max(1, rows * p.y_stride + p.y_offset) * ELEM_BYTES[y_dtype])
+    graph.matmul(p, x_dtype, xb, w_dtype, wb, y_dtype, y)
+    return y
+
+
+def matmul_fp8(graph, x, w, scale, m, n, k):
+    """src/kernels/matmul.ts:223-233"""
+    x = np.asarray(x, np.float32)
+    w = np.asarray(w, np.uint8)
+    if x.size != m * k or w.size != n * k:
+        raise WeError(1, "x or w does not match the shape")
+    return graph.read(_oneshot(graph, x, w, FP8, scale, m, n, k), dtype=np.float32, count=m * n)
+
+
+def matmul_bf16(graph, x, w, scale, m, n, k):
+    """src/kernels/matmul.ts:236-246 (w: raw little-endian bf16 bytes or uint16 values)"""
+    x = np.asarray(x, np.float32)
+    w = np.asarray(w)
+    if x.size != m * k or w.nbytes != n * k * 2:
+        raise WeError(1, "x or w does not match the shape")
+    return graph.read(_oneshot(graph, x, w, BF16, scale, m, n, k), dtype=np.float32, count=m * n)
+
+
+def matmul_f32(graph, x, w, scale, m, n, k, output_length=None, **layout):
+    """src/kernels/matmul.ts:249-265"""
+    x = np.asarray(x, np.float32)
+    w = np.asarray(w, np.float32)
+    y = _oneshot(graph, x, w, F32, scale, m, n, k, **layout)
+    return graph.read(y, dtype=np.float32, count=output_length or m * n)
+
+
+def unpack_fp8(graph, data, scale):
+    """src/kernels/fp8.ts:24-36 one-shot: out[i] = e4m3(byte i) * scale."""
+    data = np.asarray(data, np.uint8)
+    packed = graph.buffer(np.pad(data, (0, (-data.size) % 4)) if data.size else np.zeros(4, np.uint8))
+    sc = graph.buffer(np.array([scale], np.float32))
+    out = graph.buffer(max(4, data.size * 4))
+    graph.unpack_fp8_raw(packed, data.size, sc, out)
+    return graph.read(out, dtype=np.float32, count=data.size)
