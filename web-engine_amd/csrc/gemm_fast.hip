@@ -2,15 +2,25 @@
 // 16-bit weights, fp32 accumulation on MFMA 32x32x16, y = x . W^T * scale (+ bias, gelu, accumulate,
 // split-K) with the semantics of matmulWgsl (src/kernels/matmul.ts:118-178).
 //
-// Differences from the general kernel (gemm.hip), all about keeping the main loop straight-line:
-//  * global loads are buffer loads through a buffer resource whose size is the operand's extent: a row
-//    past M / N or a chunk past the K range gets an out-of-range offset and reads 0 in hardware, so no
-//    lane ever branches; the k advance is the scalar offset of the load;
-//  * LDS fragments of MFMA step s + 1 are read while the MFMAs of step s run;
-//  * the fp8 NaN-code fix-up (the reference shader decodes 0x7f / 0xff to +-480) is decided once per
-//    stage for the whole wave, so the common path has no branch between MFMAs.
-// Requirements (checked on the host): rows 16-byte aligned, K and the split-K slice multiples of 16,
-// operand extents below 2^31 bytes.
+// Structure (one workgroup per BM x BN output tile, 64 k per pipeline stage, S stages in LDS):
+//  * Operands move HBM -> LDS with direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): each load
+//    instruction of a wave fills 1 KB of LDS (lane i writes bytes [16 i, 16 i + 16)), no VGPR staging.
+//    The source address of each lane is chosen so that the LDS image is XOR-swizzled: 16-byte chunk c of
+//    row r sits at chunk position c ^ swz(r), which makes the MFMA fragment reads bank-conflict free.
+//    Rows past M / N and k past the slice read through an out-of-range buffer offset and land as zeros.
+//  * Loads run S - 1 stages ahead of the MFMAs. One workgroup barrier per 64-k block, placed before the
+//    last MFMA step of the block: after it the block's stage is free for the load S blocks ahead, and the
+//    next block's stage is complete, so its first fragments are read while the last MFMAs still run.
+//  * The weight tile is the MFMA's A operand and the activation tile its B operand, so the fp32
+//    accumulators hold runs of 4 consecutive output columns per lane: the epilogue stores 8 or 16 bytes
+//    per lane instead of 2.
+//  * fp8 weights stay 1 byte per value in LDS and are unpacked to bf16 / f16 in registers by the
+//    hardware converter (OCP e4m3fn). That converter turns the two NaN codes 0x7f / 0xff into NaN, where
+//    the reference shader decodes them as +-480 (src/kernels/fp8.ts:12-20). The main loop does not look
+//    at the codes; a NaN in a wave's accumulators (which finite weights and inputs never produce) sends
+//    that wave through an exact recompute that decodes every byte with the shader's formula.
+// Requirements (checked on the host): x / W rows 16-byte aligned, K and the split-K slice multiples of
+// 16, operand extents below 2^31 bytes.
 #include "common.h"
 #include "internal.h"
 
@@ -21,6 +31,8 @@ namespace {
 constexpr int BK = 64;
 constexpr uint32_t kInvalid = 0x80000000u;  // a byte offset past every extent: the load returns 0
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 family)
+
+typedef __attribute__((address_space(3))) void lds_ptr_t;
 
 struct FastArgs {
   const void* x;
@@ -34,6 +46,7 @@ struct FastArgs {
   uint32_t kc;
   uint32_t tiles_m, tiles_n;
   uint32_t flags, y_dtype;
+  uint32_t vec_store;  // 1: y rows and y_offset allow 4-value vector stores
 };
 
 __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
@@ -42,21 +55,18 @@ __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
   return xcd < rem ? xcd * (base + 1) + idx : rem * (base + 1) + (xcd - rem) * base + idx;
 }
 
-__device__ __forceinline__ void store_y(const FastArgs& a, size_t o, float val) {
-  const bool acc = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
-  if (a.y_dtype == F32) {
-    float* y = (float*)a.y;
-    y[o] = acc ? y[o] + val : val;
-  } else if (a.y_dtype == BF16) {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_bf16(acc ? bf16_to_f32(y[o]) + val : val);
-  } else {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_f16(acc ? f16_to_f32(y[o]) + val : val);
-  }
-}
+// Chunk position of logical 16-byte chunk c in row r: rows of 128 B (8 chunks) and rows of 64 B
+// (4 chunks). Both keep any 8 (and any 16) consecutive rows reading one logical chunk on distinct banks.
+__device__ __forceinline__ int swz128(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz64(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-// fp8 word -> 4 x 16-bit without the NaN-code check (the caller decides that per stage)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// fp8 word -> 4 x 16-bit through the hardware converter
 template <bool IS_F16>
 __device__ __forceinline__ u32x2 cvt_fp8x4(uint32_t w) {
   u32x2 r;
@@ -70,24 +80,67 @@ __device__ __forceinline__ u32x2 cvt_fp8x4(uint32_t w) {
   return r;
 }
 
+template <int YT>
+__device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float (&v)[4], bool acc) {
+  if constexpr (YT == F32) {
+    f32x4* p = (f32x4*)((float*)a.y + o);
+    f32x4 r = {v[0], v[1], v[2], v[3]};
+    if (acc) r += *p;
+    *p = r;
+  } else {
+    u32x2* p = (u32x2*)((uint16_t*)a.y + o);
+    float t[4] = {v[0], v[1], v[2], v[3]};
+    if (acc) {
+      const u32x2 old = *p;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t h = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
+        t[e] += YT == BF16 ? bf16_to_f32((uint16_t)h) : f16_to_f32((uint16_t)h);
+      }
+    }
+    uint32_t hb[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) hb[e] = YT == BF16 ? f32_to_bf16(t[e]) : f32_to_f16(t[e]);
+    *p = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+  }
+}
+
+template <int YT>
+__device__ __forceinline__ void store1(const FastArgs& a, size_t o, float v, bool acc) {
+  if constexpr (YT == F32) {
+    float* y = (float*)a.y;
+    y[o] = acc ? y[o] + v : v;
+  } else {
+    uint16_t* y = (uint16_t*)a.y;
+    if (acc) v += YT == BF16 ? bf16_to_f32(y[o]) : f16_to_f32(y[o]);
+    y[o] = YT == BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+  }
+}
+
 }  // namespace
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool IS_F16, int BT>
-__global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_fast_kernel(FastArgs a) {
-  constexpr int T = WAVES_M * WAVES_N * 64;
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool IS_F16, int BT, int S, int YT>
+__global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArgs a) {
+  constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr bool B8 = BT == FP8;
-  constexpr int A_STAGE = BM * 8;                // u32x4 chunks per stage
-  constexpr int B_STAGE = B8 ? BN * 4 : BN * 8;  // u32x4 chunks per stage
-  constexpr int STAGE = A_STAGE + B_STAGE;
-  constexpr int A_IT = A_STAGE / T, B_IT = B_STAGE / T;
-  static_assert(A_STAGE % T == 0 && B_STAGE % T == 0, "tile / thread mismatch");
-  __shared__ u32x4 lds[2 * STAGE];
+  constexpr int WB = B8 ? 1 : 2;                  // weight bytes per value
+  constexpr int A_BYTES = BM * 128;               // x: BM rows x 64 k x 2 B
+  constexpr int B_ROW = 64 * WB;                  // weight row bytes per stage
+  constexpr int B_BYTES = BN * B_ROW;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_INS = A_BYTES / 1024, B_INS = B_BYTES / 1024;
+  static_assert(A_INS % NW == 0 && B_INS % NW == 0, "stage loads must split evenly over the waves");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0 && WTM >= 32, "wave tile");
+  constexpr int A_PW = A_INS / NW, B_PW = B_INS / NW, L = A_PW + B_PW;  // loads per wave per stage
+  constexpr int B_RPI = 1024 / B_ROW;                                     // weight rows per load
+  constexpr int B_CPR = B_ROW / 16;                                       // 16-B chunks per weight row
+  __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int half = lane >> 5, l32 = lane & 31;
+  const int h = lane >> 5, l32 = lane & 31;
 
   const uint32_t pid = xcd_remap_f(blockIdx.x, gridDim.x);
   constexpr uint32_t GROUP_M = 4;
@@ -105,24 +158,64 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_fast_kernel(FastAr
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
 
-  // per-lane byte offsets of the chunks this thread stages (k = 0 of the row), invalid past M / N
-  uint32_t offa[A_IT], offb[B_IT];
-  int kca[A_IT], kcb[B_IT];  // k of the chunk inside the 64-k block
+  // ---- per-lane source offsets of the direct-to-LDS loads (k = 0 of the block), invalid past M / N
+  uint32_t offa[A_PW], offb[B_PW];
+  int ka[A_PW], kb8[B_PW];  // first k of the lane's chunk inside the 64-k block
 #pragma unroll
-  for (int i = 0; i < A_IT; i++) {
-    const int idx = i * T + tid, r = idx >> 3, c = idx & 7;
+  for (int i = 0; i < A_PW; i++) {
+    const int ins = wave + i * NW;
+    const int r = ins * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz128(r);
     const uint32_t row = row0 + r;
     offa[i] = row < a.m ? (row * a.x_stride + c * 8) * 2 : kInvalid;
-    kca[i] = c * 8;
+    ka[i] = c * 8;
   }
 #pragma unroll
-  for (int i = 0; i < B_IT; i++) {
-    const int idx = i * T + tid;
-    const int r = B8 ? idx >> 2 : idx >> 3, c = B8 ? idx & 3 : idx & 7;
+  for (int j = 0; j < B_PW; j++) {
+    const int ins = wave + j * NW;
+    const int r = ins * B_RPI + lane / B_CPR;
+    const int c = (lane % B_CPR) ^ (B8 ? swz64(r) : swz128(r));
     const uint32_t col = col0 + r;
-    offb[i] = col < a.n ? (B8 ? col * a.w_stride + c * 16 : (col * a.w_stride + c * 8) * 2) : kInvalid;
-    kcb[i] = B8 ? c * 16 : c * 8;
+    offb[j] = col < a.n ? (col * a.w_stride * WB + c * 16) : kInvalid;
+    kb8[j] = c * 16 / WB;
   }
+
+  // issue the loads of the 64-k block starting at kb into stage st
+  auto issue = [&](uint32_t kb, int st) {
+    const bool full = kb + BK <= k_end;  // only the last block of a slice can be partial
+    char* base = lds + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_PW; i++) {
+      const uint32_t o = (full || kb + ka[i] < k_end) ? offa[i] : kInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t*)(base + (wave + i * NW) * 1024), 16, o, (int)(kb * 2), 0,
+                                               0);
+    }
+#pragma unroll
+    for (int j = 0; j < B_PW; j++) {
+      const uint32_t o = (full || kb + kb8[j] < k_end) ? offb[j] : kInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(base + A_BYTES + (wave + j * NW) * 1024), 16, o,
+                                               (int)(kb * WB), 0, 0);
+    }
+  };
+
+  // ---- per-lane LDS read offsets of the MFMA fragments (within a stage)
+  // k order inside a 64-k block: MFMA step s, lane half h uses the 8 k of logical chunk 4h + s for both
+  // operands (a permutation of k shared by x and W, so the sum is unchanged).
+  uint32_t rda[4], rdb[B8 ? 2 : 4];
+  {
+    const int sa = (4 * h) ^ swz128(l32);
+#pragma unroll
+    for (int s = 0; s < 4; s++) rda[s] = (uint32_t)((wm * WTM + l32) * 128 + ((sa ^ s) * 16));
+    if constexpr (B8) {
+      const int sb = (2 * h) ^ swz64(l32);  // 16-B chunk 2h + t holds the 16 k of steps 2t, 2t + 1
+#pragma unroll
+      for (int t = 0; t < 2; t++) rdb[t] = (uint32_t)(A_BYTES + (wn * WTN + l32) * 64 + ((sb ^ t) * 16));
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; s++) rdb[s] = (uint32_t)(A_BYTES + (wn * WTN + l32) * 128 + ((sa ^ s) * 16));
+    }
+  }
+  auto rd = [&](uint32_t off) { return *(const u32x4*)(lds + off); };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -130,159 +223,172 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_fast_kernel(FastAr
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
 
-  u32x4 ra[A_IT], rb[B_IT];
-  auto load_global = [&](uint32_t kb) {
-    const bool full = kb + BK <= k_end;  // uniform: only the last block of a slice can be partial
-    const int sa = (int)(kb * 2), sb = (int)(B8 ? kb : kb * 2);
+  u32x4 xf[2][TM];           // x fragments, double-buffered over steps
+  u32x4 wr[2][TN];           // fp8: raw 16-B chunks (t = 0, 1); 16-bit: fragments double-buffered over steps
+  auto read_x = [&](uint32_t st_off, int s, u32x4 (&d)[TM]) {
 #pragma unroll
-    for (int i = 0; i < A_IT; i++) {
-      const uint32_t o = (full || kb + kca[i] < k_end) ? offa[i] : kInvalid;
-      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, sa, 0));
-    }
-#pragma unroll
-    for (int i = 0; i < B_IT; i++) {
-      const uint32_t o = (full || kb + kcb[i] < k_end) ? offb[i] : kInvalid;
-      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, sb, 0));
-    }
+    for (int i = 0; i < TM; i++) d[i] = rd(st_off + rda[s] + i * 32 * 128);
   };
-
-  auto store_lds = [&](int stage) {
-    u32x4* sa = lds + stage * STAGE;
-    u32x4* sb = sa + A_STAGE;
+  auto read_w = [&](uint32_t st_off, int q, u32x4 (&d)[TN]) {
 #pragma unroll
-    for (int i = 0; i < A_IT; i++) {
-      const int idx = i * T + tid, r = idx >> 3, c = idx & 7;
-      sa[r * 8 + (c ^ (r & 7))] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_IT; i++) {
-      const int idx = i * T + tid;
-      if constexpr (B8) {
-        const int r = idx >> 2, c = idx & 3;
-        sb[r * 4 + (c ^ ((r >> 1) & 3))] = rb[i];
-      } else {
-        const int r = idx >> 3, c = idx & 7;
-        sb[r * 8 + (c ^ (r & 7))] = rb[i];
-      }
-    }
-  };
-
-  // LDS row indices and swizzle terms of this lane's fragments
-  int arow[TM], brow[TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++) arow[i] = wm * WTM + i * 32 + l32;
-#pragma unroll
-  for (int j = 0; j < TN; j++) brow[j] = wn * WTN + j * 32 + l32;
-
-  auto compute = [&](int stage) {
-    const u32x4* sa = lds + stage * STAGE;
-    const u32x4* sb = sa + A_STAGE;
-    u32x4 af[2][TM];
-    u32x4 braw[B8 ? TN : 1][2];
-    u32x4 bf[TN];
-    if constexpr (B8) {
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int r = brow[j], sw = (r >> 1) & 3;
-        braw[j][0] = sb[r * 4 + ((2 * half) ^ sw)];
-        braw[j][1] = sb[r * 4 + ((2 * half + 1) ^ sw)];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; i++) af[0][i] = sa[arow[i] * 8 + ((half * 4) ^ (arow[i] & 7))];
-    bool nan_codes = false;
-    if constexpr (B8) {
-      uint32_t any = 0;
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int q = 0; q < 2; q++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) any |= ((braw[j][q][e] & 0x7f7f7f7fu) + 0x01010101u);
-      nan_codes = __ballot((any & 0x80808080u) != 0u) != 0;
-    }
-    static_for<0, 4>([&](auto S) {
-      constexpr int s = decltype(S)::value;
-      if constexpr (s < 3) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-          af[(s + 1) & 1][i] = sa[arow[i] * 8 + ((half * 4 + s + 1) ^ (arow[i] & 7))];
-      }
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        if constexpr (B8) {
-          const u32x4 q = braw[j][s >> 1];
-          const uint32_t w0 = q[(s & 1) * 2], w1 = q[(s & 1) * 2 + 1];
-          u32x2 lo, hi;
-          if (nan_codes) {
-            lo = fp8x4_to_16<IS_F16>(w0);
-            hi = fp8x4_to_16<IS_F16>(w1);
-          } else {
-            lo = cvt_fp8x4<IS_F16>(w0);
-            hi = cvt_fp8x4<IS_F16>(w1);
-          }
-          bf[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
-        } else {
-          bf[j] = sb[brow[j] * 8 + ((half * 4 + s) ^ (brow[j] & 7))];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(af[s & 1][i], bf[j], acc[i][j]);
-    });
+    for (int j = 0; j < TN; j++) d[j] = rd(st_off + rdb[q] + j * 32 * B_ROW);
   };
 
   if (nk > 0) {
-    load_global(k_begin);
-    store_lds(0);
-    __syncthreads();
+    // prologue: the first S blocks (or all of them)
+#pragma unroll
+    for (int p = 0; p < S; p++)
+      if (p < nk) issue(k_begin + (uint32_t)p * BK, p);
+    if (nk >= S) wait_vmcnt<(S - 1) * L>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    read_x(0, 0, xf[0]);
+    read_w(0, 0, wr[0]);
+
+    int cur = 0;
     for (int it = 0; it < nk; ++it) {
-      const int cur = it & 1;
-      if (it + 1 < nk) load_global(k_begin + (uint32_t)(it + 1) * BK);
-      compute(cur);
-      if (it + 1 < nk) store_lds(cur ^ 1);
-      __syncthreads();
+      const uint32_t cur_off = (uint32_t)(cur * STAGE);
+      const int nxt = cur + 1 == S ? 0 : cur + 1;
+      const uint32_t nxt_off = (uint32_t)(nxt * STAGE);
+      static_for<0, 4>([&](auto SI) {
+        constexpr int s = decltype(SI)::value;
+        if constexpr (s < 3) {
+          read_x(cur_off, s + 1, xf[(s + 1) & 1]);
+          if constexpr (B8) {
+            if constexpr (s == 1) read_w(cur_off, 1, wr[1]);
+          } else {
+            read_w(cur_off, s + 1, wr[(s + 1) & 1]);
+          }
+        } else {
+          // every wave has its last fragments of this block; block it + 1 must be complete
+          if (it + S - 1 < nk) wait_vmcnt<(S - 2) * L>();
+          else wait_vmcnt<0>();
+          lds_barrier();
+          if (it + S < nk) issue(k_begin + (uint32_t)(it + S) * BK, cur);
+          if (it + 1 < nk) {
+            read_x(nxt_off, 0, xf[0]);
+            read_w(nxt_off, 0, wr[0]);
+          }
+        }
+        u32x4 wf[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          if constexpr (B8) {
+            const u32x4 q = wr[s >> 1][j];
+            const u32x2 lo = cvt_fp8x4<IS_F16>(q[(s & 1) * 2]), hi = cvt_fp8x4<IS_F16>(q[(s & 1) * 2 + 1]);
+            wf[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          } else {
+            wf[j] = wr[s & 1][j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(wf[j], xf[s & 1][i], acc[i][j]);
+      });
+      cur = nxt;
     }
   }
 
-  const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;
-  static_for<0, TM>([&](auto I) {
-    static_for<0, TN>([&](auto J) {
-      constexpr int i = decltype(I)::value, j = decltype(J)::value;
-      const uint32_t col = col0 + wn * WTN + j * 32 + l32;
-      const bool col_ok = col < a.n;
-      const float b = (col_ok && (a.flags & WE_EPI_BIAS_BIT)) ? a.bias[col] : 0.0f;
-      static_for<0, 16>([&](auto V) {
-        constexpr int v = decltype(V)::value;
-        const uint32_t row = row0 + wm * WTM + i * 32 + 8 * (v / 4) + 4 * half + (v % 4);
-        if (col_ok && row < a.m) {
-          float val = acc[i][j][v] * a.scale + b;
-          if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
-          store_y(a, (size_t)a.y_offset + (zrow + row) * (size_t)a.y_stride + col, val);
+  if constexpr (B8) {
+    // NaN in the accumulators: only a NaN weight code (or a non-finite input) makes one. Recompute this
+    // wave's tile with the shader's decoding of every byte (0x7f / 0xff -> +-480).
+    float probe = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) probe += acc[i][j][v] * 0.0f;
+    if (__ballot(probe != probe) != 0) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+      for (uint32_t k0 = k_begin; k0 < k_end; k0 += 16) {
+        const uint32_t kk = k0 + 8 * h;  // 8 k per lane half; k_end - k0 >= 16 (multiples of 16)
+        u32x4 xr[TM];
+        u32x4 wv[TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+          const uint32_t o = row < a.m ? (row * a.x_stride + kk) * 2 : kInvalid;
+          xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
         }
-      });
-    });
-  });
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          const uint32_t col = col0 + wn * WTN + j * 32 + l32;
+          const uint32_t o = col < a.n ? col * a.w_stride + kk : kInvalid;
+          const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
+          const u32x2 lo = fp8x4_to_16<IS_F16>(raw.x), hi = fp8x4_to_16<IS_F16>(raw.y);
+          wv[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(wv[j], xr[i], acc[i][j]);
+      }
+    }
+  }
+
+  // ---- epilogue: lane (l32, h) holds row l32 of each 32-row sub-tile and, for q = 0..3, the columns
+  // 8q + 4h .. 8q + 4h + 3 of each 32-column sub-tile (accumulator entries 4q .. 4q + 3)
+  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
+  const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
+  const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
+  const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+    if (row >= a.m) continue;
+    const size_t yrow = (size_t)a.y_offset + (zrow + row) * (size_t)a.y_stride;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t c0 = col0 + wn * WTN + j * 32 + 8 * q + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float t = acc[i][j][4 * q + e] * a.scale;
+          if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
+          if (gelu) t = gelu_tanh(t);
+          v[e] = t;
+        }
+        if (a.vec_store && c0 + 3 < a.n) {
+          store4<YT>(a, yrow + c0, v, accum);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], accum);
+        }
+      }
+    }
+  }
 }
 
-template <int BM, int BN, int WM, int WN, bool IS_F16, int BT>
+template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S>
 static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
   a.tiles_n = (a.n + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_fast_kernel<BM, BN, WM, WN, IS_F16, BT>), dim3(a.tiles_m * a.tiles_n, splits),
-                     dim3(WM * WN * 64), 0, s, a);
+  const dim3 grid(a.tiles_m * a.tiles_n, splits), block(WM * WN * 64);
+  switch (a.y_dtype) {
+    case F32: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32>), grid, block, 0, s, a); break;
+    case F16: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F16>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, BF16>), grid, block, 0, s, a); break;
+  }
   return hipGetLastError();
 }
 
 template <bool IS_F16, int BT>
 static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg, hipStream_t s) {
+  constexpr bool B8 = BT == FP8;
   switch (cfg) {
-    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 2, IS_F16, BT>(a, splits, s);
-    case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 2, 2, IS_F16, BT>(a, splits, s);
-    case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT>(a, splits, s);
-    case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT>(a, splits, s);
-    default: return launch_fast_cfg<32, 64, 1, 2, IS_F16, BT>(a, splits, s);
+    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 4, 2, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
+    case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
+    case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
+    case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);
+    default: return launch_fast_cfg<32, 64, 1, 2, IS_F16, BT, 3>(a, splits, s);
   }
 }
 
@@ -301,6 +407,7 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   const uint64_t xb = L.k ? ((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2 : 0;
   const uint64_t wbytes = L.k ? ((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb : 0;
   if (xb >= kInvalid || wbytes >= kInvalid) return hipErrorNotSupported;
+  const int yb = L.y_dtype == F32 ? 4 : 2;
   FastArgs a{};
   a.x = (const char*)L.x + (uint64_t)L.x_offset * 2;
   a.w = (const char*)L.w + (uint64_t)L.w_offset * wb;
@@ -319,6 +426,10 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.kc = kc;
   a.flags = L.flags;
   a.y_dtype = (uint32_t)L.y_dtype;
+  a.vec_store = ((uintptr_t)L.y % (4 * yb) == 0 && ((uint64_t)L.y_offset * yb) % (4 * yb) == 0 &&
+                 ((uint64_t)L.y_stride * yb) % (4 * yb) == 0)
+                    ? 1u
+                    : 0u;
   const int cfg = L.cfg >= 0 ? L.cfg : pick_gemm_cfg(L.m, L.n, splits);
   if (f16) {
     if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, stream);
