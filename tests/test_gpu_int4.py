@@ -92,3 +92,17 @@ def test_refuses_unsupported_layouts(graph):
     with pytest.raises(we.WeError, match="split-K"):
         graph.matmul(we.matmul_params(1, 8, 128, 1.0, k_split=2, graph=graph), we.F16, xb, we.INT4, wb, we.F32, yb,
                      scales=sb, group=64, flags=we.EPI_SPLIT_K)
+
+
+@pytest.mark.parametrize("k", [256, 2048, 2304, 3072, 3584])
+def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
+    """M = 1 runs the pipelined decode kernel (x staged in LDS, weights through an LDS ring); it must give
+    bit-identical results to the general kernel at every K, including K whose x staging spans several
+    passes per thread and whose blocks span several ring chunks."""
+    n = 80
+    rng = np.random.default_rng(k)
+    words, scales, x, _ = make(rng, 1, n, k, 64)
+    fast = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
+    monkeypatch.setenv("WE_INT4_GENERIC", "1")
+    general = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
+    assert np.array_equal(fast, general)

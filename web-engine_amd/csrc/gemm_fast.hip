@@ -385,6 +385,8 @@ static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg,
   constexpr bool B8 = BT == FP8;
   switch (cfg) {
     case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 4, 2, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
+    case 5: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
+    case 6: return launch_fast_cfg<256, 256, 2, 2, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
     case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);

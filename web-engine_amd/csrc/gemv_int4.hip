@@ -1,21 +1,31 @@
-// int4-weight GEMV / skinny GEMM on gfx950 (decode shapes, M <= 32 per launch row-block):
+// int4-weight GEMV / skinny GEMM on gfx950 (decode shapes):
 //   y[m, n] = scale * sum_g s[n, g] * sum_{k in g} x[m, k] * q[n, k]
 // W: u32 [N, K/8], eight two's-complement nibbles per word along K (low nibble = lowest k);
 // s: f16 [N, K/group]. The per-group scale multiplies the f32 partial sum of that group, so the
 // dequantized value q * s is never rounded to 16 bits.
 //
-// Work split: a workgroup of 4 waves owns 32 output columns n and one block of 32 rows m; the four
-// waves split K (a wavefront-level split-K) and their f32 partials are summed through LDS.
-// Inside a wave the MFMA 32x32x16 runs with x as the A operand (rows m) and W as the B operand
-// (columns n): lane l holds row n0 + l % 32 of W and, for each 64-k block, one 16-byte load of
-// words [8b + 4h, 8b + 4h + 4) (h = l / 32). MFMA j of the block consumes word j, so its k-slot h
-// maps to k = 64b + 32h + 8j .. +8; the x fragment is read from the same k. Every W byte is loaded
-// exactly once, all loads of a wave are issued before the first MFMA needs them, and the 16 nibbles
-// of a dword pair are unpacked in registers (f16: byte-permute + mask + one packed FMA per pair).
+// The kernel is bound by the HBM stream of W (0.5 B per weight), so it is built to keep that stream
+// full: every weight load of a wave is issued before the first MFMA needs it.
+//  * A workgroup of 4 waves owns 16 output columns n and one block of 16 rows m; wave w takes a quarter
+//    of the 64-k blocks (a wavefront-level split-K); the four f32 partial tiles are summed through LDS.
+//    At K = 3584, N = 18944 that is 1184 workgroups / 4736 waves, all resident at once on 256 CUs.
+//  * MFMA 16x16x32 with x as the A operand (rows m) and W as the B operand (columns n): lane l holds
+//    column n0 + l % 16 and, for each 64-k block, the two words [8b + 2g, 8b + 2g + 2) (g = l / 16),
+//    one 8-byte load. MFMA e of the block consumes word e, so its k-slot g maps to k = 64b + 16g + 8e,
+//    all inside one scale group; x is read from the same k. The 8 nibbles of a word become 8 exact f16
+//    (byte-permute + mask + one packed FMA per pair) or bf16 values in registers.
+//  * The output column of a lane is fixed, so one f16 scale per lane and block multiplies the four
+//    accumulator entries of that block's partial.
+//  * x rows and scales are read through buffer resources: rows past M / columns past N read zeros, and
+//    x fragments are prefetched two blocks ahead of the MFMAs.
+#include <cstdlib>
+
 #include "common.h"
 #include "internal.h"
 
 namespace we {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct Int4Args {
   const void* x;
@@ -27,10 +37,24 @@ struct Int4Args {
   float scale;
   uint32_t x_stride, y_stride, x_offset, y_offset;
   uint32_t flags, y_dtype;
+  uint32_t x_bytes, w_bytes, s_bytes;  // readable extents
 };
 
-// eight nibbles (one word) -> eight f16 in k order, exact
-__device__ __forceinline__ u32x4 int4x8_to_f16(uint32_t w) {
+namespace {
+constexpr uint32_t kInvalid = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;
+}  // namespace
+
+// v_and_or_b32 with the mask in a VGPR and the constant in an SGPR (one instruction; the compiler
+// otherwise splits it into an and and an or with literals)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "s"(c));
+  return r;
+}
+
+// eight nibbles (one word) -> eight f16 in k order, exact (13 VALU ops)
+__device__ __forceinline__ u32x4 int4x8_to_f16(uint32_t w, uint32_t mask) {
   const uint32_t u = w ^ 0x88888888u;  // q + 8 in [0, 15] per nibble
   const f16x2 mul = {(_Float16)1.0f, (_Float16)0.0625f};
   const f16x2 add = {(_Float16)-1032.0f, (_Float16)-72.0f};
@@ -40,7 +64,7 @@ __device__ __forceinline__ u32x4 int4x8_to_f16(uint32_t w) {
     // byte p of u into bytes 0 and 2: lo half gets nibble 2p at bits 0-3, hi half nibble 2p+1 at bits 4-7
     const uint32_t sel = (uint32_t)p | (0x0cu << 8) | ((uint32_t)p << 16) | (0x0cu << 24);
     const uint32_t t = __builtin_amdgcn_perm(u, u, sel);
-    const uint32_t v = (t & 0x00f0000fu) | 0x64006400u;  // lo: 1024 + u0, hi: 1024 + 16 u1
+    const uint32_t v = and_or(t, mask, 0x64006400u);  // mask 0x00f0000f -> lo: 1024 + u0, hi: 1024 + 16 u1
     const f16x2 h = __builtin_bit_cast(f16x2, v);
     const f16x2 q = __builtin_elementwise_fma(h, mul, add);  // lo: u0 - 8, hi: u1 - 8
     r[p] = __builtin_bit_cast(uint32_t, q);
@@ -61,127 +85,337 @@ __device__ __forceinline__ u32x4 int4x8_to_bf16(uint32_t w) {
   return r;
 }
 
+template <bool IS_F16>
+__device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
+  if constexpr (IS_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// x fragments of one 64-k block for lane (m, g): k = 64b + 16g + 8e + (0..7), e = 0, 1. 16-bit x: one
+// 16-B load per e. f32 x: two 16-B loads per e, split into hi + lo bf16 planes.
 template <int XT>
-__device__ __forceinline__ void load_x_frag(const Int4Args& a, bool m_ok, size_t xrow, uint32_t k, u32x4 (&out)[4][2]) {
-  // 32 consecutive k of one row: 4 fragments of 8 (one per MFMA j); f32 rows give hi + lo bf16 planes
-  if (!m_ok) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) out[j][0] = out[j][1] = u32x4{0, 0, 0, 0};
-    return;
-  }
+struct XFrag {
+  static constexpr int NA = XT == F32 ? 2 : 1;
+  u32x4 v[2][NA];
+};
+
+template <int XT>
+__device__ __forceinline__ void load_x(const __amdgpu_buffer_rsrc_t& rx, uint32_t off, XFrag<XT>& f) {
   if constexpr (XT == F32) {
-    const u32x4* p = (const u32x4*)((const float*)a.x + xrow + k);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const u32x4 v0 = p[2 * j], v1 = p[2 * j + 1];
-      float f[8] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w),
-                    __uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w)};
+    for (int e = 0; e < 2; e++) {
+      const u32x4 v0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, e * 32, 0));
+      const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, e * 32 + 16, 0));
+      float fl[8] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w),
+                     __uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w)};
       uint32_t hi[8], lo[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        hi[e] = f32_to_bf16(f[e]);
-        lo[e] = f32_to_bf16(f[e] - bf16_to_f32((uint16_t)hi[e]));
+      for (int i = 0; i < 8; i++) {
+        hi[i] = f32_to_bf16(fl[i]);
+        lo[i] = f32_to_bf16(fl[i] - bf16_to_f32((uint16_t)hi[i]));
       }
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        out[j][0][e] = hi[2 * e] | (hi[2 * e + 1] << 16);
-        out[j][1][e] = lo[2 * e] | (lo[2 * e + 1] << 16);
+      for (int i = 0; i < 4; i++) {
+        f.v[e][0][i] = hi[2 * i] | (hi[2 * i + 1] << 16);
+        f.v[e][1][i] = lo[2 * i] | (lo[2 * i + 1] << 16);
       }
     }
   } else {
-    const u32x4* p = (const u32x4*)((const uint16_t*)a.x + xrow + k);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      out[j][0] = p[j];
-      out[j][1] = u32x4{0, 0, 0, 0};
-    }
+    for (int e = 0; e < 2; e++)
+      f.v[e][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, e * 16, 0));
   }
 }
 
-constexpr int INT4_PF = 8;  // 64-k blocks of W prefetched per wave at a time
+constexpr int INT4_CH = 14;  // 64-k blocks whose weights a wave stages at once (7 KB of LDS per wave)
+constexpr int INT4_XPF = 2;  // blocks of x fragments in flight ahead of the MFMAs
+
+typedef __attribute__((address_space(3))) void lds_ptr_t;
 
 template <int XT>
 __global__ void __launch_bounds__(256) int4_gemv_kernel(Int4Args a) {
   constexpr bool IS_F16 = XT == F16;
-  constexpr int NA = XT == F32 ? 2 : 1;
-  __shared__ float red[4][16][64];
+  constexpr int NA = XFrag<XT>::NA;
+  constexpr int XB = XT == F32 ? 4 : 2;
+  constexpr int WAVE_LDS = 16 * INT4_CH * 32;  // 16 rows x CH blocks x 32 B
+  static_assert(WAVE_LDS % 1024 == 0 && 4 * WAVE_LDS >= 4 * 64 * 16, "LDS staging layout");
+  __shared__ __attribute__((aligned(1024))) char lds[4 * WAVE_LDS];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l32 = lane & 31, h = lane >> 5;
-  const uint32_t n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
-  const uint32_t n = n0 + l32, m = m0 + l32;
-  const bool n_ok = n < a.n, m_ok = m < a.m;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const uint32_t n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const uint32_t m = m0 + l16;
   const uint32_t nblk = a.k / 64;
   const uint32_t per = (nblk + 3) / 4;
   const uint32_t b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
-  const uint32_t words_per_row = a.k / 8, groups_per_row = a.k / a.group;
-  const u32x4* wrow = (const u32x4*)(a.w + (size_t)(n_ok ? n : 0) * words_per_row) + h;  // + 2 per block
-  const uint16_t* srow = a.s + (size_t)(n_ok ? n : 0) * groups_per_row;
-  const size_t xrow = (size_t)a.x_offset + (size_t)(m_ok ? m : 0) * a.x_stride;
+  const uint32_t gpb = a.group / 64;  // blocks per scale group
+  const uint32_t row_bytes = a.k / 2;
+  char* wl = lds + wave * WAVE_LDS;  // this wave's staging area (no other wave touches it)
 
-  f32x16 acc = {};
-  u32x4 wq[INT4_PF];
-  auto fetch = [&](uint32_t first) {
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, (int)a.s_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
+  const uint32_t s_off = n0 + l16 < a.n ? (n0 + l16) * (a.k / a.group) * 2 : kInvalid;        // + 2 per group
+  const uint32_t x_off = m < a.m ? (a.x_offset + m * a.x_stride + g * 16) * XB : kInvalid;  // + 64 XB per block
+
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t c = b0; c < b1; c += INT4_CH) {
+    const int nb = (int)min((uint32_t)INT4_CH, b1 - c);  // wave-uniform
+    // Stage W[n0 .. n0 + 16, blocks c .. c + nb) into LDS row-major (row r at r * nb * 32): 16-byte piece
+    // p of the area is loaded by lane p % 64 of load p / 64, so every load reads whole runs of each row.
+    const int pieces_row = 2 * nb;
 #pragma unroll
-    for (int i = 0; i < INT4_PF; i++) {
-      const uint32_t b = first + i;
-      wq[i] = (n_ok && b < b1) ? __builtin_nontemporal_load(wrow + 2 * (size_t)b) : u32x4{0, 0, 0, 0};
-    }
-  };
-  if (b0 < b1) fetch(b0);
-  for (uint32_t c = b0; c < b1; c += INT4_PF) {
-    u32x4 cur[INT4_PF];
-#pragma unroll
-    for (int i = 0; i < INT4_PF; i++) cur[i] = wq[i];
-    if (c + INT4_PF < b1) fetch(c + INT4_PF);
-#pragma unroll
-    for (int i = 0; i < INT4_PF; i++) {
-      const uint32_t b = c + i;
-      if (b >= b1) break;
-      const float s = n_ok ? f16_to_f32(srow[(b * 64) / a.group]) : 0.0f;
-      u32x4 xf[4][2];
-      load_x_frag<XT>(a, m_ok, xrow, b * 64 + h * 32, xf);
-      f32x16 part = {};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const u32x4 wf = IS_F16 ? int4x8_to_f16(cur[i][j]) : int4x8_to_bf16(cur[i][j]);
-#pragma unroll
-        for (int p = 0; p < NA; p++) part = mfma_32x32x16<IS_F16>(xf[j][p], wf, part);
+    for (int j = 0; j < INT4_CH / 2; j++) {
+      if (2 * j < nb) {
+        const int p = j * 64 + lane;
+        const int r = p / pieces_row, q = p - r * pieces_row;
+        const uint32_t row = n0 + r;
+        const uint32_t o = (r < 16 && row < a.n) ? row * row_bytes + c * 32 + q * 16 : kInvalid;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(wl + j * 1024), 16, o, 0, 0, 0);
       }
-#pragma unroll
-      for (int v = 0; v < 16; v++) acc[v] += part[v] * s;
     }
+    uint16_t sc[INT4_CH];
+#pragma unroll
+    for (int i = 0; i < INT4_CH; i++)
+      if (i < nb) sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, s_off + ((c + i) / gpb) * 2, 0, 0);
+    XFrag<XT> xf[INT4_XPF + 1];
+#pragma unroll
+    for (int i = 0; i < INT4_XPF; i++)
+      if (i < nb) load_x<XT>(rx, x_off + (c + i) * 64 * XB, xf[i]);
+    // the staged weights (and the first scales / x fragments) must have landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < INT4_CH; i++) {
+      if (i < nb) {
+        if (i + INT4_XPF < nb) load_x<XT>(rx, x_off + (c + i + INT4_XPF) * 64 * XB, xf[(i + INT4_XPF) % (INT4_XPF + 1)]);
+        const XFrag<XT>& cur = xf[i % (INT4_XPF + 1)];
+        // lane (n, g): words [2g, 2g + 2) of block i of row n, i.e. k = 64 (c + i) + 16 g + 8 e
+        const u32x2 wq = *(const u32x2*)(wl + l16 * (nb * 32) + i * 32 + g * 8);
+        f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const u32x4 wf = IS_F16 ? int4x8_to_f16(wq[e], 0x00f0000fu) : int4x8_to_bf16(wq[e]);
+#pragma unroll
+          for (int p = 0; p < NA; p++) part = mfma16<IS_F16>(cur.v[e][p], wf, part);
+        }
+        acc += part * f16_to_f32(sc[i]);
+      }
+    }
+    // every lane has read its fragments before the next chunk's loads overwrite the area
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
-#pragma unroll
-  for (int v = 0; v < 16; v++) red[wave][v][lane] = acc[v];
+  // lane l holds column n0 + l % 16 and rows m0 + 4 (l / 16) + (0..3); the staging areas are reused
+  f32x4_t* red = (f32x4_t*)lds;  // [4 waves][64 lanes]
   __syncthreads();
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const int idx = threadIdx.x * 4 + e;  // 0 .. 1023
-    const int v = idx >> 6, ln = idx & 63;
-    const float sum = red[0][v][ln] + red[1][v][ln] + red[2][v][ln] + red[3][v][ln];
-    const uint32_t row = m0 + 8 * (v / 4) + 4 * (ln >> 5) + (v % 4);
-    const uint32_t col = n0 + (ln & 31);
-    if (row >= a.m || col >= a.n) continue;
-    float val = sum * a.scale;
-    if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
-    if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
-    const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
-    if (a.y_dtype == F32) {
-      float* y = (float*)a.y;
-      y[o] = (a.flags & WE_EPI_ACCUMULATE_BIT) ? y[o] + val : val;
-    } else if (a.y_dtype == BF16) {
-      uint16_t* y = (uint16_t*)a.y;
-      y[o] = f32_to_bf16((a.flags & WE_EPI_ACCUMULATE_BIT) ? bf16_to_f32(y[o]) + val : val);
-    } else {
-      uint16_t* y = (uint16_t*)a.y;
-      y[o] = f32_to_f16((a.flags & WE_EPI_ACCUMULATE_BIT) ? f16_to_f32(y[o]) + val : val);
-    }
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  const int ln = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const float sum = red[ln][r] + red[64 + ln][r] + red[128 + ln][r] + red[192 + ln][r];
+  const uint32_t row = m0 + 4 * (ln >> 4) + r, col = n0 + (ln & 15);
+  if (row >= a.m || col >= a.n) return;
+  float val = sum * a.scale;
+  if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
+  if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
+  const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
+  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
+  if (a.y_dtype == F32) {
+    float* y = (float*)a.y;
+    y[o] = accum ? y[o] + val : val;
+  } else if (a.y_dtype == BF16) {
+    uint16_t* y = (uint16_t*)a.y;
+    y[o] = f32_to_bf16(accum ? bf16_to_f32(y[o]) + val : val);
+  } else {
+    uint16_t* y = (uint16_t*)a.y;
+    y[o] = f32_to_f16(accum ? f16_to_f32(y[o]) + val : val);
   }
 }
 
+// ------------------------------------------------------------------------------------------------------
+// Decode kernel (M * K * 2 bytes of x fit in LDS, 16-bit x): the same work split and MFMA layout as
+// above, with the weight stream software-pipelined. Each wave walks its blocks in chunks of 4 (2 KB of W,
+// a 3-slot LDS ring): the loads of chunk i + 2 are in flight while chunk i is unpacked and multiplied, so
+// the HBM stream and the VALU unpack overlap inside every wave. Each chunk issues exactly 2 direct-to-LDS
+// loads (out-of-range ones read zeros) and nothing else, so the vmcnt waits are constants.
+// x is staged once per workgroup in LDS with each 8-value chunk stored in the order
+// (x0, x4, x1, x5, x2, x6, x3, x7): that is the order in which a word's nibbles come out of the cheap
+// unpack below (no byte permute per pair), so both MFMA operands agree on the k of every slot.
+// Lanes whose row m >= M read row 0 of x: rows of the 16x16 tile past M are never stored.
+
+constexpr int PIPE_CB = 4;                     // 64-k blocks per chunk
+constexpr int PIPE_NBUF = 3;                   // chunk slots per wave
+constexpr int PIPE_CHUNK = 16 * PIPE_CB * 32;  // 2 KB: 16 rows x 4 blocks x 32 B
+constexpr int PIPE_XMAX = 7680;                // bytes of staged x; 31.5 KB of LDS per workgroup in all
+constexpr int PIPE_LOADS = 2;                  // loads per chunk (direct-to-LDS)
+constexpr int PIPE_MAXB = 16;                  // 64-k blocks per wave at most (K <= 4096)
+constexpr int PIPE_XPT = (PIPE_XMAX / 16 + 255) / 256;  // 16-byte x chunks staged per thread
+
+// eight nibbles -> eight exact f16, slots ordered (k0, k4), (k1, k5), (k2, k6), (k3, k7): 10 VALU ops
+__device__ __forceinline__ u32x4 int4x8_to_f16_il(uint32_t w, uint32_t m_lo, uint32_t m_hi) {
+  const uint32_t u = w ^ 0x88888888u;  // q + 8 per nibble
+  const uint32_t u8 = u >> 8;
+  const f16x2 sub = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const f16x2 mul = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const f16x2 add = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const uint32_t t0 = and_or(u, m_lo, 0x64006400u);   // 1024 + u0, 1024 + u4
+  const uint32_t t1 = and_or(u, m_hi, 0x64006400u);   // 1024 + 16 u1, 1024 + 16 u5
+  const uint32_t t2 = and_or(u8, m_lo, 0x64006400u);  // 1024 + u2, 1024 + u6
+  const uint32_t t3 = and_or(u8, m_hi, 0x64006400u);  // 1024 + 16 u3, 1024 + 16 u7
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t0) + sub);
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, t1), mul, add));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t2) + sub);
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, t3), mul, add));
+  return r;
+}
+
+// (x0..x7) -> (x0, x4, x1, x5, x2, x6, x3, x7)
+__device__ __forceinline__ u32x4 interleave8(u32x4 v) {
+  return u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
+__device__ __forceinline__ void int4_store(const Int4Args& a, uint32_t row, uint32_t col, float sum) {
+  float val = sum * a.scale;
+  if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
+  if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
+  const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
+  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
+  if (a.y_dtype == F32) {
+    float* y = (float*)a.y;
+    y[o] = accum ? y[o] + val : val;
+  } else if (a.y_dtype == BF16) {
+    uint16_t* y = (uint16_t*)a.y;
+    y[o] = f32_to_bf16(accum ? bf16_to_f32(y[o]) + val : val);
+  } else {
+    uint16_t* y = (uint16_t*)a.y;
+    y[o] = f32_to_f16(accum ? f16_to_f32(y[o]) + val : val);
+  }
+}
+
+template <int XT>
+__global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
+  constexpr bool IS_F16 = XT == F16;
+  __shared__ __attribute__((aligned(1024))) char wst[4 * PIPE_NBUF * PIPE_CHUNK];
+  __shared__ __attribute__((aligned(16))) char xs[PIPE_XMAX];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const uint32_t n0 = blockIdx.x * 16;
+  const uint32_t nblk = a.k / 64;
+  const uint32_t per = (nblk + 3) / 4;
+  const uint32_t b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
+  const int nch = (int)((b1 - b0 + PIPE_CB - 1) / PIPE_CB);
+  const uint32_t gpb = a.group / 64;
+  const uint32_t row_bytes = a.k / 2;
+  char* ws = wst + wave * (PIPE_NBUF * PIPE_CHUNK);
+
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, (int)a.s_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
+
+  // chunk image in LDS: row r (of 16) at r * 128, 16-byte piece q at position q ^ (r & 7); piece q of a
+  // row holds block q / 2, words 4 (q % 2) .. + 4. Lane l of load j fills position (64 j + l) % 8 of row
+  // (64 j + l) / 8.
+  uint32_t dma_off[2];
+  int dma_blk[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int p = j * 64 + lane, r = p >> 3, q = (p & 7) ^ (r & 7);
+    const uint32_t row = n0 + r;
+    dma_off[j] = row < a.n ? row * row_bytes + q * 16 : kInvalid;
+    dma_blk[j] = q >> 1;
+  }
+  auto issue = [&](int ci, auto SLOT) {
+    constexpr int s = decltype(SLOT)::value;
+    const uint32_t c = b0 + (uint32_t)ci * PIPE_CB;
+    char* slot = ws + s * PIPE_CHUNK;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint32_t o = c + dma_blk[j] < b1 ? dma_off[j] + c * 32 : kInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(slot + j * 1024), 16, o, 0, 0, 0);
+    }
+  };
+
+  // x rows m < M -> LDS, interleaved per 8-value chunk; the first two weight chunks load meanwhile
+  const uint32_t xchunks = a.m * (a.k / 8), cpr = a.k / 8;
+  u32x4 xv[PIPE_XPT];
+#pragma unroll
+  for (int j = 0; j < PIPE_XPT; j++) {
+    const uint32_t idx = tid + 256 * j;
+    const uint32_t m = idx / cpr, t = idx - m * cpr;
+    const uint32_t o = idx < xchunks ? (a.x_offset + m * a.x_stride + t * 8) * 2 : kInvalid;
+    xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+  }
+  // all scales of the wave's blocks (at most PIPE_MAXB), so that only direct-to-LDS loads are in
+  // flight in the main loop and the partial vmcnt waits there count nothing else
+  const uint32_t s_off = n0 + l16 < a.n ? (n0 + l16) * (a.k / a.group) * 2 : kInvalid;
+  uint16_t sc[PIPE_MAXB];
+#pragma unroll
+  for (int i = 0; i < PIPE_MAXB; i++)
+    sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, b0 + i < b1 ? s_off + ((b0 + i) / gpb) * 2 : kInvalid, 0, 0);
+  if (nch > 0) issue(0, std::integral_constant<int, 0>{});
+  if (nch > 1) issue(1, std::integral_constant<int, 1>{});
+#pragma unroll
+  for (int j = 0; j < PIPE_XPT; j++) {
+    const uint32_t idx = tid + 256 * j;
+    if (idx < xchunks) *(u32x4*)(xs + idx * 16) = IS_F16 ? interleave8(xv[j]) : xv[j];
+  }
+  __syncthreads();
+
+  const uint32_t m_lo = 0x000f000fu, m_hi = 0x00f000f0u;
+  const uint32_t xrow = (l16 < (int)a.m ? (uint32_t)l16 : 0u) * a.k * 2;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto step = [&](auto CI) {
+    constexpr int ci = decltype(CI)::value, s = ci % PIPE_NBUF;
+    if (ci + 2 < nch) issue(ci + 2, std::integral_constant<int, (s + 2) % PIPE_NBUF>{});
+    if (ci + 2 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PIPE_LOADS) : "memory");
+    else if (ci + 1 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PIPE_LOADS) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t c = b0 + (uint32_t)ci * PIPE_CB;
+    const char* slot = ws + s * PIPE_CHUNK;
+#pragma unroll
+    for (int i = 0; i < PIPE_CB; i++) {
+      if (c + i < b1) {
+        // lane (n, g): words [2g, 2g + 2) of block i of row n = piece 2i + g / 2, half g % 2
+        const u32x2 wq = *(const u32x2*)(slot + l16 * 128 + (((2 * i + (g >> 1)) ^ (l16 & 7)) * 16) + (g & 1) * 8);
+        const uint32_t xo = xrow + ((c + i) * 8 + 2 * g) * 16;  // chunk t = 8 b + 2 g + e
+        f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const u32x4 xa = *(const u32x4*)(xs + xo + e * 16);
+          const u32x4 wf = IS_F16 ? int4x8_to_f16_il(wq[e], m_lo, m_hi) : int4x8_to_bf16(wq[e]);
+          part = mfma16<IS_F16>(xa, wf, part);
+        }
+        acc += part * f16_to_f32(sc[ci * PIPE_CB + i]);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot s is reloaded two steps later
+  };
+  static_for<0, PIPE_MAXB / PIPE_CB>([&](auto CI) {
+    if (decltype(CI)::value < nch) step(CI);
+  });
+
+  // lane l holds column n0 + l % 16 and rows 4 (l / 16) + (0..3); sum the four waves' K-quarters
+  f32x4_t* red = (f32x4_t*)wst;
+  __syncthreads();
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  const int ln = tid & 63, r = tid >> 6;
+  const float sum = red[ln][r] + red[64 + ln][r] + red[128 + ln][r] + red[192 + ln][r];
+  const uint32_t row = 4 * (ln >> 4) + r, col = n0 + (ln & 15);
+  if (row < a.m && col < a.n) int4_store(a, row, col, sum);
+}
+
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
+  const int xb = L.x_dtype == F32 ? 4 : 2;
+  const uint64_t x_need = L.k ? ((uint64_t)L.x_offset + (uint64_t)(L.m - 1) * L.x_stride + L.k) * xb : 0;
+  const uint64_t w_need = (uint64_t)L.n * L.k / 2, s_need = (uint64_t)L.n * (L.k / L.group) * 2;
+  if (x_need >= kInvalid || w_need >= kInvalid || s_need >= kInvalid) return hipErrorNotSupported;
   Int4Args a{};
   a.x = L.x;
   a.w = L.w;
@@ -199,7 +433,18 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   a.y_offset = L.y_offset;
   a.flags = L.flags;
   a.y_dtype = (uint32_t)L.y_dtype;
-  dim3 grid((L.n + 31) / 32, (L.m + 31) / 32);
+  a.x_bytes = (uint32_t)x_need;
+  a.w_bytes = (uint32_t)w_need;
+  a.s_bytes = (uint32_t)s_need;
+  dim3 grid((L.n + 15) / 16, (L.m + 15) / 16);
+  const bool pipe = L.x_dtype != F32 && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.m <= 16 &&
+                    L.k / 64 <= 4 * (uint32_t)PIPE_MAXB &&
+                    getenv("WE_INT4_GENERIC") == nullptr;
+  if (pipe) {
+    if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_pipe_kernel<F16>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(int4_gemv_pipe_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
   switch (L.x_dtype) {
     case F16: hipLaunchKernelGGL(int4_gemv_kernel<F16>, grid, dim3(256), 0, stream, a); break;
     case BF16: hipLaunchKernelGGL(int4_gemv_kernel<BF16>, grid, dim3(256), 0, stream, a); break;
