@@ -97,12 +97,13 @@ def test_refuses_unsupported_layouts(graph):
 @pytest.mark.parametrize("k", [256, 2048, 2304, 3072, 3584])
 def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
     """M = 1 runs the pipelined decode kernel (x staged in LDS, weights through an LDS ring); it must give
-    bit-identical results to the general kernel at every K, including K whose x staging spans several
-    passes per thread and whose blocks span several ring chunks."""
+    the general kernel's results at every K, including K whose x staging spans several passes per thread
+    and whose blocks span several ring chunks (both sum exact f32 products; only the order inside an MFMA
+    may differ, hence the 1e-6 bound)."""
     n = 80
     rng = np.random.default_rng(k)
     words, scales, x, _ = make(rng, 1, n, k, 64)
     fast = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
     monkeypatch.setenv("WE_INT4_GENERIC", "1")
     general = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
-    assert np.array_equal(fast, general)
+    assert O.rel_error(fast, general) < 1e-6

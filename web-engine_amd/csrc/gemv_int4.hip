@@ -4,20 +4,23 @@
 // s: f16 [N, K/group]. The per-group scale multiplies the f32 partial sum of that group, so the
 // dequantized value q * s is never rounded to 16 bits.
 //
-// The kernel is bound by the HBM stream of W (0.5 B per weight), so it is built to keep that stream
-// full: every weight load of a wave is issued before the first MFMA needs it.
+// Both kernels are bound by the HBM stream of W (0.5 B per weight). Shared structure:
 //  * A workgroup of 4 waves owns 16 output columns n and one block of 16 rows m; wave w takes a quarter
 //    of the 64-k blocks (a wavefront-level split-K); the four f32 partial tiles are summed through LDS.
-//    At K = 3584, N = 18944 that is 1184 workgroups / 4736 waves, all resident at once on 256 CUs.
+//    At K = 3584, N = 18944 that is 1184 workgroups / 4736 waves.
+//  * W reaches LDS through direct-to-LDS buffer loads that read whole 128-byte runs of 8 rows per
+//    instruction (loads of the MFMA fragments straight from HBM read 32-byte pieces per row and doubled
+//    the L1 -> L2 requests).
 //  * MFMA 16x16x32 with x as the A operand (rows m) and W as the B operand (columns n): lane l holds
 //    column n0 + l % 16 and, for each 64-k block, the two words [8b + 2g, 8b + 2g + 2) (g = l / 16),
-//    one 8-byte load. MFMA e of the block consumes word e, so its k-slot g maps to k = 64b + 16g + 8e,
-//    all inside one scale group; x is read from the same k. The 8 nibbles of a word become 8 exact f16
-//    (byte-permute + mask + one packed FMA per pair) or bf16 values in registers.
+//    read from LDS. MFMA e of the block consumes word e, so its k-slot g maps to k = 64b + 16g + 8e,
+//    all inside one scale group; x is read from the same k. The 8 nibbles of a word become 8 exact
+//    f16 or bf16 values in registers.
 //  * The output column of a lane is fixed, so one f16 scale per lane and block multiplies the four
 //    accumulator entries of that block's partial.
-//  * x rows and scales are read through buffer resources: rows past M / columns past N read zeros, and
-//    x fragments are prefetched two blocks ahead of the MFMAs.
+// The general kernel (any M, f32 / f16 / bf16 x) stages all of a wave's weights at once and reads x
+// fragments from global memory two blocks ahead; the decode kernel further down (x fits in LDS) is the
+// one the M = 1 decode shape runs.
 #include <cstdlib>
 
 #include "common.h"
@@ -38,6 +41,7 @@ struct Int4Args {
   uint32_t x_stride, y_stride, x_offset, y_offset;
   uint32_t flags, y_dtype;
   uint32_t x_bytes, w_bytes, s_bytes;  // readable extents
+  uint32_t gshift;                     // group = 64 << gshift (decode kernel)
 };
 
 namespace {
@@ -237,22 +241,26 @@ __global__ void __launch_bounds__(256) int4_gemv_kernel(Int4Args a) {
 
 // ------------------------------------------------------------------------------------------------------
 // Decode kernel (M * K * 2 bytes of x fit in LDS, 16-bit x): the same work split and MFMA layout as
-// above, with the weight stream software-pipelined. Each wave walks its blocks in chunks of 4 (2 KB of W,
-// a 3-slot LDS ring): the loads of chunk i + 2 are in flight while chunk i is unpacked and multiplied, so
-// the HBM stream and the VALU unpack overlap inside every wave. Each chunk issues exactly 2 direct-to-LDS
-// loads (out-of-range ones read zeros) and nothing else, so the vmcnt waits are constants.
+// above, with the weight stream software-pipelined. Each wave walks its blocks in chunks of 4 (2 KB of W)
+// through a 2-slot LDS ring: both slots are requested up front and chunk i + 2 as soon as chunk i has been
+// unpacked and multiplied. Two slots (not more) keep the workgroup at 25.5 KB of LDS, so 6 workgroups fit
+// per CU and all 1184 workgroups of the decode shape are resident at once; measured on MI355X that beats
+// deeper rings with fewer resident workgroups. Each chunk issues exactly 2 direct-to-LDS loads
+// (out-of-range ones read zeros) and nothing else, so the vmcnt waits are constants.
+// The workgroup's scale tile (16 rows x K / group halves, contiguous) is staged in LDS once.
 // x is staged once per workgroup in LDS with each 8-value chunk stored in the order
 // (x0, x4, x1, x5, x2, x6, x3, x7): that is the order in which a word's nibbles come out of the cheap
 // unpack below (no byte permute per pair), so both MFMA operands agree on the k of every slot.
 // Lanes whose row m >= M read row 0 of x: rows of the 16x16 tile past M are never stored.
 
 constexpr int PIPE_CB = 4;                     // 64-k blocks per chunk
-constexpr int PIPE_NBUF = 3;                   // chunk slots per wave
+constexpr int PIPE_NBUF = 2;                   // chunk slots per wave (6 workgroups per CU fit)
 constexpr int PIPE_CHUNK = 16 * PIPE_CB * 32;  // 2 KB: 16 rows x 4 blocks x 32 B
-constexpr int PIPE_XMAX = 7680;                // bytes of staged x; 31.5 KB of LDS per workgroup in all
+constexpr int PIPE_XMAX = 7680;                // bytes of staged x (25.5 KB of LDS per workgroup in all)
 constexpr int PIPE_LOADS = 2;                  // loads per chunk (direct-to-LDS)
 constexpr int PIPE_MAXB = 16;                  // 64-k blocks per wave at most (K <= 4096)
 constexpr int PIPE_XPT = (PIPE_XMAX / 16 + 255) / 256;  // 16-byte x chunks staged per thread
+constexpr int PIPE_SMAX = 16 * PIPE_MAXB * 4 * 2;       // scale tile: 16 rows x (K / 64) groups x 2 B
 
 // eight nibbles -> eight exact f16, slots ordered (k0, k4), (k1, k5), (k2, k6), (k3, k7): 10 VALU ops
 __device__ __forceinline__ u32x4 int4x8_to_f16_il(uint32_t w, uint32_t m_lo, uint32_t m_hi) {
@@ -302,6 +310,7 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
   constexpr bool IS_F16 = XT == F16;
   __shared__ __attribute__((aligned(1024))) char wst[4 * PIPE_NBUF * PIPE_CHUNK];
   __shared__ __attribute__((aligned(16))) char xs[PIPE_XMAX];
+  __shared__ __attribute__((aligned(16))) char ss[PIPE_SMAX];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
@@ -310,7 +319,7 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
   const uint32_t per = (nblk + 3) / 4;
   const uint32_t b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
   const int nch = (int)((b1 - b0 + PIPE_CB - 1) / PIPE_CB);
-  const uint32_t gpb = a.group / 64;
+  const uint32_t gshift = a.gshift;  // group = 64 << gshift
   const uint32_t row_bytes = a.k / 2;
   char* ws = wst + wave * (PIPE_NBUF * PIPE_CHUNK);
 
@@ -351,29 +360,56 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
     const uint32_t o = idx < xchunks ? (a.x_offset + m * a.x_stride + t * 8) * 2 : kInvalid;
     xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
   }
-  // all scales of the wave's blocks (at most PIPE_MAXB), so that only direct-to-LDS loads are in
-  // flight in the main loop and the partial vmcnt waits there count nothing else
-  const uint32_t s_off = n0 + l16 < a.n ? (n0 + l16) * (a.k / a.group) * 2 : kInvalid;
-  uint16_t sc[PIPE_MAXB];
+  // the workgroup's scale tile s[n0 .. n0 + 16, :] is contiguous (16 G halves): 16-byte loads by the
+  // first threads, staged in LDS with x; loaded before the weights, so waiting for them never waits
+  // for the weight stream, and only direct-to-LDS loads are in flight in the main loop
+  const uint32_t ng = a.k / a.group;
+  const uint32_t s_pieces = ng * 2;  // 16 rows x ng halves = 2 ng pieces of 16 bytes
+  // a 16-byte load that straddles the end of the buffer reads nothing, so the last column tile (rows past
+  // N) loads its scales as halves
+  const bool s_whole = n0 + 16 <= a.n;
+  constexpr int SH = PIPE_SMAX / 2 / 256;  // halves per thread on the tail path
+  u32x4 sv = {0u, 0u, 0u, 0u};
+  uint16_t sh[SH] = {};
+  if (s_whole) {
+    sv = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)tid < s_pieces ? n0 * ng * 2 + tid * 16 : kInvalid, 0, 0));
+  } else {
 #pragma unroll
-  for (int i = 0; i < PIPE_MAXB; i++)
-    sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, b0 + i < b1 ? s_off + ((b0 + i) / gpb) * 2 : kInvalid, 0, 0);
-  if (nch > 0) issue(0, std::integral_constant<int, 0>{});
-  if (nch > 1) issue(1, std::integral_constant<int, 1>{});
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + 256 * j;
+      sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < 16 * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
+    }
+  }
+  static_for<0, PIPE_NBUF>([&](auto CI) {
+    if (decltype(CI)::value < nch) issue(decltype(CI)::value, CI);
+  });
 #pragma unroll
   for (int j = 0; j < PIPE_XPT; j++) {
     const uint32_t idx = tid + 256 * j;
     if (idx < xchunks) *(u32x4*)(xs + idx * 16) = IS_F16 ? interleave8(xv[j]) : xv[j];
   }
-  __syncthreads();
+  if (s_whole) {
+    if ((uint32_t)tid < s_pieces) *(u32x4*)(ss + tid * 16) = sv;
+  } else {
+#pragma unroll
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + 256 * j;
+      if (i < 16 * ng) *(uint16_t*)(ss + i * 2) = sh[j];
+    }
+  }
+  // x and scales visible to every wave; unlike __syncthreads this does not wait for the weight loads
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   const uint32_t m_lo = 0x000f000fu, m_hi = 0x00f000f0u;
   const uint32_t xrow = (l16 < (int)a.m ? (uint32_t)l16 : 0u) * a.k * 2;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto step = [&](auto CI) {
     constexpr int ci = decltype(CI)::value, s = ci % PIPE_NBUF;
-    if (ci + 2 < nch) issue(ci + 2, std::integral_constant<int, (s + 2) % PIPE_NBUF>{});
-    if (ci + 2 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PIPE_LOADS) : "memory");
+    // chunks ci + 1 .. min(ci + NBUF - 1, nch - 1) may still be in flight
+    static_assert(PIPE_NBUF >= 2 && PIPE_NBUF <= 4, "wait ladder below");
+    if (PIPE_NBUF >= 4 && ci + 3 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PIPE_LOADS) : "memory");
+    else if (PIPE_NBUF >= 3 && ci + 2 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PIPE_LOADS) : "memory");
     else if (ci + 1 < nch) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PIPE_LOADS) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const uint32_t c = b0 + (uint32_t)ci * PIPE_CB;
@@ -391,10 +427,11 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
           const u32x4 wf = IS_F16 ? int4x8_to_f16_il(wq[e], m_lo, m_hi) : int4x8_to_bf16(wq[e]);
           part = mfma16<IS_F16>(xa, wf, part);
         }
-        acc += part * f16_to_f32(sc[ci * PIPE_CB + i]);
+        acc += part * f16_to_f32(*(const uint16_t*)(ss + (l16 * ng + ((c + i) >> gshift)) * 2));
       }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot s is reloaded two steps later
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot s is free: load chunk ci + NBUF into it
+    if (ci + PIPE_NBUF < nch) issue(ci + PIPE_NBUF, std::integral_constant<int, s>{});
   };
   static_for<0, PIPE_MAXB / PIPE_CB>([&](auto CI) {
     if (decltype(CI)::value < nch) step(CI);
@@ -437,8 +474,11 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   a.w_bytes = (uint32_t)w_need;
   a.s_bytes = (uint32_t)s_need;
   dim3 grid((L.n + 15) / 16, (L.m + 15) / 16);
+  uint32_t gshift = 0;
+  while ((64u << gshift) < L.group) gshift++;
+  a.gshift = gshift;
   const bool pipe = L.x_dtype != F32 && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.m <= 16 &&
-                    L.k / 64 <= 4 * (uint32_t)PIPE_MAXB &&
+                    L.k / 64 <= 4 * (uint32_t)PIPE_MAXB && (64u << gshift) == L.group &&
                     getenv("WE_INT4_GENERIC") == nullptr;
   if (pipe) {
     if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_pipe_kernel<F16>, grid, dim3(256), 0, stream, a);
