@@ -6,17 +6,23 @@ bf16 activations, fp8 e4m3fn weights with per-tensor f32 scales, fp32 accumulati
 step's TFLOP/s (2 GEMMs x 2*M*N*K). Inputs are synthetic, generated with numpy and uploaded before the
 timed region.
 
-The same run reports, measured with HIP events on the compute stream:
-  * the up-projection GEMM alone (the dominant kernel: `roofline`) and the down-projection;
-  * the int4 GEMV at the Qwen2 decode shape (K = 3584, N = 18944, group 64, M = 1 / 8 / 16), rotating
-    10 weight copies (> 256 MB) so no launch reads its weights from the Infinity Cache;
+The same run reports, measured with HIP events on the context's compute stream (the stream every kernel
+is launched on):
+  * roofline: the up-projection GEMM (the dominant kernel) alone: 2*M*N*K FLOP per launch over its
+    average launch time, against the bf16 / f16 dense MFMA peak;
+  * roofline_int4: the int4 decode GEMV (M = 1, K = 3584, N = 18944, group 64): algorithmic bytes per
+    launch (every tensor read or written once) over its average launch time, against HBM peak; 10
+    weight copies rotate (> 256 MB) so no launch reads its weights from the Infinity Cache; M = 8 and 16
+    are reported beside it;
   * the dense bf16 GEMM at the DiT QKV shape and the small fp8 GEMM (M = 64);
+  * traffic: HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this script, scaled by
+    what the same counters read for the elementwise add kernel of known traffic that this script also
+    launches (calibration); the measured values live in profiles/traffic.json;
   * cpu_baseline: the float64 triple loop of the reference's tests (the oracle's restatement), on one
     host core, on a time-bounded sample of rows of the up-projection, extrapolated.
 """
 import argparse
 import json
-import os
 import pathlib
 import sys
 import time
@@ -30,6 +36,7 @@ import we  # noqa: E402
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 / f16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 METRIC = "dequant-GEMM TFLOP/s @M=4096 (%MFMA peak); int4 GEMV GB/s (%HBM peak)"
+TRAFFIC = ROOT / "profiles" / "traffic.json"
 
 
 def bf16_bits(a):
@@ -47,7 +54,7 @@ def time_launches(g, fn, iters):
     g.timer_start()
     for i in range(iters):
         fn(i)
-    return g.timer_stop() / iters  # ms per launch
+    return g.timer_stop() / iters  # ms per launch, HIP events on the compute stream
 
 
 def bench_mlp(g, steps, warmup, rng):
@@ -172,6 +179,15 @@ def cpu_baseline(budget_s):
                       f"{dt:.1f} s, extrapolated"}
 
 
+def measured_traffic(name):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs, or None."""
+    try:
+        entry = json.loads(TRAFFIC.read_text())["kernels"][name]
+        return float(entry["fetch_bytes"]) + float(entry["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,13 +207,13 @@ def main():
     info = g.device_info()
     print(f"[bench] device {info}", file=sys.stderr, flush=True)
     mlp = bench_mlp(g, args.steps, args.warmup, rng) if args.only in ("mlp", "all") else None
-    print(f"[bench] mlp done", file=sys.stderr, flush=True)
+    print("[bench] mlp done", file=sys.stderr, flush=True)
     int4 = bench_int4(g, rng) if args.only in ("int4", "all") else None
-    print(f"[bench] int4 done", file=sys.stderr, flush=True)
+    print("[bench] int4 done", file=sys.stderr, flush=True)
     extra = {}
     if args.only == "all":
-        extra["c2_bf16_qkv"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
-        extra["c1_fp8_m64"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16)
+        extra["c2_bf16_qkv_4096x9216x3072"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
+        extra["c1_fp8_64x3072x3072"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16)
     extra["calibration"] = calibration_copy(g)
     g.destroy()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -213,17 +229,19 @@ def main():
         line.update({"value": mlp["step_tflops"], "ms_per_step": mlp["ms_per_step"]})
         up = mlp["up"]
         line["roofline"] = {"bound": "mfma", "achieved": up["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                            "frac": up["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,
-                            "kernel": "gemm_kernel (fp8 weights, bf16 MFMA) up-projection 4096x12288x3072",
+                            "frac": up["tflops"] / PEAK_BF16_TFLOPS, "traffic": measured_traffic("gemm_fp8_up"),
+                            "kernel": "gemm_lds_kernel<256,256,2,4,bf16,fp8> up-projection 4096x12288x3072 "
+                                      "(+ fused GELU)",
                             "algorithmic": f"{up['flop']:.0f} FLOP per launch / {up['ms'] * 1e3:.1f} us"}
         line["up_proj_tflops"] = up["tflops"]
         line["down_proj_tflops"] = mlp["down"]["tflops"]
     if int4:
         line["int4_gemv"] = int4
-        best = int4["M1"]
-        line["roofline_int4"] = {"bound": "hbm", "achieved": best["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": best["gbs"] / PEAK_HBM_GBS, "traffic": None,
-                                 "kernel": "int4_gemv_kernel<F16> M=1 K=3584 N=18944"}
+        m1 = int4["M1"]
+        line["roofline_int4"] = {"bound": "hbm", "achieved": m1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": m1["gbs"] / PEAK_HBM_GBS, "traffic": measured_traffic("int4_decode_m1"),
+                                 "kernel": "int4_gemv_pipe_kernel<f16> M=1 K=3584 N=18944 group 64",
+                                 "algorithmic": f"{m1['bytes']} B per launch / {m1['us']:.2f} us"}
     line.update(extra)
     if cpu:
         line["cpu_baseline"] = cpu

@@ -384,9 +384,7 @@ template <bool IS_F16, int BT>
 static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg, hipStream_t s) {
   constexpr bool B8 = BT == FP8;
   switch (cfg) {
-    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 4, 2, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
-    case 5: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
-    case 6: return launch_fast_cfg<256, 256, 2, 2, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
+    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
     case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);
@@ -432,7 +430,11 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
                  ((uint64_t)L.y_stride * yb) % (4 * yb) == 0)
                     ? 1u
                     : 0u;
-  const int cfg = L.cfg >= 0 ? L.cfg : pick_gemm_cfg(L.m, L.n, splits);
+  // Tile choice measured on MI355X at M = 4096: fp8 weights run best on 256 x 256 tiles (also for
+  // N = 3072, where 192 tiles leave CUs idle but each tile streams K = 12288 at full rate); 16-bit
+  // weights need twice the LDS per stage and run best on 256 x 128.
+  int cfg = L.cfg >= 0 ? L.cfg : pick_gemm_cfg(L.m, L.n, splits);
+  if (L.cfg < 0 && L.m >= 256 && L.n >= 256) cfg = L.w_dtype == FP8 ? GEMM_CFG_256x256 : GEMM_CFG_256x128;
   if (f16) {
     if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, stream);
     return launch_fast_types<true, F16>(a, splits, cfg, stream);
