@@ -230,8 +230,8 @@ def main():
         up = mlp["up"]
         line["roofline"] = {"bound": "mfma", "achieved": up["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                             "frac": up["tflops"] / PEAK_BF16_TFLOPS, "traffic": measured_traffic("gemm_fp8_up"),
-                            "kernel": "gemm_lds_kernel<256,256,2,4,bf16,fp8> up-projection 4096x12288x3072 "
-                                      "(+ fused GELU)",
+                            "kernel": "gemm_lds_kernel<256,256,2,4,bf16,fp8, ping-pong> up-projection "
+                                      "4096x12288x3072 (+ fused GELU)",
                             "algorithmic": f"{up['flop']:.0f} FLOP per launch / {up['ms'] * 1e3:.1f} us"}
         line["up_proj_tflops"] = up["tflops"]
         line["down_proj_tflops"] = mlp["down"]["tflops"]

@@ -8,9 +8,12 @@
 //    The source address of each lane is chosen so that the LDS image is XOR-swizzled: 16-byte chunk c of
 //    row r sits at chunk position c ^ swz(r), which makes the MFMA fragment reads bank-conflict free.
 //    Rows past M / N and k past the slice read through an out-of-range buffer offset and land as zeros.
-//  * Loads run S - 1 stages ahead of the MFMAs. One workgroup barrier per 64-k block, placed before the
-//    last MFMA step of the block: after it the block's stage is free for the load S blocks ahead, and the
-//    next block's stage is complete, so its first fragments are read while the last MFMAs still run.
+//  * Loads run S - 1 stages ahead of the MFMAs. The 256 x 256 tiles (8 waves, two per SIMD) use a
+//    ping-pong schedule: the two waves of a SIMD alternate between a phase of MFMAs only and a phase of
+//    fragment reads / unpack / loads, one phase apart, separated by workgroup barriers (details at the
+//    loop). Smaller tiles use one workgroup barrier per 64-k block, placed before the last MFMA step of
+//    the block: after it the block's stage is free for the load S blocks ahead, and the next block's
+//    stage is complete, so its first fragments are read while the last MFMAs still run.
 //  * The weight tile is the MFMA's A operand and the activation tile its B operand, so the fp32
 //    accumulators hold runs of 4 consecutive output columns per lane: the epilogue stores 8 or 16 bytes
 //    per lane instead of 2.
@@ -119,7 +122,7 @@ __device__ __forceinline__ void store1(const FastArgs& a, size_t o, float v, boo
 
 }  // namespace
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool IS_F16, int BT, int S, int YT>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool IS_F16, int BT, int S, int YT, bool PP>
 __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArgs a) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -138,7 +141,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   constexpr int B_CPR = B_ROW / 16;                                       // 16-B chunks per weight row
   __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int h = lane >> 5, l32 = lane & 31;
 
@@ -234,7 +237,84 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     for (int j = 0; j < TN; j++) d[j] = rd(st_off + rdb[q] + j * 32 * B_ROW);
   };
 
-  if (nk > 0) {
+  if constexpr (PP) {
+    // ---- ping-pong schedule. Waves w and w + NW / 2 share a SIMD (waves of a workgroup go round-robin
+    // over the 4 SIMDs); group grp = w / (NW / 2). Each wave alternates a memory phase (all fragment
+    // reads of one 64-k block, and the loads of the block S - 1 ahead) with a compute phase (the block's
+    // 4 x TM x TN MFMAs, the fp8 unpack interleaved between them). Group 1 runs one phase behind group 0,
+    // so in every interval between two workgroup barriers one wave of each SIMD issues MFMAs while the
+    // other prepares its next operands: the MFMA pipe does not wait on LDS latency or on a barrier that
+    // both waves of the SIMD sit at.
+    // Interval j: group 0 runs phase j (even = memory of block j / 2, odd = compute), group 1 phase
+    // j - 1. Block t is first read in interval 2t (group 0), so every wave waits for its own loads of
+    // block t before the barrier that ends interval 2t - 1. The loads of block t + S - 1 go into the stage
+    // of block t - 1, whose last read (group 1) was in interval 2t - 1, and are issued at the start of the
+    // memory phase of block t: interval 2t or 2t + 1.
+    static_assert(NW % 2 == 0 && S >= 2, "ping-pong needs two wave groups");
+    const int grp = wave / (NW / 2);
+    u32x4 xb[4][TM];                // x fragments of the 4 MFMA steps of a block
+    u32x4 wb[B8 ? 2 : 4][TN];       // fp8: raw 16-byte chunks (2 steps each); 16-bit: fragments per step
+    auto pp_barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto memory_block = [&](uint32_t st_off) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) read_x(st_off, q, xb[q]);
+#pragma unroll
+      for (int q = 0; q < (B8 ? 2 : 4); q++) read_w(st_off, q, wb[q]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    auto compute_block = [&]() {
+      static_for<0, 4>([&](auto Q) {
+        constexpr int q = decltype(Q)::value;
+        u32x4 w[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          if constexpr (B8) {
+            const u32x4 r = wb[q >> 1][j];
+            const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
+            w[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          } else {
+            w[j] = wb[q][j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(w[j], xb[q][i], acc[i][j]);
+      });
+    };
+    // own loads of block t + 1 complete; blocks issued after it (up to S - 2 of them) may be in flight
+    auto wait_next = [&](int t) {
+      if (t + 1 >= nk) return;
+      if (S >= 3 && t + 2 < nk) wait_vmcnt<(S >= 3 ? (S - 2) * L : 0)>();
+      else wait_vmcnt<0>();
+    };
+    if (nk > 0) {
+#pragma unroll
+      for (int p = 0; p < S - 1; p++)
+        if (p < nk) issue(k_begin + (uint32_t)p * BK, p);
+      if (S >= 3 && nk >= 2) wait_vmcnt<(S >= 3 ? (S - 2) * L : 0)>();
+      else wait_vmcnt<0>();
+      lds_barrier();
+      if (grp == 1) pp_barrier();  // group 1 sits out interval 0
+      int cur = 0;
+      for (int t = 0; t < nk; ++t) {
+        const uint32_t cur_off = (uint32_t)(cur * STAGE);
+        const int ahead = cur + S - 1 >= S ? cur - 1 : cur + S - 1;  // stage of block t + S - 1
+        if (t + S - 1 < nk) issue(k_begin + (uint32_t)(t + S - 1) * BK, ahead);
+        memory_block(cur_off);
+        wait_next(t);
+        pp_barrier();
+        compute_block();
+        wait_next(t);
+        if (!(grp == 1 && t + 1 == nk)) pp_barrier();  // both groups pass the same number of barriers
+        cur = cur + 1 == S ? 0 : cur + 1;
+      }
+    }
+  } else if (nk > 0) {
     // prologue: the first S blocks (or all of them)
 #pragma unroll
     for (int p = 0; p < S; p++)
@@ -367,15 +447,15 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S>
+template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S, bool PP = false>
 static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
   a.tiles_n = (a.n + BN - 1) / BN;
   const dim3 grid(a.tiles_m * a.tiles_n, splits), block(WM * WN * 64);
   switch (a.y_dtype) {
-    case F32: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32>), grid, block, 0, s, a); break;
-    case F16: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F16>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, BF16>), grid, block, 0, s, a); break;
+    case F32: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32, PP>), grid, block, 0, s, a); break;
+    case F16: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F16, PP>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, BF16, PP>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }
@@ -384,7 +464,9 @@ template <bool IS_F16, int BT>
 static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg, hipStream_t s) {
   constexpr bool B8 = BT == FP8;
   switch (cfg) {
-    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2>(a, splits, s);
+    // ping-pong schedule, 2 x 4 waves (128 x 64 each): measured on MI355X the fastest layout for fp8
+    // and 16-bit weights
+    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, s);
     case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);
@@ -430,11 +512,11 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
                  ((uint64_t)L.y_stride * yb) % (4 * yb) == 0)
                     ? 1u
                     : 0u;
-  // Tile choice measured on MI355X at M = 4096: fp8 weights run best on 256 x 256 tiles (also for
-  // N = 3072, where 192 tiles leave CUs idle but each tile streams K = 12288 at full rate); 16-bit
-  // weights need twice the LDS per stage and run best on 256 x 128.
+  // Tile choice measured on MI355X at M = 4096: 256 x 256 tiles with the ping-pong schedule, for fp8 and
+  // 16-bit weights alike (also for N = 3072, where 192 tiles leave CUs idle but each tile streams
+  // K = 12288 at full rate).
   int cfg = L.cfg >= 0 ? L.cfg : pick_gemm_cfg(L.m, L.n, splits);
-  if (L.cfg < 0 && L.m >= 256 && L.n >= 256) cfg = L.w_dtype == FP8 ? GEMM_CFG_256x256 : GEMM_CFG_256x128;
+  if (L.cfg < 0 && L.m >= 256 && L.n >= 256) cfg = GEMM_CFG_256x256;
   if (f16) {
     if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, stream);
     return launch_fast_types<true, F16>(a, splits, cfg, stream);
