@@ -64,7 +64,7 @@ typedef struct we_matmul_params {
 /* ---- context: replaces getDevice (src/gpu/compute.ts:6-20) and the Graph object (src/gpu/graph.ts:26-35) ---- */
 int we_ctx_create(int device, we_ctx** out);
 int we_ctx_destroy(we_ctx* ctx);
-const char* we_last_error(const we_ctx* ctx);
+const char* we_last_error(const we_ctx* ctx); /* ctx = NULL: the last context-free failure of this thread */
 /* device name, compute-unit count, LDS bytes per workgroup (for reports) */
 int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units, int* lds_bytes);
 

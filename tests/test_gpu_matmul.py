@@ -267,3 +267,86 @@ def test_full_size_sampled_rows(graph, name, m, n, k, w_dt):
     xs = O.bf16_to_f32(x).astype(np.float64).reshape(m, k)
     want_sum = xs @ wdec.sum(0) * scale
     assert np.abs(got.sum(1) - want_sum).max() < 1e-4 * np.abs(want_sum).max() + 1e-3
+
+
+# ------------------------------------------------------------------ LoRA through linear() (tests/gpu/lora.test.ts)
+
+def rms_rel(got, want):
+    """src/model/compare.ts:2-17 relativeError: sqrt(sum (a - b)^2 / sum b^2)."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.sqrt(((got - want) ** 2).sum() / (want ** 2).sum()))
+
+
+class LcgDraws:
+    """tests/gpu/lora.test.ts:12-21: one LCG stream; floats in [-1, 1) as f32, bf16 as the top half of such
+    a float (truncated), fp8 bytes floor((r + 1) * 60) (no NaN codes)."""
+
+    def __init__(self, seed, total):
+        self.u, self.i = O.lcg(seed, total), 0
+
+    def _take(self, n):
+        u = self.u[self.i:self.i + n]
+        self.i += n
+        assert u.size == n
+        return u
+
+    def floats(self, n):
+        return (self._take(n) * 2 - 1).astype(np.float32)
+
+    def bf16(self, n):
+        bits = (self.floats(n).view(np.uint32) >> 16).astype(np.uint16)
+        return bits, O.bf16_to_f32(bits).astype(np.float64)
+
+    def fp8(self, n):
+        return np.floor(self._take(n) * 120).astype(np.uint8)
+
+
+def lora_reference(x, w, w_scale, down, up, s, m, n, k, r):
+    """tests/gpu/lora.test.ts:23-38 in float64."""
+    x = x.astype(np.float64).reshape(m, k)
+    t = x @ down.reshape(r, k).T
+    return ((x @ w.reshape(n, k).T) * w_scale + s * (t @ up.reshape(n, r).T)).ravel()
+
+
+def test_lora_on_fp8_linear_bf16_and_f32_weights(graph):  # tests/gpu/lora.test.ts:40-78
+    m, n, k, r, s = 5, 12, 16, 4, 0.8 * 0.5
+    d = LcgDraws(7, m * k + n * k + r * k + n * r)
+    x, w = d.floats(m * k), d.fp8(n * k)
+    (down_b, down_v), (up_b, up_v) = d.bf16(r * k), d.bf16(n * r)
+    mark = graph.mark()
+    base = we.Linear(graph.buffer(w), "fp8", 0.25, n, k)
+    lora_bf = (we.Linear(graph.buffer(down_b), "bf16", 1.0, r, k), we.Linear(graph.buffer(up_b), "bf16", s, n, r))
+    lora_f32 = (we.Linear(graph.buffer(down_v.astype(np.float32)), "f32", 1.0, r, k),
+                we.Linear(graph.buffer(up_v.astype(np.float32)), "f32", s, n, r))
+    want = lora_reference(x, O.e4m3_table()[w], 0.25, down_v, up_v, s, m, n, k, r)
+    for lora in (lora_bf, lora_f32):
+        lin = we.Linear(base.buffer, "fp8", 0.25, n, k, lora=lora)
+        got = graph.read(we.linear(graph, graph.buffer(x), lin, m), dtype=np.float32, count=m * n)
+        assert rms_rel(got, want) < 1e-6
+    plain = graph.read(we.linear(graph, graph.buffer(x), base, m), dtype=np.float32, count=m * n)
+    assert rms_rel(plain, want) > 1e-3  # the update is really there
+    graph.release(mark)
+
+
+def test_lora_rank_not_multiple_of_4_is_rejected(graph):  # tests/gpu/lora.test.ts:80-89
+    mark = graph.mark()
+    lin = lambda n, k, scale=1.0: we.Linear(graph.buffer(n * k * 4), "f32", scale, n, k)  # noqa: E731
+    w = lin(8, 8)
+    w.lora = (lin(3, 8), lin(8, 3))
+    with pytest.raises(we.WeError, match="LoRA shapes do not fit the linear layer"):
+        we.linear(graph, graph.buffer(8 * 4), w, 1)
+    graph.release(mark)
+
+
+def test_lora_down_split_over_long_k(graph):  # tests/gpu/lora.test.ts:120-146
+    m, n, k, r, s = 5, 8, 1024, 4, 0.3
+    assert we.k_split_for(m, r, k) == 4
+    d = LcgDraws(11, m * k + n * k + r * k + n * r)
+    x = d.floats(m * k)
+    (w_b, w_v), (down_b, down_v), (up_b, up_v) = d.bf16(n * k), d.bf16(r * k), d.bf16(n * r)
+    mark = graph.mark()
+    lora = (we.Linear(graph.buffer(down_b), "bf16", 1.0, r, k), we.Linear(graph.buffer(up_b), "bf16", s, n, r))
+    lin = we.Linear(graph.buffer(w_b), "bf16", 1.0, n, k, lora=lora)
+    got = graph.read(we.linear(graph, graph.buffer(x), lin, m), dtype=np.float32, count=m * n)
+    assert rms_rel(got, lora_reference(x, w_v, 1.0, down_v, up_v, s, m, n, k, r)) < 1e-6
+    graph.release(mark)

@@ -1,0 +1,219 @@
+"""The Node N-API addon (web-engine_amd/node): the binding a TypeScript host of the reference uses.
+
+CPU: the addon loads under `node`, exports one function per entry point of include/we.h, and its host logic
+(matmulParams image and messages, kSplitFor) equals the oracle's.
+GPU: tests/node_driver.js runs linear (fp8 + bias, fp8 + GELU, fp8 + LoRA, int4), norm, rotate, the
+elementwise ops and a pinned-host stream copy through the addon; the results are checked here against the
+oracle with the bars of the matching C-ABI tests (test_gpu_matmul, test_gpu_int4, test_gpu_norm_rope,
+test_gpu_elementwise)."""
+import json
+import pathlib
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import we
+from test_gpu_matmul import LcgDraws, lora_reference, rms_rel
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+NODE_DIR = ROOT / "web-engine_amd" / "node"
+ADDON = NODE_DIR / "we_node.node"
+NODE = shutil.which("node")
+
+pytestmark = pytest.mark.skipif(NODE is None or not ADDON.exists(),
+                                reason="node or the built addon (web-engine_amd/node/we_node.node) is missing")
+
+# include/we.h entry point -> addon export
+EXPORTS = {
+    "we_ctx_create": "create", "we_ctx_destroy": "destroy", "we_device_info": "deviceInfo", "we_sync": "sync",
+    "we_buf_alloc": "bufAlloc", "we_buf_free": "bufFree", "we_buf_upload": "upload", "we_buf_download": "download",
+    "we_buf_copy": "copy", "we_mark": "mark", "we_release": "release", "we_stats": "stats",
+    "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_stream_copy": "streamCopy",
+    "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
+    "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
+    "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_rmsnorm": "rmsnorm", "we_rope": "rope",
+    "we_qk_norm_rope": "qkNormRope", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
+    "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
+}
+
+
+def node_eval(script, timeout=60):
+    out = subprocess.run([NODE, "-e", script], cwd=NODE_DIR, capture_output=True, text=True, timeout=timeout)
+    assert out.returncode == 0, out.stderr
+    return json.loads(out.stdout)
+
+
+def test_addon_exports_every_entry_point():
+    assert set(EXPORTS) == set(we.header_functions())
+    keys = node_eval('console.log(JSON.stringify(Object.keys(require("./we_node.node"))))')
+    assert set(EXPORTS.values()) <= set(keys)
+
+
+LAYOUTS = [
+    dict(m=3, n=5, k=8, scale=0.25),
+    dict(m=20, n=20, k=128, scale=1.0, xStride=512, xOffset=256, wStride=256, wOffset=128, yStride=24),
+    dict(m=5, n=12, k=200, scale=0.5, kSplit=3),
+    dict(m=1, n=1, k=6, scale=1.0),
+    dict(m=1, n=1, k=4, scale=1.0, xStride=6),
+    dict(m=1, n=1, k=4, scale=1.0, wStride=10),
+    dict(m=1, n=1, k=4, scale=1.0, xOffset=1),
+    dict(m=1, n=1, k=4, scale=1.0, wOffset=2),
+]
+
+
+def test_matmul_params_image_and_messages_match_the_oracle():  # src/kernels/matmul.ts:198-212
+    script = f"""
+const we = require("./index.js");
+const out = {json.dumps(LAYOUTS)}.map((l) => {{
+  try {{ return Array.from(we.matmulParams({{ m: l.m, n: l.n, k: l.k }}, l.scale, l)); }}
+  catch (e) {{ return e.message; }}
+}});
+console.log(JSON.stringify(out));"""
+    got = node_eval(script)
+    names = dict(xStride="x_stride", wStride="w_stride", yStride="y_stride", xOffset="x_offset", wOffset="w_offset",
+                 yOffset="y_offset", kSplit="k_split")
+    for layout, g in zip(LAYOUTS, got):
+        kw = {names[key]: v for key, v in layout.items() if key in names}
+        try:
+            p = O.matmul_params(layout["m"], layout["n"], layout["k"], layout["scale"], **kw)
+        except ValueError as e:
+            assert g == str(e), (layout, g)
+            continue
+        assert np.frombuffer(bytes(p), np.uint32).tolist() == g, layout
+
+
+def test_ksplit_for_matches_the_oracle():  # src/model/ops.ts:42-45
+    grid = [(m, n, k) for m in (1, 5, 64, 1088, 4160) for n in (4, 64, 300) for k in (64, 1024, 6144, 16384)]
+    got = node_eval(f'const a = require("./we_node.node"); '
+                    f'console.log(JSON.stringify({json.dumps(grid)}.map(([m, n, k]) => a.kSplitFor(m, n, k))))')
+    assert got == [O.ksplit_for(m, n, k) for m, n, k in grid]
+    assert got[grid.index((1088, 64, 6144))] == 24 and got[grid.index((4160, 64, 16384))] == 8
+
+
+def test_context_free_errors_throw_with_the_message():
+    got = node_eval('const a = require("./we_node.node"); const r = [];'
+                    'try { a.matmul(null, new Uint32Array(13), 0, null, 3, null, null, 0, 0, null, null, 0); }'
+                    'catch (e) { r.push(e.message); }'
+                    'try { a.bufAlloc(null, 16); } catch (e) { r.push(e.message); }'
+                    'console.log(JSON.stringify(r));')
+    assert got == ["context is null", "context is null"]
+
+
+# ------------------------------------------------------------------------------------------------ GPU
+
+def _write(tmp, name, arr):
+    np.ascontiguousarray(arr).tofile(tmp / name)
+    return name
+
+
+@pytest.mark.gpu
+def test_graph_steps_through_the_addon(tmp_path):
+    cases, checks = [], {}
+    # fp8 linear + fused bias (tests/gpu/matmul.test.ts shapes; bias as ops.ts:65)
+    m, n, k = 37, 70, 100
+    x, w = O.matmul_test_data(m, n, k, 1)
+    bias = ((O.lcg(5, n) - 0.5) * 4).astype(np.float32)
+    base = O.matmul(O.matmul_params(m, n, k, 0.002), O.F32, x, O.FP8, w) + np.tile(bias.astype(np.float64), m)
+    wspec = dict(file=_write(tmp_path, "w8", w), dtype="fp8", scale=0.002, n=n, k=k, bias=_write(tmp_path, "b", bias))
+    cases.append(dict(name="fp8_bias", op="linear", m=m, x=_write(tmp_path, "x", x), xDtype=we.F32,
+                      yDtype=we.F32, w=wspec))
+    checks["fp8_bias"] = (np.float32, lambda g: O.rel_error(g, base) < 1e-5)
+    gel = np.array([O.lib.or_gelu_tanh(v) for v in base])
+    cases.append(dict(cases[-1], name="fp8_gelu", geluTanh=True))
+    checks["fp8_gelu"] = (np.float32, lambda g: np.abs(g - gel).max() < 1e-4 * np.abs(gel).max())
+
+    # LoRA on an fp8 linear (tests/gpu/lora.test.ts:40-78)
+    m2, n2, k2, r, s = 5, 12, 16, 4, 0.4
+    d = LcgDraws(7, m2 * k2 + n2 * k2 + r * k2 + n2 * r)
+    x2, w2 = d.floats(m2 * k2), d.fp8(n2 * k2)
+    (db, dv), (ub, uv) = d.bf16(r * k2), d.bf16(n2 * r)
+    lora_want = lora_reference(x2, O.e4m3_table()[w2], 0.25, dv, uv, s, m2, n2, k2, r)
+    lora = dict(down=dict(file=_write(tmp_path, "down", db), dtype="bf16", scale=1.0, n=r, k=k2),
+                up=dict(file=_write(tmp_path, "up", ub), dtype="bf16", scale=s, n=n2, k=r))
+    cases.append(dict(name="lora", op="linear", m=m2, x=_write(tmp_path, "x2", x2), xDtype=we.F32, yDtype=we.F32,
+                      w=dict(file=_write(tmp_path, "w2", w2), dtype="fp8", scale=0.25, n=n2, k=k2, lora=lora)))
+    checks["lora"] = (np.float32, lambda g: rms_rel(g, lora_want) < 1e-6)
+    bad = dict(down=dict(lora["down"], n=3), up=dict(lora["up"], k=3))
+    cases.append(dict(cases[-1], name="lora_rank3", expectError=True, w=dict(cases[-1]["w"], lora=bad)))
+
+    # int4 weights, f16 activations, ragged N (the additive int4 format)
+    m3, n3, k3, group = 3, 33, 192, 64
+    rng = np.random.default_rng(3)
+    words = rng.integers(0, 2 ** 32, n3 * k3 // 8, dtype=np.uint64).astype(np.uint32)
+    scales = np.abs(rng.normal(0, 0.01, n3 * k3 // group)).astype(np.float16).view(np.uint16)
+    x3 = rng.standard_normal(m3 * k3).astype(np.float16).view(np.uint16)
+    i4_want = O.matmul(O.matmul_params(m3, n3, k3, 1.0), O.F16, x3, O.INT4, words, scales=scales, group=group)
+    cases.append(dict(name="int4", op="linear", m=m3, x=_write(tmp_path, "x3", x3), xDtype=we.F16, yDtype=we.F32,
+                      w=dict(file=_write(tmp_path, "w4", words), dtype="int4", scale=1.0, n=n3, k=k3,
+                             scales=_write(tmp_path, "s4", scales), group=group)))
+    checks["int4"] = (np.float32, lambda g: O.rel_error(g, i4_want) < 1e-5)
+
+    # norm with modulation (tests/gpu/rmsnorm.test.ts:25-31)
+    dn = 6144
+    u = O.lcg(1, 6 * dn)
+    xn = ((u[: 3 * dn] - 0.5) * 8).astype(np.float32)
+    wn = ((u[3 * dn: 4 * dn] - 0.5) * 0.2).astype(np.float32)
+    sc = ((u[4 * dn: 5 * dn] - 0.5) * 2).astype(np.float32)
+    sh = ((u[5 * dn:] - 0.5) * 2).astype(np.float32)
+    norm_want = O.rmsnorm(xn, wn, 1e-5, 1.0, sc, sh)
+    cases.append(dict(name="norm", op="norm", rows=3, d=dn, eps=1e-5, offset=1.0, x=_write(tmp_path, "xn", xn),
+                      weight=_write(tmp_path, "wn", wn), scale=_write(tmp_path, "sc", sc),
+                      shift=_write(tmp_path, "sh", sh)))
+    checks["norm"] = (np.float32, lambda g: np.abs(g - norm_want).max() < 1e-5)
+
+    # rotate, interleaved pairs over three axes (tests/gpu/rope.test.ts:5-22)
+    heads = 3
+    pos = O.rope_positions(2, 3, 4, 3)
+    cos, sin, pairs = O.rope_tables(pos, [32, 48, 48], 1000.0)
+    tokens = pos.shape[0]
+    xr = (O.lcg(1, tokens * heads * 128) * 2 - 1).astype(np.float32)
+    rope_want = O.rope_rotate(xr, tokens, heads, pairs, cos, sin)
+    cases.append(dict(name="rotate", op="rotate", tokens=tokens, heads=heads, pairs=pairs, pairing="interleaved",
+                      x=_write(tmp_path, "xr", xr), cos=_write(tmp_path, "cos", np.asarray(cos, np.float32)),
+                      sin=_write(tmp_path, "sin", np.asarray(sin, np.float32))))
+    checks["rotate"] = (np.float32, lambda g: np.abs(g - rope_want).max() < 1e-6)
+
+    # elementwise (tests/gpu/elementwise.test.ts:15-40)
+    ne, de = 1000, 40
+    a = ((O.lcg(1, ne) - 0.5) * 16).astype(np.float32)
+    b = ((O.lcg(2, ne) - 0.5) * 16).astype(np.float32)
+    gg = ((O.lcg(7, de) - 0.5) * 2).astype(np.float32)
+    fa, fb, fg = _write(tmp_path, "ea", a), _write(tmp_path, "eb", b), _write(tmp_path, "eg", gg)
+    for fn, inputs, sizes, want, tol in [
+        ("swiglu", [fa, fb], [ne], O.elementwise(O.SWIGLU, a, b), 1e-4),
+        ("sigmoidGate", [fa, fb], [ne], O.elementwise(O.SIGMOID_GATE, a, b), 1e-5),
+        ("gatedAdd", [fa, fb, fg], [ne, de], O.elementwise(O.GATED_ADD, a, b, gg, de), 1e-5),
+        ("addBias", [fa, fg], [ne, de], O.elementwise(O.ADD_BIAS, a, gg, d=de), 1e-6),
+        ("add", [fa, fb], [ne], O.elementwise(O.ADD, a, b), 1e-6),
+        ("gelu", [fa], [ne], O.elementwise(O.GELU_TANH, a), 1e-5),
+        ("silu", [fa], [ne], O.elementwise(O.SILU, a), 1e-5),
+    ]:
+        cases.append(dict(name=fn, op="elementwise", fn=fn, inputs=inputs, sizes=sizes))
+        checks[fn] = (np.float32, lambda g, want=want, tol=tol: np.abs(g - want).max() <= tol)
+
+    # pinned host memory -> device over the copy stream (src/model/weights.ts:124-129)
+    blob = np.random.default_rng(9).integers(0, 256, (1 << 20) + 12, dtype=np.uint8)
+    cases.append(dict(name="stream", op="stream", x=_write(tmp_path, "blob", blob)))
+    checks["stream"] = (np.uint8, lambda g: np.array_equal(g, blob))
+
+    (tmp_path / "spec.json").write_text(json.dumps(dict(cases=cases)))
+    print(f"[node] {len(cases)} cases in {tmp_path}", flush=True)
+    out = subprocess.run([NODE, str(ROOT / "tests" / "node_driver.js"), str(tmp_path)], capture_output=True,
+                         text=True, timeout=100)
+    print(out.stdout[-2000:], out.stderr[-2000:], flush=True)
+    assert out.returncode == 0
+    result = json.loads((tmp_path / "result.json").read_text())
+    assert result["device"]["arch"].startswith("gfx950")
+    assert result["errors"] == {"lora_rank3": "LoRA shapes do not fit the linear layer"}
+    assert result["reusedDelta"] >= 1 and result["zeroed"]
+    failed = []
+    for name, (dtype, ok) in checks.items():
+        got = np.fromfile(tmp_path / f"{name}.out", dtype)
+        if dtype == np.float32:
+            got = got.astype(np.float64)
+        if not ok(got):
+            failed.append(name)
+    assert not failed, failed

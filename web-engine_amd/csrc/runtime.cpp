@@ -44,6 +44,9 @@ struct we_ctx {
 
 namespace {
 
+// message of the last failed call made without a context (e.g. we_matmul_params_make(NULL, ...)), per thread
+thread_local std::string g_no_ctx_err = "no context";
+
 int fail(we_ctx* ctx, int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -51,6 +54,7 @@ int fail(we_ctx* ctx, int code, const char* fmt, ...) {
   vsnprintf(buf, sizeof buf, fmt, ap);
   va_end(ap);
   if (ctx) ctx->err = buf;
+  else g_no_ctx_err = buf;
   return code;
 }
 
@@ -116,16 +120,16 @@ int ticket_valid(we_ctx* ctx, uint64_t t) {
 extern "C" {
 
 int we_ctx_create(int device, we_ctx** out) {
-  if (!out) return WE_EINVAL;
+  if (!out) return fail(nullptr, WE_EINVAL, "output pointer is null");
   *out = nullptr;
   int count = 0;
-  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return WE_EHIP;
-  if (device < 0 || device >= count) return WE_EINVAL;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return fail(nullptr, WE_EHIP, "no HIP device is visible");
+  if (device < 0 || device >= count) return fail(nullptr, WE_EINVAL, "device %d out of range (%d visible)", device, count);
   we_ctx* ctx = new we_ctx();
   ctx->device = device;
   auto cleanup = [&](int code) {
     we_ctx_destroy(ctx);
-    return code;
+    return fail(nullptr, code, "HIP set-up of device %d failed", device);
   };
   if (hipSetDevice(device) != hipSuccess) return cleanup(WE_EHIP);
   if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return cleanup(WE_EHIP);
@@ -156,10 +160,10 @@ int we_ctx_destroy(we_ctx* ctx) {
   return WE_OK;
 }
 
-const char* we_last_error(const we_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+const char* we_last_error(const we_ctx* ctx) { return ctx ? ctx->err.c_str() : g_no_ctx_err.c_str(); }
 
 int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units, int* lds_bytes) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (name && name_len) snprintf(name, name_len, "%s", ctx->prop.gcnArchName);
   if (compute_units) *compute_units = ctx->prop.multiProcessorCount;
   if (lds_bytes) *lds_bytes = (int)ctx->prop.sharedMemPerBlock;
@@ -196,7 +200,7 @@ int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
 }
 
 int we_buf_free(we_ctx* ctx, void* buf) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   auto it = ctx->allocs.find((uintptr_t)buf);
   if (it == ctx->allocs.end()) return fail(ctx, WE_EINVAL, "we_buf_free: not a buffer of this context");
   for (size_t i = 0; i < ctx->owned.size(); i++)
@@ -209,7 +213,7 @@ int we_buf_free(we_ctx* ctx, void* buf) {
 }
 
 int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t bytes) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (bytes == 0) return WE_OK;
   if (!src) return fail(ctx, WE_EINVAL, "upload source is null");
   int rc = check_span(ctx, (char*)buf + offset, bytes, "upload destination");
@@ -221,7 +225,7 @@ int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t
 }
 
 int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size_t bytes) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (bytes == 0) return WE_OK;
   if (!dst) return fail(ctx, WE_EINVAL, "download destination is null");
   int rc = check_span(ctx, (const char*)buf + offset, bytes, "download source");
@@ -233,7 +237,7 @@ int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size
 }
 
 int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (bytes == 0) return WE_OK;
   int rc = check_span(ctx, (const char*)src + src_offset, bytes, "copy source");
   if (!rc) rc = check_span(ctx, (char*)dst + dst_offset, bytes, "copy destination");
@@ -251,7 +255,7 @@ int we_mark(we_ctx* ctx, size_t* mark) {
 }
 
 int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (mark > ctx->owned.size()) return fail(ctx, WE_EINVAL, "mark %zu is past the %zu live buffers", mark, ctx->owned.size());
   std::vector<void*> later(ctx->owned.begin() + (long)mark, ctx->owned.end());
   ctx->owned.resize(mark);
@@ -265,7 +269,7 @@ int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep) {
 }
 
 int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (created) *created = ctx->created;
   if (reused) *reused = ctx->reused;
   if (created_bytes) *created_bytes = ctx->created_bytes;
@@ -273,7 +277,7 @@ int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created
 }
 
 int we_sync(we_ctx* ctx) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
   HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "compute stream");
@@ -293,7 +297,7 @@ int we_host_alloc(we_ctx* ctx, size_t bytes, void** out) {
 }
 
 int we_host_free(we_ctx* ctx, void* ptr) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   auto it = ctx->pinned.find((uintptr_t)ptr);
   if (it == ctx->pinned.end()) return fail(ctx, WE_EINVAL, "we_host_free: not pinned memory of this context");
   HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
@@ -322,7 +326,7 @@ int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes,
 }
 
 int we_wait_ticket(we_ctx* ctx, uint64_t ticket) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   int rc = ticket_valid(ctx, ticket);
   if (rc) return rc;
   HIP_OK(ctx, hipStreamWaitEvent(ctx->compute, ticket_event(ctx, ticket), 0), "hipStreamWaitEvent");
@@ -346,7 +350,7 @@ int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
 }
 
 int we_timer_start(we_ctx* ctx) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   HIP_OK(ctx, hipEventRecord(ctx->t0, ctx->compute), "hipEventRecord");
   return WE_OK;
 }
@@ -385,7 +389,7 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
 
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
   {
@@ -492,7 +496,7 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
 
 int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
                const float* weight, const float* scale, const float* shift, void* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "rmsnorm dtype %d is not f32 / f16 / bf16", dtype);
   const uint64_t n = (uint64_t)rows * d * elem_bytes(dtype);
   int rc = check_span(ctx, x, n, "x");
@@ -507,7 +511,7 @@ int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, 
 
 int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
             const float* cos_t, const float* sin_t, void* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "rope dtype %d is not f32 / f16 / bf16", dtype);
   const uint64_t n = (uint64_t)tokens * heads * pairs * 2 * elem_bytes(dtype);
   int rc = check_span(ctx, x, n, "x");
@@ -522,7 +526,7 @@ int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int ha
 int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                     const float* weight, uint32_t rope_from, int half, const float* cos_t, const float* sin_t,
                     int dtype, const void* x, void* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "dtype %d is not f32 / f16 / bf16", dtype);
   if (head_dim % 2 || head_dim == 0 || head_dim > 512)
     return fail(ctx, WE_EINVAL, "head_dim must be even and at most 512, got %u", head_dim);
@@ -541,7 +545,7 @@ int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_
 
 int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,
                    void* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "elementwise dtype %d is not f32 / f16 / bf16", dtype);
   if (op < WE_OP_SWIGLU || op > WE_OP_SILU) return fail(ctx, WE_EINVAL, "unknown elementwise op %d", op);
   const uint64_t bytes = (uint64_t)n * elem_bytes(dtype);
@@ -560,7 +564,7 @@ int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const voi
 
 int we_layer_sum(we_ctx* ctx, uint32_t tokens, uint32_t layers, uint32_t dim, const float* x, const float* w,
                  float* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   int rc = check_span(ctx, x, (uint64_t)tokens * layers * dim * 4, "x");
   if (!rc) rc = check_span(ctx, w, (uint64_t)layers * 4, "w");
   if (!rc) rc = check_span(ctx, out, (uint64_t)tokens * dim * 4, "out");
@@ -570,7 +574,7 @@ int we_layer_sum(we_ctx* ctx, uint32_t tokens, uint32_t layers, uint32_t dim, co
 }
 
 int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale, float* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   int rc = check_span(ctx, packed, n, "packed");
   if (!rc) rc = check_span(ctx, scale, 4, "scale");
   if (!rc) rc = check_span(ctx, out, (uint64_t)n * 4, "out");
@@ -581,7 +585,7 @@ int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale,
 
 int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, uint32_t rows, uint32_t k,
                     uint32_t group, float* out) {
-  if (!ctx) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (k % 8 || group == 0 || k % group) return fail(ctx, WE_EINVAL, "K must be a multiple of 8 and of the group size");
   int rc = check_span(ctx, words, (uint64_t)rows * k / 2, "words");
   if (!rc) rc = check_span(ctx, scales, (uint64_t)rows * (k / group) * 2, "scales");

@@ -1,0 +1,221 @@
+"use strict";
+/*
+ * CommonJS glue over we_node.node: a Graph with the method names of the reference's WebGPU Graph
+ * (src/gpu/graph.ts:26-160) and the graph steps of src/model/ops.ts, running on the MI355X kernels of libwe.so.
+ * A buffer is { ptr: BigInt, size: number } in place of a GPUBuffer; Graph.slice gives a binding into one.
+ */
+const addon = require("./we_node.node");
+
+const F32 = 0, F16 = 1, BF16 = 2, FP8 = 3, INT4 = 4;
+const DTYPES = { f32: F32, f16: F16, bf16: BF16, fp8: FP8, int4: INT4 };
+const ELEM_BYTES = { [F32]: 4, [F16]: 2, [BF16]: 2, [FP8]: 1 };
+const EPI = { ACCUMULATE: 1, SPLIT_K: 2, BIAS: 4, GELU_TANH: 8 };
+const OP = { SWIGLU: 0, SIGMOID_GATE: 1, GATED_ADD: 2, ADD_BIAS: 3, GELU_TANH: 4, ADD: 5, SILU: 6 };
+
+const ptrOf = (b) => (b == null ? null : typeof b === "bigint" ? b : b.ptr);
+
+class Graph {
+  /** src/gpu/graph.ts:35: one context (device, streams, pool) per graph. */
+  constructor(device = 0) {
+    this.ctx = addon.create(device);
+  }
+
+  /** src/gpu/graph.ts:38-54: a device buffer with this data, or zeroed with this many bytes (pooled by size). */
+  buffer(data) {
+    const bytes = typeof data === "number" ? data : data.byteLength;
+    const size = Math.max(4, Math.ceil(bytes / 4) * 4);
+    const ptr = addon.bufAlloc(this.ctx, size);
+    if (typeof data !== "number" && data.byteLength) addon.upload(this.ctx, ptr, 0, data);
+    return { ptr, size };
+  }
+
+  /** src/gpu/graph.ts:57-60 */
+  static slice(buffer, offset, size) {
+    return { ptr: buffer.ptr + BigInt(offset), size };
+  }
+
+  /** Work is queued on the context's stream as it is issued; nothing is held back. */
+  submit() {}
+
+  /** src/gpu/graph.ts:109-119: runs everything queued, then copies `bytes` of `buffer` back. */
+  async read(buffer, bytes = buffer.size) {
+    return addon.download(this.ctx, buffer.ptr, 0, bytes);
+  }
+
+  copy(src, srcOffset, dst, dstOffset, size) {
+    addon.copy(this.ctx, src.ptr, srcOffset, dst.ptr, dstOffset, size);
+  }
+
+  mark() {
+    return addon.mark(this.ctx);
+  }
+
+  release(mark, keep = []) {
+    addon.release(this.ctx, mark, keep.map((b) => b.ptr));
+  }
+
+  free(buffer) {
+    addon.bufFree(this.ctx, buffer.ptr);
+  }
+
+  /** src/gpu/graph.ts:32: buffers created vs taken from the pool, and bytes created. */
+  get stats() {
+    return addon.stats(this.ctx);
+  }
+
+  destroy() {
+    if (this.ctx !== null) addon.destroy(this.ctx);
+    this.ctx = null;
+  }
+
+  sync() {
+    addon.sync(this.ctx);
+  }
+
+  deviceInfo() {
+    return addon.deviceInfo(this.ctx);
+  }
+
+  // ---- the kernels, one call each ----
+  matmul(params, xDtype, x, wDtype, w, yDtype, y, { scales = null, group = 0, bias = null, flags = 0 } = {}) {
+    addon.matmul(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
+                 ptrOf(bias), flags);
+  }
+
+  rmsnorm(rows, d, eps, offset, dtype, x, weight, scale, shift, out) {
+    addon.rmsnorm(this.ctx, rows, d, eps, offset, dtype, ptrOf(x), ptrOf(weight), ptrOf(scale), ptrOf(shift),
+                  ptrOf(out));
+  }
+
+  rope(tokens, heads, pairs, half, dtype, x, cos, sin, out) {
+    addon.rope(this.ctx, tokens, heads, pairs, half ? 1 : 0, dtype, ptrOf(x), ptrOf(cos), ptrOf(sin), ptrOf(out));
+  }
+
+  qkNormRope(tokens, heads, headDim, eps, offset, weight, ropeFrom, half, cos, sin, dtype, x, out) {
+    addon.qkNormRope(this.ctx, tokens, heads, headDim, eps, offset, ptrOf(weight), ropeFrom, half ? 1 : 0, ptrOf(cos),
+                     ptrOf(sin), dtype, ptrOf(x), ptrOf(out));
+  }
+
+  elementwise(op, n, d, dtype, a, b, c, out) {
+    addon.elementwise(this.ctx, op, n, d, dtype, ptrOf(a), ptrOf(b), ptrOf(c), ptrOf(out));
+  }
+
+  layerSum(tokens, layers, dim, x, w, out) {
+    addon.layerSum(this.ctx, tokens, layers, dim, ptrOf(x), ptrOf(w), ptrOf(out));
+  }
+
+  // ---- pinned host memory and the copy stream (src/model/weights.ts:124-129, src/gpu/run-ahead.ts:7-21) ----
+  hostAlloc(bytes) {
+    return { ptr: addon.hostAlloc(this.ctx, bytes), size: bytes };
+  }
+
+  hostWrite(pinned, offset, data) {
+    addon.hostWrite(this.ctx, pinned.ptr, offset, data);
+  }
+
+  hostFree(pinned) {
+    addon.hostFree(this.ctx, pinned.ptr);
+  }
+
+  streamCopy(dst, pinnedSrc, bytes, after = 0) {
+    return addon.streamCopy(this.ctx, ptrOf(dst), ptrOf(pinnedSrc), bytes, after);
+  }
+
+  waitTicket(ticket) {
+    addon.waitTicket(this.ctx, ticket);
+  }
+
+  ticketDone(ticket) {
+    return addon.ticketDone(this.ctx, ticket);
+  }
+
+  recordCompute() {
+    return addon.recordCompute(this.ctx);
+  }
+}
+
+/** src/kernels/matmul.ts:198-212: the 13 x u32 Params image, with the same defaults and errors. */
+function matmulParams({ m, n, k }, scale, layout = {}, graph = null) {
+  const l = layout;
+  return addon.matmulParams(graph ? graph.ctx : null, m, n, k, scale, l.xStride, l.wStride, l.yStride, l.xOffset,
+                            l.wOffset, l.yOffset, l.kSplit == null ? 1 : l.kSplit);
+}
+
+/** src/model/ops.ts:42-45 */
+const kSplitFor = (m, n, k) => addon.kSplitFor(m, n, k);
+
+const wdt = (dtype) => (typeof dtype === "string" ? DTYPES[dtype] : dtype);
+
+/** src/model/ops.ts:48-58: split-K partials, then a layer sum over them. */
+function narrowLinear(graph, x, w, m, xDtype = F32) {
+  const split = kSplitFor(m, w.n, w.k);
+  if (split === 1) return linear(graph, x, w, m, { xDtype });
+  const shape = { m, n: w.n, k: w.k };
+  const partials = graph.buffer(split * m * w.n * 4);
+  graph.matmul(matmulParams(shape, w.scale, { kSplit: split }, graph), xDtype, x, wdt(w.dtype), w.buffer, F32, partials,
+               { flags: EPI.SPLIT_K });
+  const y = graph.buffer(m * w.n * 4);
+  graph.layerSum(1, split, m * w.n, partials, graph.buffer(new Float32Array(split).fill(1)), y);
+  return y;
+}
+
+/**
+ * src/model/ops.ts:61-73: y[m, n] = x[m, k] . W^T (+ bias) (+ up.scale * (x . down^T) . up^T, added in place).
+ * The bias (and, on request, the tanh GELU) run in the GEMM epilogue. `w.dtype` may also be "int4" with
+ * `w.scales` (f16 [n, k / group]) and `w.group`.
+ */
+function linear(graph, x, w, m, { xDtype = F32, yDtype = F32, geluTanh = false } = {}) {
+  const shape = { m, n: w.n, k: w.k };
+  const y = graph.buffer(m * w.n * ELEM_BYTES[yDtype]);
+  const flags = (w.bias ? EPI.BIAS : 0) | (geluTanh ? EPI.GELU_TANH : 0);
+  const int4 = wdt(w.dtype) === INT4;
+  graph.matmul(matmulParams(shape, w.scale, {}, graph), xDtype, x, wdt(w.dtype), w.buffer, yDtype, y,
+               { scales: w.scales, group: int4 ? (w.group == null ? 64 : w.group) : 0, bias: w.bias, flags });
+  if (!w.lora) return y;
+  const { down, up } = w.lora;
+  if (down.k !== w.k || up.n !== w.n || up.k !== down.n || down.n % 4) throw new Error("LoRA shapes do not fit the linear layer");
+  const t = narrowLinear(graph, x, down, m, xDtype);
+  graph.matmul(matmulParams({ m, n: up.n, k: up.k }, up.scale, {}, graph), F32, t, wdt(up.dtype), up.buffer, yDtype, y,
+               { flags: EPI.ACCUMULATE });
+  return y;
+}
+
+/** src/model/ops.ts:78-82 */
+function norm(graph, x, weight, rows, d, mod, eps = 1e-5, offset = 1, dtype = F32) {
+  const out = graph.buffer(rows * d * ELEM_BYTES[dtype]);
+  graph.rmsnorm(rows, d, eps, offset, dtype, x, weight, mod ? mod.scale : null, mod ? mod.shift : null, out);
+  return out;
+}
+
+/** src/model/ops.ts:85 */
+const noMod = (graph, d) => ({ scale: graph.buffer(d * 4), shift: graph.buffer(d * 4) });
+
+/** src/model/ops.ts:89-93 */
+function rotate(graph, x, heads, rope, pairing = "interleaved", dtype = F32) {
+  const out = graph.buffer(rope.tokens * heads * rope.pairs * 2 * ELEM_BYTES[dtype]);
+  graph.rope(rope.tokens, heads, rope.pairs, pairing === "half", dtype, x, rope.cos, rope.sin, out);
+  return out;
+}
+
+function elementwise(graph, op, inputs, n, d = 1, dtype = F32) {
+  const out = graph.buffer(n * ELEM_BYTES[dtype]);
+  graph.elementwise(op, n, d, dtype, inputs[0], inputs.length > 1 ? inputs[1] : null,
+                    inputs.length > 2 ? inputs[2] : null, out);
+  return out;
+}
+
+// src/model/ops.ts:102-113
+const swiglu = (graph, gate, up, n, dtype = F32) => elementwise(graph, OP.SWIGLU, [gate, up], n, 1, dtype);
+const sigmoidGate = (graph, a, gate, n, dtype = F32) => elementwise(graph, OP.SIGMOID_GATE, [a, gate], n, 1, dtype);
+const gatedAdd = (graph, x, h, g, n, d, dtype = F32) => elementwise(graph, OP.GATED_ADD, [x, h, g], n, d, dtype);
+const addBias = (graph, x, b, n, d, dtype = F32) => elementwise(graph, OP.ADD_BIAS, [x, b], n, d, dtype);
+const add = (graph, x, h, n, dtype = F32) => elementwise(graph, OP.ADD, [x, h], n, 1, dtype);
+const gelu = (graph, x, n, dtype = F32) => elementwise(graph, OP.GELU_TANH, [x], n, 1, dtype);
+const silu = (graph, x, n, dtype = F32) => elementwise(graph, OP.SILU, [x], n, 1, dtype);
+
+module.exports = {
+  addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP,
+  matmulParams, kSplitFor, linear, norm, noMod, rotate,
+  swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
+  lastError: (graph) => addon.lastError(graph ? graph.ctx : null),
+};

@@ -1,0 +1,599 @@
+/*
+ * Node N-API (v8) addon over the C ABI of include/we.h: the binding a TypeScript host of the engine uses in
+ * place of its WebGPU Graph (src/gpu/graph.ts) to reach the MI355X kernels.
+ *
+ * Conventions of the JS side:
+ *   - a context and every device / pinned-host buffer are passed as BigInt addresses;
+ *   - null or undefined stands for a NULL pointer;
+ *   - matmul Params travel as the reference's 13 x u32 image (a Uint32Array, src/kernels/matmul.ts:120-126);
+ *   - a non-zero status throws an Error whose message is we_last_error() (for shape errors the reference's
+ *     own text, e.g. "K must be a multiple of 4, got 6").
+ */
+#define NAPI_VERSION 8
+#include <node_api.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "we.h"
+
+#define MAXARGS 16
+
+typedef struct {
+  napi_env env;
+  size_t argc;
+  napi_value argv[MAXARGS];
+  int bad;
+} args_t;
+
+static napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+static int get_args(napi_env env, napi_callback_info info, args_t* a, size_t need) {
+  a->env = env;
+  a->argc = MAXARGS;
+  a->bad = 0;
+  napi_get_cb_info(env, info, &a->argc, a->argv, NULL, NULL);
+  if (a->argc < need) {
+    napi_throw_type_error(env, NULL, "too few arguments");
+    a->bad = 1;
+    return 0;
+  }
+  return 1;
+}
+
+static int is_nullish(napi_env env, napi_value v) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  return t == napi_null || t == napi_undefined;
+}
+
+static void* ptr_arg(args_t* a, size_t i) {
+  if (i >= a->argc || is_nullish(a->env, a->argv[i])) return NULL;
+  uint64_t v = 0;
+  bool lossless = true;
+  if (napi_get_value_bigint_uint64(a->env, a->argv[i], &v, &lossless) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a BigInt address");
+    a->bad = 1;
+  }
+  return (void*)(uintptr_t)v;
+}
+
+static uint32_t u32_arg(args_t* a, size_t i) {
+  uint32_t v = 0;
+  if (napi_get_value_uint32(a->env, a->argv[i], &v) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a number");
+    a->bad = 1;
+  }
+  return v;
+}
+
+static int32_t i32_arg(args_t* a, size_t i) {
+  int32_t v = 0;
+  if (napi_get_value_int32(a->env, a->argv[i], &v) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a number");
+    a->bad = 1;
+  }
+  return v;
+}
+
+static int64_t i64_arg(args_t* a, size_t i) { /* undefined / null -> -1: the reference's default */
+  if (i >= a->argc || is_nullish(a->env, a->argv[i])) return -1;
+  int64_t v = 0;
+  if (napi_get_value_int64(a->env, a->argv[i], &v) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a number");
+    a->bad = 1;
+  }
+  return v;
+}
+
+static double f64_arg(args_t* a, size_t i) {
+  double v = 0;
+  if (napi_get_value_double(a->env, a->argv[i], &v) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a number");
+    a->bad = 1;
+  }
+  return v;
+}
+
+static napi_value status(napi_env env, we_ctx* ctx, int rc) {
+  if (rc != WE_OK) napi_throw_error(env, NULL, we_last_error(ctx));
+  return undefined(env);
+}
+
+static napi_value big(napi_env env, const void* p) {
+  napi_value v;
+  napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &v);
+  return v;
+}
+
+static napi_value num(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+/* ---- context ---- */
+static napi_value Create(napi_env env, napi_callback_info info) {
+  args_t a;
+  get_args(env, info, &a, 0);
+  int device = a.argc > 0 ? i32_arg(&a, 0) : 0;
+  if (a.bad) return NULL;
+  we_ctx* ctx = NULL;
+  int rc = we_ctx_create(device, &ctx);
+  if (rc != WE_OK) return status(env, NULL, rc);
+  return big(env, ctx);
+}
+
+static napi_value Destroy(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_ctx_destroy(ctx));
+}
+
+static napi_value DeviceInfo(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  char name[128] = {0};
+  int cus = 0, lds = 0;
+  int rc = we_device_info(ctx, name, sizeof name, &cus, &lds);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  napi_value o, s;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &s);
+  napi_set_named_property(env, o, "arch", s);
+  napi_set_named_property(env, o, "computeUnits", num(env, cus));
+  napi_set_named_property(env, o, "ldsBytes", num(env, lds));
+  return o;
+}
+
+static napi_value Sync(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_sync(ctx));
+}
+
+/* ---- buffers ---- */
+static napi_value BufAlloc(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double bytes = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  void* p = NULL;
+  int rc = we_buf_alloc(ctx, (size_t)bytes, &p);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return big(env, p);
+}
+
+static napi_value BufFree(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* p = ptr_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_buf_free(ctx, p));
+}
+
+/* bytes of a TypedArray / DataView / ArrayBuffer / Buffer argument */
+static int bytes_of(args_t* a, size_t i, void** data, size_t* len) {
+  napi_value v = a->argv[i];
+  bool is;
+  if (napi_is_typedarray(a->env, v, &is) == napi_ok && is) {
+    napi_typedarray_type t;
+    size_t n, off;
+    napi_value ab;
+    napi_get_typedarray_info(a->env, v, &t, &n, data, &ab, &off);
+    size_t el = 1;
+    switch (t) {
+      case napi_int16_array: case napi_uint16_array: el = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: el = 8; break;
+      default: el = 1;
+    }
+    *len = n * el;
+    return 1;
+  }
+  if (napi_is_arraybuffer(a->env, v, &is) == napi_ok && is) {
+    napi_get_arraybuffer_info(a->env, v, data, len);
+    return 1;
+  }
+  if (napi_is_dataview(a->env, v, &is) == napi_ok && is) {
+    napi_value ab;
+    size_t off;
+    napi_get_dataview_info(a->env, v, len, data, &ab, &off);
+    return 1;
+  }
+  napi_throw_type_error(a->env, NULL, "expected a TypedArray, DataView or ArrayBuffer");
+  a->bad = 1;
+  return 0;
+}
+
+static napi_value Upload(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 4)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* dst = ptr_arg(&a, 1);
+  double off = f64_arg(&a, 2);
+  void* data = NULL;
+  size_t len = 0;
+  bytes_of(&a, 3, &data, &len);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_buf_upload(ctx, dst, (size_t)off, data, len));
+}
+
+static napi_value Download(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 4)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* src = ptr_arg(&a, 1);
+  double off = f64_arg(&a, 2), bytes = f64_arg(&a, 3);
+  if (a.bad) return NULL;
+  void* data = NULL;
+  napi_value ab;
+  napi_create_arraybuffer(env, (size_t)bytes, &data, &ab);
+  int rc = we_buf_download(ctx, src, (size_t)off, data, (size_t)bytes);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return ab;
+}
+
+static napi_value Copy(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 6)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* src = ptr_arg(&a, 1);
+  double so = f64_arg(&a, 2);
+  void* dst = ptr_arg(&a, 3);
+  double doff = f64_arg(&a, 4), bytes = f64_arg(&a, 5);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_buf_copy(ctx, src, (size_t)so, dst, (size_t)doff, (size_t)bytes));
+}
+
+static napi_value Mark(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  size_t m = 0;
+  int rc = we_mark(ctx, &m);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)m);
+}
+
+static napi_value Release(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double mark = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  void* keep[64];
+  uint32_t nkeep = 0;
+  if (a.argc > 2 && !is_nullish(env, a.argv[2])) {
+    napi_get_array_length(env, a.argv[2], &nkeep);
+    if (nkeep > 64) {
+      napi_throw_range_error(env, NULL, "at most 64 buffers can be kept");
+      return NULL;
+    }
+    for (uint32_t i = 0; i < nkeep; i++) {
+      napi_value e;
+      uint64_t v = 0;
+      bool lossless;
+      napi_get_element(env, a.argv[2], i, &e);
+      napi_get_value_bigint_uint64(env, e, &v, &lossless);
+      keep[i] = (void*)(uintptr_t)v;
+    }
+  }
+  return status(env, ctx, we_release(ctx, (size_t)mark, keep, nkeep));
+}
+
+static napi_value Stats(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  uint64_t created = 0, reused = 0, bytes = 0;
+  int rc = we_stats(ctx, &created, &reused, &bytes);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "created", num(env, (double)created));
+  napi_set_named_property(env, o, "reused", num(env, (double)reused));
+  napi_set_named_property(env, o, "createdBytes", num(env, (double)bytes));
+  return o;
+}
+
+/* ---- pinned host memory and streaming ---- */
+static napi_value HostAlloc(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double bytes = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  void* p = NULL;
+  int rc = we_host_alloc(ctx, (size_t)bytes, &p);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return big(env, p);
+}
+
+static napi_value HostFree(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* p = ptr_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_host_free(ctx, p));
+}
+
+/* hostWrite(ctx, pinned, offset, bytes): fill pinned host memory from JS */
+static napi_value HostWrite(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 4)) return NULL;
+  void* p = ptr_arg(&a, 1);
+  double off = f64_arg(&a, 2);
+  void* data = NULL;
+  size_t len = 0;
+  bytes_of(&a, 3, &data, &len);
+  if (a.bad) return NULL;
+  if (!p) {
+    napi_throw_error(env, NULL, "pinned buffer is null");
+    return NULL;
+  }
+  memcpy((char*)p + (size_t)off, data, len);
+  return undefined(env);
+}
+
+static napi_value StreamCopy(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* dst = ptr_arg(&a, 1);
+  void* src = ptr_arg(&a, 2);
+  double bytes = f64_arg(&a, 3);
+  double after = f64_arg(&a, 4);
+  if (a.bad) return NULL;
+  uint64_t ticket = 0;
+  int rc = we_stream_copy(ctx, dst, src, (size_t)bytes, (uint64_t)after, &ticket);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)ticket);
+}
+
+static napi_value WaitTicket(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double t = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_wait_ticket(ctx, (uint64_t)t));
+}
+
+static napi_value RecordCompute(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  uint64_t t = 0;
+  int rc = we_record_compute(ctx, &t);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)t);
+}
+
+/* ---- matmul ---- */
+static napi_value MatmulParams(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t m = u32_arg(&a, 1), n = u32_arg(&a, 2), k = u32_arg(&a, 3);
+  double scale = f64_arg(&a, 4);
+  int64_t xs = i64_arg(&a, 5), ws = i64_arg(&a, 6), ys = i64_arg(&a, 7), xo = i64_arg(&a, 8), wo = i64_arg(&a, 9),
+          yo = i64_arg(&a, 10), ks = i64_arg(&a, 11);
+  if (a.bad) return NULL;
+  we_matmul_params p;
+  int rc = we_matmul_params_make(ctx, m, n, k, (float)scale, xs, ws, ys, xo, wo, yo, ks, &p);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  void* data;
+  napi_value ab, arr;
+  napi_create_arraybuffer(env, sizeof p, &data, &ab);
+  memcpy(data, &p, sizeof p);
+  napi_create_typedarray(env, napi_uint32_array, sizeof p / 4, ab, 0, &arr);
+  return arr;
+}
+
+static napi_value KSplitFor(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 3)) return NULL;
+  uint32_t m = u32_arg(&a, 0), n = u32_arg(&a, 1), k = u32_arg(&a, 2);
+  if (a.bad) return NULL;
+  return num(env, we_ksplit_for(m, n, k));
+}
+
+/* matmul(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags) */
+static napi_value Matmul(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 12)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* pdata = NULL;
+  size_t plen = 0;
+  bytes_of(&a, 1, &pdata, &plen);
+  int32_t xdt = i32_arg(&a, 2);
+  void* x = ptr_arg(&a, 3);
+  int32_t wdt = i32_arg(&a, 4);
+  void* w = ptr_arg(&a, 5);
+  void* scales = ptr_arg(&a, 6);
+  uint32_t group = u32_arg(&a, 7);
+  int32_t ydt = i32_arg(&a, 8);
+  void* y = ptr_arg(&a, 9);
+  void* bias = ptr_arg(&a, 10);
+  uint32_t flags = u32_arg(&a, 11);
+  if (a.bad) return NULL;
+  if (plen != sizeof(we_matmul_params)) {
+    napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
+    return NULL;
+  }
+  return status(env, ctx, we_matmul(ctx, (const we_matmul_params*)pdata, xdt, x, wdt, w, scales, group, ydt, y,
+                                    (const float*)bias, flags));
+}
+
+/* ---- norms, rotary, elementwise ---- */
+static napi_value RmsNorm(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 11)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t rows = u32_arg(&a, 1), d = u32_arg(&a, 2);
+  double eps = f64_arg(&a, 3), offset = f64_arg(&a, 4);
+  int32_t dt = i32_arg(&a, 5);
+  void *x = ptr_arg(&a, 6), *wt = ptr_arg(&a, 7), *sc = ptr_arg(&a, 8), *sh = ptr_arg(&a, 9), *out = ptr_arg(&a, 10);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_rmsnorm(ctx, rows, d, (float)eps, (float)offset, dt, x, (const float*)wt,
+                                     (const float*)sc, (const float*)sh, out));
+}
+
+static napi_value Rope(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 10)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t tokens = u32_arg(&a, 1), heads = u32_arg(&a, 2), pairs = u32_arg(&a, 3);
+  int32_t half = i32_arg(&a, 4), dt = i32_arg(&a, 5);
+  void *x = ptr_arg(&a, 6), *c = ptr_arg(&a, 7), *s = ptr_arg(&a, 8), *out = ptr_arg(&a, 9);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_rope(ctx, tokens, heads, pairs, half, dt, x, (const float*)c, (const float*)s, out));
+}
+
+static napi_value Elementwise(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 9)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  int32_t op = i32_arg(&a, 1);
+  double n = f64_arg(&a, 2), d = f64_arg(&a, 3);
+  int32_t dt = i32_arg(&a, 4);
+  void *x = ptr_arg(&a, 5), *b = ptr_arg(&a, 6), *c = ptr_arg(&a, 7), *out = ptr_arg(&a, 8);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_elementwise(ctx, op, (size_t)n, (size_t)d, dt, x, b, c, out));
+}
+
+static napi_value LayerSum(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 7)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t tokens = u32_arg(&a, 1), layers = u32_arg(&a, 2), dim = u32_arg(&a, 3);
+  void *x = ptr_arg(&a, 4), *w = ptr_arg(&a, 5), *out = ptr_arg(&a, 6);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_layer_sum(ctx, tokens, layers, dim, (const float*)x, (const float*)w, (float*)out));
+}
+
+static napi_value QkNormRope(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 14)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t tokens = u32_arg(&a, 1), heads = u32_arg(&a, 2), hd = u32_arg(&a, 3);
+  double eps = f64_arg(&a, 4), offset = f64_arg(&a, 5);
+  void* wt = ptr_arg(&a, 6);
+  uint32_t rope_from = u32_arg(&a, 7);
+  int32_t half = i32_arg(&a, 8);
+  void *c = ptr_arg(&a, 9), *s = ptr_arg(&a, 10);
+  int32_t dt = i32_arg(&a, 11);
+  void *x = ptr_arg(&a, 12), *out = ptr_arg(&a, 13);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_qk_norm_rope(ctx, tokens, heads, hd, (float)eps, (float)offset, (const float*)wt,
+                                          rope_from, half, (const float*)c, (const float*)s, dt, x, out));
+}
+
+static napi_value UnpackFp8(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* packed = ptr_arg(&a, 1);
+  double n = f64_arg(&a, 2);
+  void *sc = ptr_arg(&a, 3), *out = ptr_arg(&a, 4);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_unpack_fp8(ctx, packed, (size_t)n, (const float*)sc, (float*)out));
+}
+
+static napi_value DequantInt4(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 7)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void *words = ptr_arg(&a, 1), *scales = ptr_arg(&a, 2);
+  uint32_t rows = u32_arg(&a, 3), k = u32_arg(&a, 4), group = u32_arg(&a, 5);
+  void* out = ptr_arg(&a, 6);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_dequant_int4(ctx, (const uint32_t*)words, (const uint16_t*)scales, rows, k, group,
+                                          (float*)out));
+}
+
+static napi_value TicketDone(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double t = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  int done = 0;
+  int rc = we_ticket_done(ctx, (uint64_t)t, &done);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  napi_value v;
+  napi_get_boolean(env, done != 0, &v);
+  return v;
+}
+
+static napi_value TimerStart(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_timer_start(ctx));
+}
+
+static napi_value TimerStop(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  float ms = 0;
+  int rc = we_timer_stop(ctx, &ms);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, ms);
+}
+
+static napi_value LastError(napi_env env, napi_callback_info info) {
+  args_t a;
+  get_args(env, info, &a, 0);
+  we_ctx* ctx = a.argc > 0 ? ptr_arg(&a, 0) : NULL;
+  if (a.bad) return NULL;
+  napi_value s;
+  napi_create_string_utf8(env, we_last_error(ctx), NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+static napi_value Init(napi_env env, napi_value exports) {
+  const struct {
+    const char* name;
+    napi_callback fn;
+  } fns[] = {
+      {"create", Create},         {"destroy", Destroy},       {"deviceInfo", DeviceInfo},
+      {"sync", Sync},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
+      {"upload", Upload},         {"download", Download},     {"copy", Copy},
+      {"mark", Mark},             {"release", Release},       {"stats", Stats},
+      {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite},
+      {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
+      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul},
+      {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
+      {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope},
+      {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
+      {"timerStart", TimerStart}, {"timerStop", TimerStop},
+  };
+  for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
+    napi_value f;
+    napi_create_function(env, fns[i].name, NAPI_AUTO_LENGTH, fns[i].fn, NULL, &f);
+    napi_set_named_property(env, exports, fns[i].name, f);
+  }
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

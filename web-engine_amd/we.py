@@ -308,19 +308,8 @@ def matmul_params(m, n, k, scale, x_stride=None, w_stride=None, y_stride=None, x
     rc = lib.we_matmul_params_make(ctx, m, n, k, scale, d(x_stride), d(w_stride), d(y_stride), d(x_offset),
                                    d(w_offset), d(y_offset), k_split, ctypes.byref(p))
     if rc:
-        msg = lib.we_last_error(ctx).decode() if ctx is not None else _params_message(k, x_stride, w_stride, x_offset,
-                                                                                       w_offset)
-        raise WeError(rc, msg)
+        raise WeError(rc, lib.we_last_error(ctx).decode())  # ctx None: this thread's context-free message
     return p
-
-
-def _params_message(k, xs, ws, xo, wo):
-    vals = {"K": k, "xStride": k if xs is None else xs, "wStride": k if ws is None else ws,
-            "xOffset": xo or 0, "wOffset": wo or 0}
-    for name, v in vals.items():
-        if v % 4:
-            return f"{name} must be a multiple of 4, got {v}"
-    return "invalid matmul parameters"
 
 
 def k_split_for(m, n, k):
