@@ -119,10 +119,22 @@ int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int ha
             const float* cos_t, const float* sin_t, void* out);
 /* the q/k path of attend() (src/model/block.ts:53-56) in one pass: per-head RMSNorm (offset, eps) of
  * x [tokens, heads, head_dim], then RoPE on tokens >= rope_from (earlier tokens are only normalized);
- * cos/sin rows are indexed by token. */
+ * cos/sin row r belongs to token rope_from + r. Token t's heads start at t * x_stride of x and
+ * t * out_stride of out (0 = heads * head_dim), so q and k can be read from a fused QKV row. */
 int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                     const float* weight, uint32_t rope_from, int half, const float* cos_t, const float* sin_t,
-                    int dtype, const void* x, void* out);
+                    int dtype, const void* x, uint32_t x_stride, void* out, uint32_t out_stride);
+
+/* ---- attention: attention(graph, q, k, v, shape) (src/kernels/attention.ts:20-51) ---- */
+/* out[t, h] = softmax(q[t, h] . k[j, g]^T / sqrt(dim)) . v[j, g] over keys j (causal: j <= t), g = h / (heads /
+ * kv_heads); fails with "heads must be a multiple of kvHeads" (attention.ts:23). Token t of q starts at
+ * t * q_stride elements (0 = heads * dim; k and v: 0 = kv_heads * dim; out: 0 = heads * dim), so q, k and v
+ * may be slices of one fused QKV row. dtype F32 (exact f32 products), BF16 or F16 (fp32 scores, softmax and
+ * accumulation; probabilities rounded to the operand type). dim: a multiple of 8 (F32: 4), at most 128.
+ * The reference's `chunk` only bounds its score buffer; no score matrix exists here, so it has no analogue. */
+int we_attention(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t dim, int causal, int dtype,
+                 const void* q, uint32_t q_stride, const void* k, uint32_t k_stride, const void* v, uint32_t v_stride,
+                 void* out, uint32_t out_stride);
 
 /* ---- elementwise and reductions (src/kernels/elementwise.ts:38-84, src/kernels/text.ts:67-84) ---- */
 int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,

@@ -6,6 +6,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -415,6 +416,45 @@ void or_rope_rotate_f64(uint32_t tokens, uint32_t heads, uint32_t pairs, int hal
           out[base + j + pairs] = b * c + a * s;
         }
       }
+}
+
+/* tests/gpu/attention.test.ts:9-32 (and src/kernels/attention.ts:9-18): per query head h (kv head
+ * g = h / (heads / kv_heads)) and query i, s_j = q_i . k_j / sqrt(dim) over keys j (causal: j <= i),
+ * p = exp(s - max s) / sum, out = sum_j p_j v_j. q [tokens, heads, dim], k/v [tokens, kv_heads, dim];
+ * only query rows [q_begin, q_end) are computed, into out[(i - q_begin), heads, dim]. */
+void or_attention_f64(uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t dim, int causal, uint32_t q_begin,
+                      uint32_t q_end, const double* q, const double* k, const double* v, double* out) {
+  const uint32_t group = heads / kv_heads;
+  const double rs = 1.0 / sqrt((double)dim);
+  double* s = (double*)malloc(sizeof(double) * (tokens ? tokens : 1));
+  for (uint32_t h = 0; h < heads; h++) {
+    const uint32_t g = h / group;
+    for (uint32_t i = q_begin; i < q_end; i++) {
+      const uint32_t n = causal ? i + 1 : tokens;
+      const double* qi = q + ((size_t)i * heads + h) * dim;
+      double mx = -INFINITY;
+      for (uint32_t j = 0; j < n; j++) {
+        const double* kj = k + ((size_t)j * kv_heads + g) * dim;
+        double dot = 0.0;
+        for (uint32_t d = 0; d < dim; d++) dot += qi[d] * kj[d];
+        s[j] = dot * rs;
+        if (s[j] > mx) mx = s[j];
+      }
+      double sum = 0.0;
+      for (uint32_t j = 0; j < n; j++) {
+        s[j] = exp(s[j] - mx);
+        sum += s[j];
+      }
+      double* o = out + ((size_t)(i - q_begin) * heads + h) * dim;
+      for (uint32_t d = 0; d < dim; d++) o[d] = 0.0;
+      for (uint32_t j = 0; j < n; j++) {
+        const double p = s[j] / sum;
+        const double* vj = v + ((size_t)j * kv_heads + g) * dim;
+        for (uint32_t d = 0; d < dim; d++) o[d] += p * vj[d];
+      }
+    }
+  }
+  free(s);
 }
 
 /* tests/gpu/text.test.ts:58 — PyTorch's tanh GELU, textbook form. */

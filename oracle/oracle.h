@@ -71,6 +71,8 @@ void or_rmsnorm_f64(size_t rows, size_t d, double eps, double offset, const floa
 void or_rope_positions(uint32_t text_tokens, uint32_t rows, uint32_t columns, uint32_t axes, double* pos);
 int or_rope_tables(const double* pos, uint32_t tokens, const uint32_t* axes, uint32_t naxes, double theta,
                    float* cos_out, float* sin_out);
+void or_attention_f64(uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t dim, int causal, uint32_t q_begin,
+                      uint32_t q_end, const double* q, const double* k, const double* v, double* out);
 void or_rope_rotate_f64(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, const float* x,
                         const float* cos_t, const float* sin_t, double* out);
 double or_gelu_tanh(double v);

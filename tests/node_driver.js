@@ -35,6 +35,9 @@ async function runCase(graph, c) {
       const rope = { cos: load(graph, c.cos), sin: load(graph, c.sin), pairs: c.pairs, tokens: c.tokens };
       return we.rotate(graph, load(graph, c.x), c.heads, rope, c.pairing);
     }
+    case "attention":
+      return we.attention(graph, load(graph, c.q), load(graph, c.k), load(graph, c.v),
+                          { tokens: c.tokens, heads: c.heads, kvHeads: c.kvHeads, dim: c.dim, causal: c.causal });
     case "elementwise":
       return we[c.fn](graph, ...c.inputs.map((f) => load(graph, f)), ...c.sizes);
     case "stream": {  // pinned host memory -> device on the copy stream, ordered by a ticket

@@ -43,6 +43,7 @@ def _load():
         "or_rope_positions": (None, [u32, u32, u32, u32, P]),
         "or_rope_tables": (ctypes.c_int, [P, u32, P, u32, d, P, P]),
         "or_rope_rotate_f64": (None, [u32, u32, u32, ctypes.c_int, P, P, P, P]),
+        "or_attention_f64": (None, [u32, u32, u32, u32, ctypes.c_int, u32, u32, P, P, P, P]),
         "or_gelu_tanh": (d, [d]), "or_gelu_tanh_shader": (f, [f]), "or_sigmoid": (d, [d]),
         "or_elementwise_f64": (None, [ctypes.c_int, sz, sz, P, P, P, P]),
         "or_rel_error": (d, [P, P, sz]), "or_compare": (None, [P, P, sz, P, P, P]),
@@ -206,6 +207,16 @@ def rope_rotate(x, tokens, heads, pairs, cos, sin, half=False):
     out = np.empty(x.size, np.float64)
     lib.or_rope_rotate_f64(tokens, heads, pairs, 1 if half else 0, ptr(x), ptr(c_contig(cos, np.float32)),
                            ptr(c_contig(sin, np.float32)), ptr(out))
+    return out
+
+
+def attention(q, k, v, tokens, heads, kv_heads, dim, causal=False, rows=None):
+    """f64 attention of dense q [tokens, heads, dim], k/v [tokens, kv_heads, dim]; rows = (begin, end) of the
+    query rows to compute (default all). Returns [rows, heads, dim] flattened."""
+    q, k, v = (c_contig(a, np.float64) for a in (q, k, v))
+    b, e = rows if rows is not None else (0, tokens)
+    out = np.empty((e - b) * heads * dim, np.float64)
+    lib.or_attention_f64(tokens, heads, kv_heads, dim, 1 if causal else 0, b, e, ptr(q), ptr(k), ptr(v), ptr(out))
     return out
 
 

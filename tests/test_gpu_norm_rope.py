@@ -107,3 +107,27 @@ def test_fused_qk_norm_rope(graph, half, dtype):
     want = np.concatenate([normed.reshape(tokens, heads * hd)[:text].ravel().astype(np.float64), rot])
     tol = 2e-5 if dtype == we.F32 else 2 ** -8
     assert np.all(np.abs(got - want) <= tol * np.maximum(np.abs(want), 1.0))
+
+
+def test_fused_qk_norm_rope_strided_in_place(graph):
+    """q/k normalized and rotated in place inside a fused [tokens, 3 * heads * head_dim] QKV row: the k slice
+    equals the dense result, the q and v slices are untouched."""
+    text, rows, cols, heads, hd = 4, 3, 5, 2, 64
+    tokens, row = text + rows * cols, heads * hd
+    pos = O.rope_positions(0, rows, cols, 2)
+    cos, sin, pairs = O.rope_tables(pos, [32, 32], 10000.0)
+    rng = np.random.default_rng(8)
+    qkv = O.bf16_rne(rng.standard_normal(tokens * 3 * row).astype(np.float32))
+    w = rng.uniform(-0.3, 0.3, hd).astype(np.float32)
+    kpart = np.ascontiguousarray(qkv.reshape(tokens, 3, row)[:, 1])
+    wb, cb, sb = graph.buffer(w), graph.buffer(cos), graph.buffer(sin)
+    dense = graph.buffer(kpart.nbytes)
+    graph.qk_norm_rope(tokens, heads, hd, 1e-6, 1.0, wb, text, False, cb, sb, we.BF16, graph.buffer(kpart), dense)
+    buf = graph.buffer(qkv)
+    kslice = we.Graph.slice(buf, row * 2, 0)
+    graph.qk_norm_rope(tokens, heads, hd, 1e-6, 1.0, wb, text, False, cb, sb, we.BF16, kslice, kslice,
+                       x_stride=3 * row, out_stride=3 * row)
+    got = graph.read(buf).view(np.uint16).reshape(tokens, 3, row)
+    assert np.array_equal(got[:, 1], graph.read(dense).view(np.uint16).reshape(tokens, row))
+    assert np.array_equal(got[:, 0], qkv.reshape(tokens, 3, row)[:, 0])
+    assert np.array_equal(got[:, 2], qkv.reshape(tokens, 3, row)[:, 2])

@@ -2,10 +2,10 @@
 
 CPU: the addon loads under `node`, exports one function per entry point of include/we.h, and its host logic
 (matmulParams image and messages, kSplitFor) equals the oracle's.
-GPU: tests/node_driver.js runs linear (fp8 + bias, fp8 + GELU, fp8 + LoRA, int4), norm, rotate, the
+GPU: tests/node_driver.js runs linear (fp8 + bias, fp8 + GELU, fp8 + LoRA, int4), norm, rotate, attention, the
 elementwise ops and a pinned-host stream copy through the addon; the results are checked here against the
 oracle with the bars of the matching C-ABI tests (test_gpu_matmul, test_gpu_int4, test_gpu_norm_rope,
-test_gpu_elementwise)."""
+test_gpu_elementwise, test_gpu_attention)."""
 import json
 import pathlib
 import shutil
@@ -35,7 +35,7 @@ EXPORTS = {
     "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
     "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
     "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_rmsnorm": "rmsnorm", "we_rope": "rope",
-    "we_qk_norm_rope": "qkNormRope", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
+    "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
 }
 
@@ -175,6 +175,17 @@ def test_graph_steps_through_the_addon(tmp_path):
                       x=_write(tmp_path, "xr", xr), cos=_write(tmp_path, "cos", np.asarray(cos, np.float32)),
                       sin=_write(tmp_path, "sin", np.asarray(sin, np.float32))))
     checks["rotate"] = (np.float32, lambda g: np.abs(g - rope_want).max() < 1e-6)
+
+    # attention, causal, grouped kv heads (tests/gpu/attention.test.ts:87-101 shape, f32)
+    ta, ha, kva, da = 19, 4, 1, 128
+    ua = O.lcg(9, ta * (ha + 2 * kva) * da)
+    qa = ((ua[: ta * ha * da] * 2 - 1) * 2).astype(np.float32)
+    ka = ((ua[ta * ha * da: ta * (ha + kva) * da] * 2 - 1) * 2).astype(np.float32)
+    va = ((ua[ta * (ha + kva) * da:] * 2 - 1) * 2).astype(np.float32)
+    att_want = O.attention(qa, ka, va, ta, ha, kva, da, causal=True)
+    cases.append(dict(name="attention", op="attention", tokens=ta, heads=ha, kvHeads=kva, dim=da, causal=True,
+                      q=_write(tmp_path, "qa", qa), k=_write(tmp_path, "ka", ka), v=_write(tmp_path, "va", va)))
+    checks["attention"] = (np.float32, lambda g: np.abs(g - att_want).max() < 1e-5)
 
     # elementwise (tests/gpu/elementwise.test.ts:15-40)
     ne, de = 1000, 40

@@ -378,3 +378,55 @@ def test_compare_known_answers():  # src/model/compare.ts:2-17
     r = O.compare(np.array([1.0, 0.0]), np.array([0.0, 1.0]))
     assert r["cosine"] == 0 and r["relativeError"] == pytest.approx(math.sqrt(2))
     assert O.rel_error(np.array([1.0, 2.5]), np.array([1.0, 2.0])) == pytest.approx(0.25)
+
+
+# ----------------------------------------------------------------------------------- attention oracle
+
+def _attention_numpy(q, k, v, tokens, heads, kv_heads, dim, causal):
+    """Independent formulation: batched einsum scores, scipy softmax, masked by an upper-triangular -inf."""
+    from scipy.special import softmax
+    q = q.reshape(tokens, heads, dim)
+    k = np.repeat(k.reshape(tokens, kv_heads, dim), heads // kv_heads, axis=1)
+    v = np.repeat(v.reshape(tokens, kv_heads, dim), heads // kv_heads, axis=1)
+    s = np.einsum("ihd,jhd->hij", q, k) / np.sqrt(dim)
+    if causal:
+        s = s + np.triu(np.full((tokens, tokens), -np.inf), 1)
+    return np.einsum("hij,jhd->ihd", softmax(s, axis=-1), v).ravel()
+
+
+@pytest.mark.parametrize("tokens,heads,kv_heads,dim,causal", [(37, 4, 1, 16, False), (64, 8, 2, 32, False),
+                                                              (19, 4, 1, 24, True), (50, 6, 3, 8, True)])
+def test_attention_oracle_matches_numpy(tokens, heads, kv_heads, dim, causal):  # tests/gpu/attention.test.ts:9-32
+    u = O.lcg(tokens + dim, tokens * (heads + 2 * kv_heads) * dim) * 4 - 2
+    q = u[: tokens * heads * dim]
+    k = u[tokens * heads * dim: tokens * (heads + kv_heads) * dim]
+    v = u[tokens * (heads + kv_heads) * dim:]
+    got = O.attention(q, k, v, tokens, heads, kv_heads, dim, causal)
+    assert np.abs(got - _attention_numpy(q, k, v, tokens, heads, kv_heads, dim, causal)).max() < 1e-12
+    b, e = 5, 17
+    part = O.attention(q, k, v, tokens, heads, kv_heads, dim, causal, rows=(b, e))
+    assert np.array_equal(part, got.reshape(tokens, -1)[b:e].ravel())
+
+
+def test_attention_oracle_closed_forms():
+    rng = np.random.default_rng(0)
+    tokens, heads, kv_heads, dim = 9, 4, 2, 8
+    v = rng.standard_normal(tokens * kv_heads * dim)
+    q = rng.standard_normal(tokens * heads * dim)
+    # equal keys: uniform weights, every query gets the mean of its kv head's values
+    k = np.tile(rng.standard_normal(kv_heads * dim), tokens)
+    out = O.attention(q, k, v, tokens, heads, kv_heads, dim).reshape(tokens, heads, dim)
+    mean = v.reshape(tokens, kv_heads, dim).mean(0)
+    for h in range(heads):
+        assert np.allclose(out[:, h], mean[h // 2], atol=1e-12)  # query head h reads kv head h // (heads / kv)
+    # causal: query 0 sees only key 0
+    k = rng.standard_normal(tokens * kv_heads * dim)
+    out = O.attention(q, k, v, tokens, heads, kv_heads, dim, causal=True).reshape(tokens, heads, dim)
+    for h in range(heads):
+        assert np.array_equal(out[0, h], v.reshape(tokens, kv_heads, dim)[0, h // 2])
+    # one dominant key: q . k_3 / sqrt(dim) exceeds the others by ~1000, so the output is v_3
+    k = np.zeros(tokens * kv_heads * dim)
+    k.reshape(tokens, kv_heads, dim)[3] = 1.0
+    q1 = np.full(tokens * heads * dim, 1000.0 * np.sqrt(dim) / dim)
+    out = O.attention(q1, k, v, tokens, heads, kv_heads, dim).reshape(tokens, heads, dim)
+    assert np.allclose(out, v.reshape(tokens, kv_heads, dim)[3][[0, 0, 1, 1]][None], atol=1e-12)

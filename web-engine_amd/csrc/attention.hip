@@ -1,0 +1,414 @@
+// Scaled dot-product attention for gfx950, one pass over the keys with an online softmax.
+//
+// Semantics of src/kernels/attention.ts:20-51: q [tokens, heads, dim], k and v [tokens, kvHeads, dim];
+// query head h reads kv head h / (heads / kvHeads); out [tokens, heads, dim] = softmax(q k^T / sqrt(dim)) v,
+// over all keys or (causal) keys j <= i. Each token's heads may start `stride` elements after the previous
+// token's, so q, k and v can be column slices of one fused QKV projection output.
+//
+// Work split: a workgroup = 4 waves = 128 queries of one head; a wave owns 32 queries. Keys are walked in
+// tiles of 64 that all four waves share through LDS.
+//
+// 16-bit kernel (bf16 or f16 operands, fp32 accumulation, 32x32x16 MFMA):
+//   * S^T = K Q^T: the MFMA's A operand is a K tile row (a key), B is the wave's Q held in registers. In the
+//     32x32 result a lane owns ONE query (column lane % 32) and 16 keys, so the running max, the rescale of
+//     the output and the row sum are per-lane scalars; the two half-waves (the other 16 keys of each 32)
+//     meet through one permlane32 swap.
+//   * O^T = V^T P^T: P never leaves registers. The 8 values a lane feeds the next MFMA are the keys it
+//     owns in the S^T result ({0-3, 8-11} or {4-7, 12-15} of each 16); V^T is written to LDS with bits 2 and
+//     3 of the key index swapped, which puts exactly those 8 keys side by side for one 16-byte read.
+//   * K rows and V^T rows are XOR-swizzled by 16-byte chunk so the MFMA operand reads are bank-conflict free.
+//   * LDS is double-buffered: the next tile's loads are in flight during this tile's MFMAs, then stored to
+//     the other buffer; one barrier per tile.
+// f32 kernel (reference f32 API, 32x32x2 f32 MFMA, exact f32 products): same work split, a single LDS
+// buffer, P kept in f32.
+#include "common.h"
+#include "internal.h"
+
+namespace we {
+namespace {
+
+constexpr int ATT_BM = 128;  // queries per workgroup
+constexpr int ATT_BN = 64;   // keys per tile
+constexpr int ATT_NT = 256;  // threads per workgroup
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  uint32_t tokens, heads, group, dim;  // group = heads / kvHeads
+  uint32_t qs, ks, vs, os;             // elements between consecutive tokens
+  uint32_t nqb;                        // query blocks per head
+  float scale_log2;                    // log2(e) / sqrt(dim)
+  int causal;
+};
+
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// (query block, head) of this workgroup. When the grid splits evenly over the 8 XCDs, each XCD takes a
+// contiguous run of (head-major) blocks, so the workgroups reading one head's K and V share an L2.
+__device__ __forceinline__ void block_coords(const AttnArgs& a, uint32_t& qb, uint32_t& h) {
+  uint32_t b = blockIdx.x;
+  const uint32_t nb = gridDim.x;
+  if ((nb & 7u) == 0u) b = (b & 7u) * (nb >> 3) + (b >> 3);
+  qb = b % a.nqb;
+  h = b / a.nqb;
+}
+
+// two f32 -> two 16-bit values in one word, round to nearest even (v_cvt_pk_bf16_f32 for bf16)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::true_type /*f16*/) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::false_type /*bf16*/) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+
+// ------------------------------------------------------------------------------------ 16-bit kernel
+// DP = head dim padded to 32, 64 or 128 (dims below DP read as zeros and are not stored).
+template <int DP, bool IS_F16>
+__global__ void __launch_bounds__(ATT_NT, 2) attn16_kernel(AttnArgs a) {
+  constexpr int NCH = DP / 8;                       // 16-byte chunks per K row
+  constexpr int KSH = NCH == 16 ? 0 : NCH == 8 ? 1 : 2;
+  constexpr int KS_BYTES = ATT_BN * DP * 2;
+  constexpr int STAGE = 2 * KS_BYTES;               // K tile + V^T tile
+  constexpr int KL = ATT_BN * NCH / ATT_NT;         // K chunks each thread loads
+  constexpr int VU = (ATT_BN / 4) * NCH;            // V units: 4 keys x 8 dims
+  static_assert(KL >= 1 && VU <= ATT_NT, "tile split");
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+
+  uint32_t qb, h;
+  block_coords(a, qb, h);
+  const uint32_t g = h / a.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hf = lane >> 5;
+  const uint32_t q0 = qb * ATT_BM;
+  const uint32_t qw = q0 + 32 * wave;  // first query of this wave
+  const uint32_t qi = qw + c;          // this lane's query
+  const uint16_t* Q = (const uint16_t*)a.q;
+  const uint16_t* K = (const uint16_t*)a.k + (size_t)g * a.dim;
+  const uint16_t* V = (const uint16_t*)a.v + (size_t)g * a.dim;
+
+  // Q as the B operand of S^T = K Q^T: query qi, dims 16 s + 8 hf .. + 7
+  u32x4 qf[DP / 16];
+  static_for<0, DP / 16>([&](auto S) {
+    constexpr int s = S;
+    const uint32_t d = 16 * s + 8 * hf;
+    qf[s] = u32x4{0, 0, 0, 0};
+    if (qi < a.tokens && d < a.dim) qf[s] = *(const u32x4*)(Q + (size_t)qi * a.qs + (size_t)h * a.dim + d);
+  });
+
+  const uint32_t kv_end = a.causal ? min(a.tokens, q0 + ATT_BM) : a.tokens;
+  const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
+
+  u32x4 kr[KL], vr[4];
+  auto load_tile = [&](int t) {
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+#pragma unroll
+    for (int i = 0; i < KL; i++) {
+      const int idx = tid + ATT_NT * i, r = idx / NCH, ch = idx % NCH;
+      const uint32_t key = k0 + r, d = 8 * ch;
+      kr[i] = u32x4{0, 0, 0, 0};
+      if (key < a.tokens && d < a.dim) kr[i] = *(const u32x4*)(K + (size_t)key * a.ks + d);
+    }
+    if (tid < VU) {
+      const int kg = tid & 15, ch = tid >> 4;
+      const uint32_t d = 8 * ch;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t key = k0 + 4 * kg + j;
+        vr[j] = u32x4{0, 0, 0, 0};
+        if (key < a.tokens && d < a.dim) vr[j] = *(const u32x4*)(V + (size_t)key * a.vs + d);
+      }
+    }
+  };
+  auto store_tile = [&](int stage) {
+    char* ks = lds + stage * STAGE;
+    char* vt = ks + KS_BYTES;
+#pragma unroll
+    for (int i = 0; i < KL; i++) {
+      const int idx = tid + ATT_NT * i, r = idx / NCH, ch = idx % NCH;
+      *(u32x4*)(ks + r * DP * 2 + ((ch ^ ((r >> KSH) & (NCH - 1))) << 4)) = kr[i];
+    }
+    if (tid < VU) {
+      const int kg = tid & 15, ch = tid >> 4;
+      // keys 4 kg .. 4 kg + 3 sit at position 4 kg with bits 2 and 3 swapped
+      const int pos = 16 * (kg >> 2) + 4 * (((kg & 1) << 1) | ((kg >> 1) & 1));
+      const int pch = pos >> 3, off = (pos & 7) * 2;
+#pragma unroll
+      for (int dd = 0; dd < 8; dd++) {
+        const int d = 8 * ch + dd, w = dd >> 1, sh = (dd & 1) * 16;
+        const uint32_t e0 = (vr[0][w] >> sh) & 0xffffu, e1 = (vr[1][w] >> sh) & 0xffffu;
+        const uint32_t e2 = (vr[2][w] >> sh) & 0xffffu, e3 = (vr[3][w] >> sh) & 0xffffu;
+        *(u32x2*)(vt + d * ATT_BN * 2 + ((pch ^ ((d >> 1) & 7)) << 4) + off) = u32x2{e0 | (e1 << 16), e2 | (e3 << 16)};
+      }
+    }
+  };
+
+  f32x16 o[DP / 32];
+  static_for<0, DP / 32>([&](auto D) { o[D] = f32x16{}; });
+  float m = -__builtin_inff(), l = 0.0f;
+  const float sl2 = a.scale_log2;
+
+  if (nt > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < nt; t++) {
+    if (t + 1 < nt) load_tile(t + 1);
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    // a wave whose queries all precede the tile has nothing to add (causal)
+    const bool active = !(a.causal && k0 > qw + 31);
+    if (active) {
+      const char* ks = lds + (t & 1) * STAGE;
+      const char* vt = ks + KS_BYTES;
+      f32x16 sacc[2];
+      static_for<0, 2>([&](auto B) {
+        constexpr int b = B;
+        sacc[b] = f32x16{};
+        const int r = 32 * b + c;
+        static_for<0, DP / 16>([&](auto S) {
+          constexpr int s = S;
+          const u32x4 af = *(const u32x4*)(ks + r * DP * 2 + (((2 * s + hf) ^ ((r >> KSH) & (NCH - 1))) << 4));
+          sacc[b] = mfma_32x32x16<IS_F16>(af, qf[s], sacc[b]);
+        });
+      });
+      // scores in log2 units; keys past the end (or after the query, causal) get -inf
+      float x[32];
+      const bool mask = (k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw);
+      static_for<0, 32>([&](auto I) {
+        constexpr int i = I, b = i / 16, v = i % 16;
+        x[i] = sacc[b][v] * sl2;
+        if (mask) {
+          const uint32_t key = k0 + 32 * b + 8 * (v / 4) + 4 * hf + (v % 4);
+          if (key >= a.tokens || (a.causal && key > qi)) x[i] = -__builtin_inff();
+        }
+      });
+      float tmax = x[0];
+      static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
+      tmax = halves_max(tmax);
+      const float mn = fmaxf(m, tmax);
+      const float ms = mn == -__builtin_inff() ? 0.0f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);
+      float ps = 0.0f;
+      u32x4 pf[4];
+      static_for<0, 4>([&](auto S) {
+        constexpr int s = S;
+        float p[8];
+        static_for<0, 8>([&](auto I) {
+          p[I] = __builtin_amdgcn_exp2f(x[16 * (s / 2) + 8 * (s % 2) + I] - ms);
+          ps += p[I];
+        });
+        static_for<0, 4>([&](auto J) {
+          constexpr int j = J;
+          pf[s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
+        });
+      });
+      l = l * alpha + ps;
+      m = mn;
+      static_for<0, DP / 32>([&](auto D) { o[D] *= alpha; });
+      static_for<0, DP / 32>([&](auto D) {
+        constexpr int db = D;
+        const int r = 32 * db + c;
+        static_for<0, 4>([&](auto S) {
+          constexpr int s = S;
+          const u32x4 vf = *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
+          o[db] = mfma_32x32x16<IS_F16>(vf, pf[s], o[db]);
+        });
+      });
+    }
+    if (t + 1 < nt) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  const float inv = 1.0f / halves_sum(l);
+  if (qi < a.tokens) {
+    uint16_t* O = (uint16_t*)a.o + (size_t)qi * a.os + (size_t)h * a.dim;
+    static_for<0, DP / 32>([&](auto D) {
+      constexpr int db = D;
+      static_for<0, 4>([&](auto G) {
+        constexpr int g4 = G;
+        const uint32_t d = 32 * db + 8 * g4 + 4 * hf;
+        if (d < a.dim) {
+          const auto tag = std::integral_constant<bool, IS_F16>{};
+          const u32x2 w{pack2(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, tag),
+                        pack2(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv, tag)};
+          *(u32x2*)(O + d) = w;
+        }
+      });
+    });
+  }
+}
+
+// ------------------------------------------------------------------------------------ f32 kernel
+template <int DP>
+__global__ void __launch_bounds__(ATT_NT, 1) attn32_kernel(AttnArgs a) {
+  constexpr int KROW = DP + 4;                       // floats per K row (padding breaks bank aliasing)
+  constexpr int F4 = ATT_BN * DP / 4 / ATT_NT;       // float4 per thread per tile, each of K and V
+  __shared__ __attribute__((aligned(16))) float ks[ATT_BN * KROW];
+  __shared__ __attribute__((aligned(16))) float vs[ATT_BN * DP];
+
+  uint32_t qb, h;
+  block_coords(a, qb, h);
+  const uint32_t g = h / a.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hf = lane >> 5;
+  const uint32_t q0 = qb * ATT_BM;
+  const uint32_t qw = q0 + 32 * wave;
+  const uint32_t qi = qw + c;
+  const float* Q = (const float*)a.q;
+  const float* K = (const float*)a.k + (size_t)g * a.dim;
+  const float* V = (const float*)a.v + (size_t)g * a.dim;
+
+  // B operand of S^T: step (j, i) contracts dim 8 j + 4 hf + i
+  f32x4 qf[DP / 8];
+  static_for<0, DP / 8>([&](auto J) {
+    const uint32_t d = 8 * J + 4 * hf;
+    qf[J] = f32x4{0, 0, 0, 0};
+    if (qi < a.tokens && d < a.dim) qf[J] = *(const f32x4*)(Q + (size_t)qi * a.qs + (size_t)h * a.dim + d);
+  });
+
+  const uint32_t kv_end = a.causal ? min(a.tokens, q0 + ATT_BM) : a.tokens;
+  const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
+  f32x16 o[DP / 32];
+  static_for<0, DP / 32>([&](auto D) { o[D] = f32x16{}; });
+  float m = -__builtin_inff(), l = 0.0f;
+
+  for (int t = 0; t < nt; t++) {
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    f32x4 kr[F4], vr[F4];
+#pragma unroll
+    for (int i = 0; i < F4; i++) {
+      const int idx = tid + ATT_NT * i, r = idx / (DP / 4), d = 4 * (idx % (DP / 4));
+      const uint32_t key = k0 + r;
+      kr[i] = vr[i] = f32x4{0, 0, 0, 0};
+      if (key < a.tokens && (uint32_t)d < a.dim) {
+        kr[i] = *(const f32x4*)(K + (size_t)key * a.ks + d);
+        vr[i] = *(const f32x4*)(V + (size_t)key * a.vs + d);
+      }
+    }
+    __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+    for (int i = 0; i < F4; i++) {
+      const int idx = tid + ATT_NT * i, r = idx / (DP / 4), d = 4 * (idx % (DP / 4));
+      *(f32x4*)(ks + r * KROW + d) = kr[i];
+      *(f32x4*)(vs + r * DP + d) = vr[i];
+    }
+    __syncthreads();
+    if (a.causal && k0 > qw + 31) continue;
+
+    f32x16 sacc[2];
+    static_for<0, 2>([&](auto B) {
+      constexpr int b = B;
+      sacc[b] = f32x16{};
+      static_for<0, DP / 8>([&](auto J) {
+        constexpr int j = J;
+        const f32x4 kf = *(const f32x4*)(ks + (32 * b + c) * KROW + 8 * j + 4 * hf);
+        static_for<0, 4>([&](auto I) {
+          constexpr int i = I;
+          sacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i], qf[j][i], sacc[b], 0, 0, 0);
+        });
+      });
+    });
+    float x[32];
+    const bool mask = (k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw);
+    static_for<0, 32>([&](auto I) {
+      constexpr int i = I, b = i / 16, v = i % 16;
+      x[i] = sacc[b][v] * a.scale_log2;
+      if (mask) {
+        const uint32_t key = k0 + 32 * b + 8 * (v / 4) + 4 * hf + (v % 4);
+        if (key >= a.tokens || (a.causal && key > qi)) x[i] = -__builtin_inff();
+      }
+    });
+    float tmax = x[0];
+    static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
+    tmax = halves_max(tmax);
+    const float mn = fmaxf(m, tmax);
+    const float ms = mn == -__builtin_inff() ? 0.0f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - ms);
+    float ps = 0.0f;
+    static_for<0, 32>([&](auto I) {
+      x[I] = __builtin_amdgcn_exp2f(x[I] - ms);
+      ps += x[I];
+    });
+    l = l * alpha + ps;
+    m = mn;
+    static_for<0, DP / 32>([&](auto D) { o[D] *= alpha; });
+    // O^T += V^T P^T: step v of key block b contracts key 32 b + 8 (v / 4) + 4 hf + v % 4
+    static_for<0, DP / 32>([&](auto D) {
+      constexpr int db = D;
+      static_for<0, 32>([&](auto I) {
+        constexpr int i = I, b = i / 16, v = i % 16;
+        const float vv = vs[(32 * b + 8 * (v / 4) + 4 * hf + (v % 4)) * DP + 32 * db + c];
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, x[i], o[db], 0, 0, 0);
+      });
+    });
+  }
+
+  const float inv = 1.0f / halves_sum(l);
+  if (qi < a.tokens) {
+    float* O = (float*)a.o + (size_t)qi * a.os + (size_t)h * a.dim;
+    static_for<0, DP / 32>([&](auto D) {
+      constexpr int db = D;
+      static_for<0, 4>([&](auto G) {
+        constexpr int g4 = G;
+        const uint32_t d = 32 * db + 8 * g4 + 4 * hf;
+        if (d < a.dim)
+          *(f32x4*)(O + d) = f32x4{o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, o[db][4 * g4 + 2] * inv,
+                                   o[db][4 * g4 + 3] * inv};
+      });
+    });
+  }
+}
+
+template <class Kern>
+hipError_t launch_attn(Kern kern, const AttnArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(kern, dim3(a.nqb * a.heads), dim3(ATT_NT), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
+  if (L.tokens == 0 || L.heads == 0) return hipSuccess;
+  AttnArgs a;
+  a.q = L.q;
+  a.k = L.k;
+  a.v = L.v;
+  a.o = L.out;
+  a.tokens = L.tokens;
+  a.heads = L.heads;
+  a.group = L.heads / L.kv_heads;
+  a.dim = L.dim;
+  a.qs = L.q_stride;
+  a.ks = L.k_stride;
+  a.vs = L.v_stride;
+  a.os = L.out_stride;
+  a.nqb = (L.tokens + ATT_BM - 1) / ATT_BM;
+  a.scale_log2 = 1.4426950408889634f / sqrtf((float)L.dim);
+  a.causal = L.causal;
+  const int dp = L.dim <= 32 ? 32 : L.dim <= 64 ? 64 : 128;
+  switch (L.dtype) {
+    case BF16:
+      return dp == 32 ? launch_attn(attn16_kernel<32, false>, a, s)
+                      : dp == 64 ? launch_attn(attn16_kernel<64, false>, a, s) : launch_attn(attn16_kernel<128, false>, a, s);
+    case F16:
+      return dp == 32 ? launch_attn(attn16_kernel<32, true>, a, s)
+                      : dp == 64 ? launch_attn(attn16_kernel<64, true>, a, s) : launch_attn(attn16_kernel<128, true>, a, s);
+    default:
+      return dp == 32 ? launch_attn(attn32_kernel<32>, a, s)
+                      : dp == 64 ? launch_attn(attn32_kernel<64>, a, s) : launch_attn(attn32_kernel<128>, a, s);
+  }
+}
+
+}  // namespace we

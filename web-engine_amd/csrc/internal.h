@@ -46,6 +46,18 @@ struct Int4Launch {
 };
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream);
 
+struct AttnLaunch {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int dtype;  // F32, F16 or BF16 for q, k, v and out
+  uint32_t tokens, heads, kv_heads, dim;
+  uint32_t q_stride, k_stride, v_stride, out_stride;  // elements between consecutive tokens
+  int causal;
+};
+hipError_t attention_launch(const AttnLaunch& L, hipStream_t stream);
+
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
 hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
@@ -60,6 +72,7 @@ hipError_t launch_rope(uint32_t tokens, uint32_t heads, uint32_t pairs, int half
                        const float* c, const float* sn, void* out, hipStream_t s);
 hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                                const float* weight, uint32_t rope_from, int half, const float* c, const float* sn,
-                               int dtype, const void* x, void* out, hipStream_t s);
+                               int dtype, const void* x, uint32_t x_stride, void* out, uint32_t out_stride,
+                               hipStream_t s);
 
 }  // namespace we

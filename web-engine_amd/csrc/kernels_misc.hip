@@ -237,17 +237,20 @@ hipError_t launch_rope(uint32_t tokens, uint32_t heads, uint32_t pairs, int half
 // One wave per (token, head) row of head_dim = 2 * pairs values (pairs <= 256): lane l owns pairs
 // l, l + 64, ..., so both values of each of its pairs are in its registers (interleaved: 2j, 2j+1;
 // half: j, j + pairs). Tokens below rope_from are only normalized; cos/sin row = token - rope_from.
+// Token t's heads start at t * xs (input) and t * os (output) elements.
 template <int DT>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(uint32_t tokens, uint32_t heads, uint32_t head_dim,
                                                           float eps, float offset, const float* weight,
                                                           uint32_t rope_from, int half, const float* cs,
-                                                          const float* sn, const void* x, void* out) {
+                                                          const float* sn, const void* x, uint32_t xs, void* out,
+                                                          uint32_t os) {
   const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= (size_t)tokens * heads) return;
-  const uint32_t t = (uint32_t)(row / heads);
+  const uint32_t t = (uint32_t)(row / heads), hh = (uint32_t)(row % heads);
   const uint32_t pairs = head_dim / 2;
-  const size_t base = row * head_dim;
+  const size_t base = (size_t)t * xs + (size_t)hh * head_dim;
+  const size_t obase = (size_t)t * os + (size_t)hh * head_dim;
   float va[4], vb[4];
   float ss = 0.0f;
 #pragma unroll
@@ -279,29 +282,29 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(uint32_t tokens, uint
       ra = a * c - b * s;
       rb = b * c + a * s;
     }
-    store_from_f32<DT>(out, base + ia, ra);
-    store_from_f32<DT>(out, base + ib, rb);
+    store_from_f32<DT>(out, obase + ia, ra);
+    store_from_f32<DT>(out, obase + ib, rb);
   }
 }
 
 hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                                const float* weight, uint32_t rope_from, int half, const float* c, const float* sn,
-                               int dtype, const void* x, void* out, hipStream_t s) {
+                               int dtype, const void* x, uint32_t xs, void* out, uint32_t os, hipStream_t s) {
   const size_t rows = (size_t)tokens * heads;
   if (rows == 0) return hipSuccess;
   const dim3 g((unsigned)((rows + 3) / 4)), t(256);
   switch (dtype) {
     case F16:
       hipLaunchKernelGGL(qk_norm_rope_kernel<F16>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
-                         half, c, sn, x, out);
+                         half, c, sn, x, xs, out, os);
       break;
     case BF16:
       hipLaunchKernelGGL(qk_norm_rope_kernel<BF16>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
-                         half, c, sn, x, out);
+                         half, c, sn, x, xs, out, os);
       break;
     default:
       hipLaunchKernelGGL(qk_norm_rope_kernel<F32>, g, t, 0, s, tokens, heads, head_dim, eps, offset, weight, rope_from,
-                         half, c, sn, x, out);
+                         half, c, sn, x, xs, out, os);
       break;
   }
   return hipGetLastError();

@@ -525,22 +525,60 @@ int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int ha
 
 int we_qk_norm_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                     const float* weight, uint32_t rope_from, int half, const float* cos_t, const float* sin_t,
-                    int dtype, const void* x, void* out) {
+                    int dtype, const void* x, uint32_t x_stride, void* out, uint32_t out_stride) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "dtype %d is not f32 / f16 / bf16", dtype);
   if (head_dim % 2 || head_dim == 0 || head_dim > 512)
     return fail(ctx, WE_EINVAL, "head_dim must be even and at most 512, got %u", head_dim);
-  const uint64_t n = (uint64_t)tokens * heads * head_dim * elem_bytes(dtype);
+  const uint64_t row = (uint64_t)heads * head_dim;
+  const uint64_t xs = x_stride ? x_stride : row, os = out_stride ? out_stride : row;
+  if (xs < row || os < row) return fail(ctx, WE_EINVAL, "token stride below heads * head_dim (%llu)", (unsigned long long)row);
+  const uint64_t esz = elem_bytes(dtype);
   const uint64_t rot_tokens = tokens > rope_from ? tokens - rope_from : 0;
-  int rc = check_span(ctx, x, n, "x");
-  if (!rc) rc = check_span(ctx, out, n, "out");
+  int rc = tokens ? check_span(ctx, x, ((tokens - 1) * xs + row) * esz, "x") : WE_OK;
+  if (!rc && tokens) rc = check_span(ctx, out, ((tokens - 1) * os + row) * esz, "out");
   if (!rc) rc = check_span(ctx, weight, (uint64_t)head_dim * 4, "weight");
   if (!rc) rc = check_span(ctx, cos_t, rot_tokens * (head_dim / 2) * 4, "cos");
   if (!rc) rc = check_span(ctx, sin_t, rot_tokens * (head_dim / 2) * 4, "sin");
   if (rc) return rc;
   hipError_t e = we::launch_qk_norm_rope(tokens, heads, head_dim, eps, offset, weight, rope_from, half ? 1 : 0, cos_t,
-                                         sin_t, dtype, x, out, ctx->compute);
+                                         sin_t, dtype, x, (uint32_t)xs, out, (uint32_t)os, ctx->compute);
   return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "qk norm rope launch");
+}
+
+int we_attention(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t dim, int causal, int dtype,
+                 const void* q, uint32_t q_stride, const void* k, uint32_t k_stride, const void* v, uint32_t v_stride,
+                 void* out, uint32_t out_stride) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (kv_heads == 0 || heads % kv_heads) return fail(ctx, WE_EINVAL, "heads must be a multiple of kvHeads");
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "attention dtype %d is not f32 / f16 / bf16", dtype);
+  const uint32_t align = dtype == WE_F32 ? 4 : 8;
+  if (dim == 0 || dim % align || dim > 128)
+    return fail(ctx, WE_EUNSUPPORTED, "attention dim must be a multiple of %u and at most 128, got %u", align, dim);
+  const uint64_t qrow = (uint64_t)heads * dim, kvrow = (uint64_t)kv_heads * dim;
+  const uint64_t qs = q_stride ? q_stride : qrow, ks = k_stride ? k_stride : kvrow;
+  const uint64_t vs = v_stride ? v_stride : kvrow, os = out_stride ? out_stride : qrow;
+  if (qs < qrow || os < qrow || ks < kvrow || vs < kvrow)
+    return fail(ctx, WE_EINVAL, "attention token stride below the heads it holds");
+  if (qs % align || ks % align || vs % align || os % align)
+    return fail(ctx, WE_EINVAL, "attention token strides must be multiples of %u", align);
+  if (qs > 0xffffffffull || os > 0xffffffffull) return fail(ctx, WE_EINVAL, "attention stride too large");
+  const uint64_t esz = elem_bytes(dtype);
+  const void* ptrs[4] = {q, k, v, out};
+  for (const void* p : ptrs)
+    if (((uintptr_t)p) % 16) return fail(ctx, WE_EINVAL, "attention operands must be 16-byte aligned");
+  if (tokens && heads) {
+    const uint64_t last = tokens - 1;
+    int rc = check_span(ctx, q, (last * qs + qrow) * esz, "q");
+    if (!rc) rc = check_span(ctx, k, (last * ks + kvrow) * esz, "k");
+    if (!rc) rc = check_span(ctx, v, (last * vs + kvrow) * esz, "v");
+    if (!rc) rc = check_span(ctx, out, (last * os + qrow) * esz, "out");
+    if (rc) return rc;
+  }
+  we::AttnLaunch L{q, k, v, out, dtype, tokens, heads, kv_heads, dim, (uint32_t)qs, (uint32_t)ks, (uint32_t)vs,
+                   (uint32_t)os, causal ? 1 : 0};
+  hipError_t e = we::attention_launch(L, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "attention launch");
 }
 
 int we_elementwise(we_ctx* ctx, int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,

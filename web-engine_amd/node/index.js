@@ -91,9 +91,16 @@ class Graph {
     addon.rope(this.ctx, tokens, heads, pairs, half ? 1 : 0, dtype, ptrOf(x), ptrOf(cos), ptrOf(sin), ptrOf(out));
   }
 
-  qkNormRope(tokens, heads, headDim, eps, offset, weight, ropeFrom, half, cos, sin, dtype, x, out) {
+  qkNormRope(tokens, heads, headDim, eps, offset, weight, ropeFrom, half, cos, sin, dtype, x, out, xStride = 0,
+             outStride = 0) {
     addon.qkNormRope(this.ctx, tokens, heads, headDim, eps, offset, ptrOf(weight), ropeFrom, half ? 1 : 0, ptrOf(cos),
-                     ptrOf(sin), dtype, ptrOf(x), ptrOf(out));
+                     ptrOf(sin), dtype, ptrOf(x), xStride, ptrOf(out), outStride);
+  }
+
+  attention(tokens, heads, kvHeads, dim, causal, dtype, q, k, v, out,
+            { qStride = 0, kStride = 0, vStride = 0, outStride = 0 } = {}) {
+    addon.attention(this.ctx, tokens, heads, kvHeads, dim, causal ? 1 : 0, dtype, ptrOf(q), qStride, ptrOf(k), kStride,
+                    ptrOf(v), vStride, ptrOf(out), outStride);
   }
 
   elementwise(op, n, d, dtype, a, b, c, out) {
@@ -197,6 +204,15 @@ function rotate(graph, x, heads, rope, pairing = "interleaved", dtype = F32) {
   return out;
 }
 
+/** src/kernels/attention.ts:20-51: shape { tokens, heads, kvHeads, dim, chunk?, causal? } -> new out buffer. */
+function attention(graph, q, k, v, shape, dtype = F32) {
+  const { tokens, heads, kvHeads, dim } = shape;
+  if (!kvHeads || heads % kvHeads) throw new Error("heads must be a multiple of kvHeads");
+  const out = graph.buffer(tokens * heads * dim * ELEM_BYTES[dtype]);
+  graph.attention(tokens, heads, kvHeads, dim, !!shape.causal, dtype, q, k, v, out);
+  return out;
+}
+
 function elementwise(graph, op, inputs, n, d = 1, dtype = F32) {
   const out = graph.buffer(n * ELEM_BYTES[dtype]);
   graph.elementwise(op, n, d, dtype, inputs[0], inputs.length > 1 ? inputs[1] : null,
@@ -215,7 +231,7 @@ const silu = (graph, x, n, dtype = F32) => elementwise(graph, OP.SILU, [x], n, 1
 
 module.exports = {
   addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP,
-  matmulParams, kSplitFor, linear, norm, noMod, rotate,
+  matmulParams, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
   lastError: (graph) => addon.lastError(graph ? graph.ctx : null),
 };

@@ -490,7 +490,7 @@ static napi_value LayerSum(napi_env env, napi_callback_info info) {
 
 static napi_value QkNormRope(napi_env env, napi_callback_info info) {
   args_t a;
-  if (!get_args(env, info, &a, 14)) return NULL;
+  if (!get_args(env, info, &a, 16)) return NULL;
   we_ctx* ctx = ptr_arg(&a, 0);
   uint32_t tokens = u32_arg(&a, 1), heads = u32_arg(&a, 2), hd = u32_arg(&a, 3);
   double eps = f64_arg(&a, 4), offset = f64_arg(&a, 5);
@@ -499,10 +499,32 @@ static napi_value QkNormRope(napi_env env, napi_callback_info info) {
   int32_t half = i32_arg(&a, 8);
   void *c = ptr_arg(&a, 9), *s = ptr_arg(&a, 10);
   int32_t dt = i32_arg(&a, 11);
-  void *x = ptr_arg(&a, 12), *out = ptr_arg(&a, 13);
+  void* x = ptr_arg(&a, 12);
+  uint32_t xs = u32_arg(&a, 13);
+  void* out = ptr_arg(&a, 14);
+  uint32_t os = u32_arg(&a, 15);
   if (a.bad) return NULL;
   return status(env, ctx, we_qk_norm_rope(ctx, tokens, heads, hd, (float)eps, (float)offset, (const float*)wt,
-                                          rope_from, half, (const float*)c, (const float*)s, dt, x, out));
+                                          rope_from, half, (const float*)c, (const float*)s, dt, x, xs, out, os));
+}
+
+/* attention(ctx, tokens, heads, kvHeads, dim, causal, dtype, q, qStride, k, kStride, v, vStride, out, outStride) */
+static napi_value Attention(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 15)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t tokens = u32_arg(&a, 1), heads = u32_arg(&a, 2), kvh = u32_arg(&a, 3), dim = u32_arg(&a, 4);
+  int32_t causal = i32_arg(&a, 5), dt = i32_arg(&a, 6);
+  void* q = ptr_arg(&a, 7);
+  uint32_t qs = u32_arg(&a, 8);
+  void* k = ptr_arg(&a, 9);
+  uint32_t ks = u32_arg(&a, 10);
+  void* v = ptr_arg(&a, 11);
+  uint32_t vs = u32_arg(&a, 12);
+  void* out = ptr_arg(&a, 13);
+  uint32_t os = u32_arg(&a, 14);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_attention(ctx, tokens, heads, kvh, dim, causal, dt, q, qs, k, ks, v, vs, out, os));
 }
 
 static napi_value UnpackFp8(napi_env env, napi_callback_info info) {
@@ -584,7 +606,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
-      {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope},
+      {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
       {"timerStart", TimerStart}, {"timerStop", TimerStop},
   };

@@ -79,7 +79,8 @@ SIGNATURES = {
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
     "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
-    "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _P]),
+    "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _U32, _P, _U32]),
+    "we_attention": (_I, [_P, _U32, _U32, _U32, _U32, _I, _I, _P, _U32, _P, _U32, _P, _U32, _P, _U32]),
     "we_elementwise": (_I, [_P, _I, _SZ, _SZ, _I, _P, _P, _P, _P]),
     "we_layer_sum": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "we_unpack_fp8": (_I, [_P, _P, _SZ, _P, _P]),
@@ -279,9 +280,16 @@ class Graph:
         self.check(self.lib.we_rope(self.ctx, tokens, heads, pairs, 1 if half else 0, dtype, _addr(x), _addr(cos),
                                     _addr(sin), _addr(out)))
 
-    def qk_norm_rope(self, tokens, heads, head_dim, eps, offset, weight, rope_from, half, cos, sin, dtype, x, out):
+    def qk_norm_rope(self, tokens, heads, head_dim, eps, offset, weight, rope_from, half, cos, sin, dtype, x, out,
+                     x_stride=0, out_stride=0):
         self.check(self.lib.we_qk_norm_rope(self.ctx, tokens, heads, head_dim, eps, offset, _addr(weight), rope_from,
-                                            1 if half else 0, _addr(cos), _addr(sin), dtype, _addr(x), _addr(out)))
+                                            1 if half else 0, _addr(cos), _addr(sin), dtype, _addr(x), x_stride,
+                                            _addr(out), out_stride))
+
+    def attention(self, tokens, heads, kv_heads, dim, causal, dtype, q, k, v, out, q_stride=0, k_stride=0,
+                  v_stride=0, out_stride=0):
+        self.check(self.lib.we_attention(self.ctx, tokens, heads, kv_heads, dim, 1 if causal else 0, dtype, _addr(q),
+                                         q_stride, _addr(k), k_stride, _addr(v), v_stride, _addr(out), out_stride))
 
     def elementwise(self, op, n, d, dtype, a, b, c, out):
         self.check(self.lib.we_elementwise(self.ctx, op, n, d, dtype, _addr(a), _addr(b), _addr(c), _addr(out)))
@@ -387,6 +395,25 @@ def rotate(graph, x, heads, rope, pairing="interleaved", dtype=F32):
     """src/model/ops.ts:89-93"""
     out = graph.buffer(rope.tokens * heads * rope.pairs * 2 * ELEM_BYTES[dtype])
     graph.rope(rope.tokens, heads, rope.pairs, pairing == "half", dtype, x, rope.cos, rope.sin, out)
+    return out
+
+
+class AttentionShape:
+    """src/kernels/attention.ts:7: tokens, heads, kvHeads, dim, chunk (accepted; nothing to bound here), causal."""
+
+    def __init__(self, tokens, heads, kv_heads, dim, chunk=None, causal=False):
+        self.tokens, self.heads, self.kv_heads, self.dim = tokens, heads, kv_heads, dim
+        self.chunk, self.causal = chunk, causal
+
+
+def attention(graph, q, k, v, shape, dtype=F32):
+    """src/kernels/attention.ts:20-51: q [tokens, heads, dim], k/v [tokens, kvHeads, dim] -> new out
+    [tokens, heads, dim]; raises "heads must be a multiple of kvHeads" like the reference."""
+    s = shape
+    if s.kv_heads == 0 or s.heads % s.kv_heads:
+        raise WeError(1, "heads must be a multiple of kvHeads")
+    out = graph.buffer(s.tokens * s.heads * s.dim * ELEM_BYTES[dtype])
+    graph.attention(s.tokens, s.heads, s.kv_heads, s.dim, s.causal, dtype, q, k, v, out)
     return out
 
 
