@@ -457,6 +457,166 @@ void or_attention_f64(uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32
   free(s);
 }
 
+/* ------------------------------------------------------------------------------------------------ */
+/* Blocks                                                                                           */
+/* ------------------------------------------------------------------------------------------------ */
+
+/* tests/gpu/block.test.ts:26-35: y[m, n] = scale * x[m, k] . e4m3(W[n, k]) in f64. */
+static double* blk_mm(const double* x, const or_linear* w, size_t m) {
+  double* y = (double*)malloc(sizeof(double) * m * w->n);
+  double tab[256];
+  for (int b = 0; b < 256; b++) tab[b] = or_e4m3((uint8_t)b);
+  for (size_t i = 0; i < m; i++)
+    for (uint32_t j = 0; j < w->n; j++) {
+      double s = 0.0;
+      const uint8_t* wr = w->bytes + (size_t)j * w->k;
+      const double* xr = x + i * w->k;
+      for (uint32_t t = 0; t < w->k; t++) s += xr[t] * tab[wr[t]];
+      y[i * w->n + j] = s * w->scale;
+    }
+  return y;
+}
+
+/* tests/gpu/block.test.ts:36-45: x / sqrt(mean x^2 + eps) * (offset + w) * (1 + scale) + shift, per row. */
+static double* blk_rmsnorm(const double* x, const float* w, size_t rows, size_t d, double eps, double offset,
+                           const double* scale, const double* shift) {
+  double* y = (double*)malloc(sizeof(double) * rows * d);
+  for (size_t r = 0; r < rows; r++) {
+    double ss = 0.0;
+    for (size_t i = 0; i < d; i++) ss += x[r * d + i] * x[r * d + i];
+    const double inv = 1.0 / sqrt(ss / (double)d + eps);
+    for (size_t i = 0; i < d; i++)
+      y[r * d + i] = x[r * d + i] * inv * (offset + w[i]) * (1.0 + (scale ? scale[i] : 0.0)) + (shift ? shift[i] : 0.0);
+  }
+  return y;
+}
+
+/* tests/gpu/block.test.ts:46-58: interleaved pairs, in place; row t of cos/sin for token t. */
+static void blk_rope(double* x, size_t tokens, size_t heads, size_t pairs, const float* c, const float* s) {
+  for (size_t t = 0; t < tokens; t++)
+    for (size_t h = 0; h < heads; h++)
+      for (size_t j = 0; j < pairs; j++) {
+        const size_t i = ((t * heads + h) * pairs + j) * 2;
+        const double cc = c[t * pairs + j], ss = s[t * pairs + j];
+        const double a = x[i], b = x[i + 1];
+        x[i] = a * cc - b * ss;
+        x[i + 1] = b * cc + a * ss;
+      }
+}
+
+static double blk_sigmoid(double v) { return 1.0 / (1.0 + exp(-v)); }
+
+/* tests/gpu/block.test.ts:60-100 (the composition of src/model/block.ts:91-105): Krea single-stream block. */
+void or_krea_block_f64(const or_block_cfg* cfg, uint32_t tokens, const double* x, const or_linear* w,
+                       const float* norm1, const float* norm2, const float* norm_q, const float* norm_k,
+                       const float* table, const float* temb, const float* cos_t, const float* sin_t, double* out) {
+  const size_t H = cfg->hidden, T = tokens, hd = cfg->head_dim;
+  double* mod = (double*)malloc(sizeof(double) * 6 * H);
+  for (size_t i = 0; i < 6 * H; i++) mod[i] = (double)temb[i] + (double)table[i];
+  const double *prescale = mod, *preshift = mod + H, *pregate = mod + 2 * H, *postscale = mod + 3 * H,
+               *postshift = mod + 4 * H, *postgate = mod + 5 * H;
+  double* h = blk_rmsnorm(x, norm1, T, H, cfg->eps, 1.0, prescale, preshift);
+  double* q0 = blk_mm(h, &w[0], T);
+  double* q = blk_rmsnorm(q0, norm_q, T * cfg->heads, hd, cfg->eps, 1.0, NULL, NULL);
+  blk_rope(q, T, cfg->heads, hd / 2, cos_t, sin_t);
+  double* k0 = blk_mm(h, &w[1], T);
+  double* k = blk_rmsnorm(k0, norm_k, T * cfg->kv_heads, hd, cfg->eps, 1.0, NULL, NULL);
+  blk_rope(k, T, cfg->kv_heads, hd / 2, cos_t, sin_t);
+  double* v = blk_mm(h, &w[2], T);
+  double* g = blk_mm(h, &w[3], T);
+  double* o = (double*)malloc(sizeof(double) * T * cfg->heads * hd);
+  or_attention_f64(tokens, cfg->heads, cfg->kv_heads, cfg->head_dim, 0, 0, tokens, q, k, v, o);
+  for (size_t i = 0; i < T * H; i++) o[i] = o[i] * blk_sigmoid(g[i]);
+  double* a = blk_mm(o, &w[4], T);
+  double* x1 = (double*)malloc(sizeof(double) * T * H);
+  for (size_t i = 0; i < T * H; i++) x1[i] = x[i] + pregate[i % H] * a[i];
+  double* h2 = blk_rmsnorm(x1, norm2, T, H, cfg->eps, 1.0, postscale, postshift);
+  double* gg = blk_mm(h2, &w[5], T);
+  double* uu = blk_mm(h2, &w[6], T);
+  for (size_t i = 0; i < T * cfg->mlp; i++) gg[i] = gg[i] * blk_sigmoid(gg[i]) * uu[i];
+  double* d = blk_mm(gg, &w[7], T);
+  for (size_t i = 0; i < T * H; i++) out[i] = x1[i] + postgate[i % H] * d[i];
+  double* bufs[] = {mod, h, q0, q, k0, k, v, g, o, a, x1, h2, gg, uu, d};
+  for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) free(bufs[i]);
+}
+
+/* The double-stream block of the DiT configuration, composed from the same steps (src/model/block.ts:33-105
+ * order) with one set of weights per stream (text, image) and one joint attention:
+ *   mod_s = tvec + table_s (6 vectors, src/model/block.ts:30-37)
+ *   h_s = rmsnorm(x_s, norm1_s) * (1 + prescale_s) + preshift_s
+ *   [q_s | k_s | v_s] = h_s . qkv_s^T;  q_s, k_s: per-head rmsnorm (norm_q_s, norm_k_s); image q, k: RoPE
+ *   o = attention([q_txt; q_img], [k_txt; k_img], [v_txt; v_img])   (text rows first)
+ *   x1_s = x_s + pregate_s * (o_s . proj_s^T)
+ *   out_s = x1_s + postgate_s * (gelu_tanh((rmsnorm(x1_s, norm2_s) * (1 + postscale_s) + postshift_s) . up_s^T)
+ *           . down_s^T)
+ * All norms use offset 1 and cfg->eps; heads == kv_heads. */
+void or_double_block_f64(const or_block_cfg* cfg, uint32_t txt_tokens, uint32_t img_tokens, const double* x_txt,
+                         const double* x_img, const or_stream_weights* txt, const or_stream_weights* img,
+                         const float* tvec, const float* cos_img, const float* sin_img, double* out_txt,
+                         double* out_img) {
+  const size_t H = cfg->hidden, hd = cfg->head_dim, heads = cfg->heads, T = (size_t)txt_tokens + img_tokens;
+  const or_stream_weights* ws[2] = {txt, img};
+  const double* xs[2] = {x_txt, x_img};
+  double* outs[2] = {out_txt, out_img};
+  const size_t rows[2] = {txt_tokens, img_tokens}, row0[2] = {0, txt_tokens};
+  double* q = (double*)malloc(sizeof(double) * T * H);
+  double* k = (double*)malloc(sizeof(double) * T * H);
+  double* v = (double*)malloc(sizeof(double) * T * H);
+  double* mod[2];
+  for (int s = 0; s < 2; s++) {
+    mod[s] = (double*)malloc(sizeof(double) * 6 * H);
+    for (size_t i = 0; i < 6 * H; i++) mod[s][i] = (double)tvec[i] + (double)ws[s]->table[i];
+    double* h = blk_rmsnorm(xs[s], ws[s]->norm1, rows[s], H, cfg->eps, 1.0, mod[s], mod[s] + H);
+    double* qkv = blk_mm(h, &ws[s]->qkv, rows[s]);
+    double* qs = (double*)malloc(sizeof(double) * rows[s] * H);
+    double* ks = (double*)malloc(sizeof(double) * rows[s] * H);
+    for (size_t r = 0; r < rows[s]; r++)
+      for (size_t i = 0; i < H; i++) {
+        qs[r * H + i] = qkv[r * 3 * H + i];
+        ks[r * H + i] = qkv[r * 3 * H + H + i];
+        v[(row0[s] + r) * H + i] = qkv[r * 3 * H + 2 * H + i];
+      }
+    double* qn = blk_rmsnorm(qs, ws[s]->norm_q, rows[s] * heads, hd, cfg->eps, 1.0, NULL, NULL);
+    double* kn = blk_rmsnorm(ks, ws[s]->norm_k, rows[s] * heads, hd, cfg->eps, 1.0, NULL, NULL);
+    if (s == 1) {
+      blk_rope(qn, rows[s], heads, hd / 2, cos_img, sin_img);
+      blk_rope(kn, rows[s], heads, hd / 2, cos_img, sin_img);
+    }
+    memcpy(q + row0[s] * H, qn, sizeof(double) * rows[s] * H);
+    memcpy(k + row0[s] * H, kn, sizeof(double) * rows[s] * H);
+    free(h);
+    free(qkv);
+    free(qs);
+    free(ks);
+    free(qn);
+    free(kn);
+  }
+  double* o = (double*)malloc(sizeof(double) * T * H);
+  or_attention_f64((uint32_t)T, (uint32_t)heads, (uint32_t)heads, (uint32_t)hd, 0, 0, (uint32_t)T, q, k, v, o);
+  for (int s = 0; s < 2; s++) {
+    const double *pregate = mod[s] + 2 * H, *postscale = mod[s] + 3 * H, *postshift = mod[s] + 4 * H,
+                 *postgate = mod[s] + 5 * H;
+    double* a = blk_mm(o + row0[s] * H, &ws[s]->proj, rows[s]);
+    double* x1 = (double*)malloc(sizeof(double) * rows[s] * H);
+    for (size_t i = 0; i < rows[s] * H; i++) x1[i] = xs[s][i] + pregate[i % H] * a[i];
+    double* h2 = blk_rmsnorm(x1, ws[s]->norm2, rows[s], H, cfg->eps, 1.0, postscale, postshift);
+    double* u = blk_mm(h2, &ws[s]->up, rows[s]);
+    for (size_t i = 0; i < rows[s] * cfg->mlp; i++) u[i] = or_gelu_tanh(u[i]);
+    double* d = blk_mm(u, &ws[s]->down, rows[s]);
+    for (size_t i = 0; i < rows[s] * H; i++) outs[s][i] = x1[i] + postgate[i % H] * d[i];
+    free(a);
+    free(x1);
+    free(h2);
+    free(u);
+    free(d);
+    free(mod[s]);
+  }
+  free(q);
+  free(k);
+  free(v);
+  free(o);
+}
+
 /* tests/gpu/text.test.ts:58 — PyTorch's tanh GELU, textbook form. */
 double or_gelu_tanh(double v) { return 0.5 * v * (1.0 + tanh(sqrt(2.0 / M_PI) * (v + 0.044715 * v * v * v))); }
 

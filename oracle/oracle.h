@@ -71,6 +71,28 @@ void or_rmsnorm_f64(size_t rows, size_t d, double eps, double offset, const floa
 void or_rope_positions(uint32_t text_tokens, uint32_t rows, uint32_t columns, uint32_t axes, double* pos);
 int or_rope_tables(const double* pos, uint32_t tokens, const uint32_t* axes, uint32_t naxes, double theta,
                    float* cos_out, float* sin_out);
+/* Blocks (f64 compositions of the primitives above). */
+typedef struct {
+  const uint8_t* bytes; /* fp8 e4m3fn [n, k] */
+  float scale;
+  uint32_t n, k;
+} or_linear;
+typedef struct {
+  uint32_t hidden, mlp, heads, kv_heads, head_dim;
+  double eps;
+} or_block_cfg;
+/* w: wq, wk, wv, gate, wo, mlpGate, mlpUp, mlpDown */
+void or_krea_block_f64(const or_block_cfg* cfg, uint32_t tokens, const double* x, const or_linear* w,
+                       const float* norm1, const float* norm2, const float* norm_q, const float* norm_k,
+                       const float* table, const float* temb, const float* cos_t, const float* sin_t, double* out);
+typedef struct {
+  or_linear qkv, proj, up, down;
+  const float *norm1, *norm2, *norm_q, *norm_k, *table;
+} or_stream_weights;
+void or_double_block_f64(const or_block_cfg* cfg, uint32_t txt_tokens, uint32_t img_tokens, const double* x_txt,
+                         const double* x_img, const or_stream_weights* txt, const or_stream_weights* img,
+                         const float* tvec, const float* cos_img, const float* sin_img, double* out_txt,
+                         double* out_img);
 void or_attention_f64(uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t dim, int causal, uint32_t q_begin,
                       uint32_t q_end, const double* q, const double* k, const double* v, double* out);
 void or_rope_rotate_f64(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, const float* x,

@@ -18,6 +18,20 @@ class Params(ctypes.Structure):
                                        "cin", "k_split")]
 
 
+class Linear(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_void_p), ("scale", ctypes.c_float), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32)]
+
+
+class BlockCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("hidden", "mlp", "heads", "kv_heads", "head_dim")] + [
+        ("eps", ctypes.c_double)]
+
+
+class StreamW(ctypes.Structure):
+    _fields_ = [(n, Linear) for n in ("qkv", "proj", "up", "down")] + [
+        (n, ctypes.c_void_p) for n in ("norm1", "norm2", "norm_q", "norm_k", "table")]
+
+
 def _load():
     if not LIB_PATH.exists():
         subprocess.run(["make", "-C", str(LIB_PATH.parent)], check=True, capture_output=True)
@@ -44,6 +58,8 @@ def _load():
         "or_rope_tables": (ctypes.c_int, [P, u32, P, u32, d, P, P]),
         "or_rope_rotate_f64": (None, [u32, u32, u32, ctypes.c_int, P, P, P, P]),
         "or_attention_f64": (None, [u32, u32, u32, u32, ctypes.c_int, u32, u32, P, P, P, P]),
+        "or_krea_block_f64": (None, [P, u32, P, P, P, P, P, P, P, P, P, P, P]),
+        "or_double_block_f64": (None, [P, u32, u32, P, P, P, P, P, P, P, P, P]),
         "or_gelu_tanh": (d, [d]), "or_gelu_tanh_shader": (f, [f]), "or_sigmoid": (d, [d]),
         "or_elementwise_f64": (None, [ctypes.c_int, sz, sz, P, P, P, P]),
         "or_rel_error": (d, [P, P, sz]), "or_compare": (None, [P, P, sz, P, P, P]),
@@ -218,6 +234,49 @@ def attention(q, k, v, tokens, heads, kv_heads, dim, causal=False, rows=None):
     out = np.empty((e - b) * heads * dim, np.float64)
     lib.or_attention_f64(tokens, heads, kv_heads, dim, 1 if causal else 0, b, e, ptr(q), ptr(k), ptr(v), ptr(out))
     return out
+
+
+def _lin(bytes_, scale, n, k, keep):
+    b = c_contig(bytes_, np.uint8)
+    keep.append(b)
+    return Linear(b.ctypes.data, scale, n, k)
+
+
+def _cfg(cfg):
+    return BlockCfg(cfg.hidden, cfg.mlp, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.eps)
+
+
+def krea_block(cfg, tokens, x, lins, norm1, norm2, norm_q, norm_k, table, temb, cos, sin):
+    """lins: 8 (bytes, scale, n, k) in the order wq, wk, wv, gate, wo, mlpGate, mlpUp, mlpDown."""
+    keep = []
+    arr = (Linear * 8)(*[_lin(b, s, n, k, keep) for b, s, n, k in lins])
+    vecs = [c_contig(v, np.float32) for v in (norm1, norm2, norm_q, norm_k, table, temb, cos, sin)]
+    x = c_contig(x, np.float64)
+    out = np.empty(tokens * cfg.hidden, np.float64)
+    c = _cfg(cfg)
+    lib.or_krea_block_f64(ctypes.byref(c), tokens, ptr(x), arr, *[ptr(v) for v in vecs], ptr(out))
+    return out
+
+
+def _stream(sw, keep):
+    """sw: dict with qkv/proj/up/down = (bytes, scale, n, k) and f32 vectors norm1/norm2/norm_q/norm_k/table."""
+    vecs = {n: c_contig(sw[n], np.float32) for n in ("norm1", "norm2", "norm_q", "norm_k", "table")}
+    keep.extend(vecs.values())
+    lins = {n: _lin(*sw[n], keep) for n in ("qkv", "proj", "up", "down")}
+    return StreamW(**lins, **{n: v.ctypes.data for n, v in vecs.items()})
+
+
+def double_block(cfg, txt_tokens, img_tokens, x_txt, x_img, w_txt, w_img, tvec, cos_img, sin_img):
+    keep = []
+    st, si = _stream(w_txt, keep), _stream(w_img, keep)
+    x_txt, x_img = c_contig(x_txt, np.float64), c_contig(x_img, np.float64)
+    tv, cs, sn = (c_contig(v, np.float32) for v in (tvec, cos_img, sin_img))
+    out_t = np.empty(txt_tokens * cfg.hidden, np.float64)
+    out_i = np.empty(img_tokens * cfg.hidden, np.float64)
+    c = _cfg(cfg)
+    lib.or_double_block_f64(ctypes.byref(c), txt_tokens, img_tokens, ptr(x_txt), ptr(x_img), ctypes.byref(st),
+                            ctypes.byref(si), ptr(tv), ptr(cs), ptr(sn), ptr(out_t), ptr(out_i))
+    return out_t, out_i
 
 
 def elementwise(op, a, b=None, c=None, d=1):

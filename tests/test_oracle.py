@@ -430,3 +430,120 @@ def test_attention_oracle_closed_forms():
     q1 = np.full(tokens * heads * dim, 1000.0 * np.sqrt(dim) / dim)
     out = O.attention(q1, k, v, tokens, heads, kv_heads, dim).reshape(tokens, heads, dim)
     assert np.allclose(out, v.reshape(tokens, kv_heads, dim)[3][[0, 0, 1, 1]][None], atol=1e-12)
+
+
+# ----------------------------------------------------------------------------------- block oracles
+
+def _np_rms(x, w, d, eps, scale=None, shift=None):
+    x = x.reshape(-1, d)
+    y = x / np.sqrt((x * x).mean(1, keepdims=True) + eps) * (1.0 + w.astype(np.float64))
+    if scale is not None:
+        y = y * (1.0 + scale) + shift
+    return y.ravel()
+
+
+def _np_rope(x, tokens, heads, pairs, cos, sin):
+    z = x.reshape(tokens, heads, pairs, 2)
+    c = cos.reshape(tokens, 1, pairs).astype(np.float64)
+    s = sin.reshape(tokens, 1, pairs).astype(np.float64)
+    rot = (z[..., 0] + 1j * z[..., 1]) * (c + 1j * s)  # a rotation is a complex multiplication
+    return np.stack([rot.real, rot.imag], -1).ravel()
+
+
+def _np_mm(x, lin, m):
+    b, s, n, k = lin
+    return (x.reshape(m, k) @ O.e4m3_table()[b].reshape(n, k).T * s).ravel()
+
+
+class _Cfg:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def _draw_linear(rng, n, k):
+    b = rng.integers(0, 254, n * k).astype(np.uint8)
+    return (b + (b >= 0x7f)).astype(np.uint8), float(np.float32(rng.uniform(0.001, 0.004))), n, k
+
+
+def _krea_inputs(rng, cfg, tokens):
+    H, M, hd = cfg.hidden, cfg.mlp, cfg.head_dim
+    shapes = [(cfg.heads * hd, H), (cfg.kv_heads * hd, H), (cfg.kv_heads * hd, H), (H, H), (H, H), (M, H), (M, H),
+              (H, M)]
+    lins = [_draw_linear(rng, n, k) for n, k in shapes]
+    v = lambda n, s: rng.uniform(-s, s, n).astype(np.float32)  # noqa: E731
+    vecs = dict(norm1=v(H, .5), norm2=v(H, .5), norm_q=v(hd, .5), norm_k=v(hd, .5), table=v(6 * H, .3),
+                temb=v(6 * H, .3))
+    pos = O.rope_positions(3, 2, (tokens - 3) // 2, 3)
+    cos, sin, _ = O.rope_tables(pos, [4, 6, 6], 1000.0)
+    return lins, vecs, cos, sin, rng.uniform(-2, 2, tokens * H)
+
+
+def test_krea_block_oracle_matches_numpy_composition():  # tests/gpu/block.test.ts:60-100
+    cfg = _Cfg(hidden=64, mlp=96, heads=4, kv_heads=2, head_dim=16, eps=1e-5)
+    tokens, H, hd = 9, 64, 16
+    rng = np.random.default_rng(1)
+    lins, vc, cos, sin, x = _krea_inputs(rng, cfg, tokens)
+    got = O.krea_block(cfg, tokens, x, lins, vc["norm1"], vc["norm2"], vc["norm_q"], vc["norm_k"], vc["table"],
+                       vc["temb"], cos, sin)
+    mod = (vc["temb"].astype(np.float64) + vc["table"]).reshape(6, H)
+    h = _np_rms(x, vc["norm1"], H, cfg.eps, mod[0], mod[1])
+    q = _np_rope(_np_rms(_np_mm(h, lins[0], tokens), vc["norm_q"], hd, cfg.eps), tokens, 4, hd // 2, cos, sin)
+    k = _np_rope(_np_rms(_np_mm(h, lins[1], tokens), vc["norm_k"], hd, cfg.eps), tokens, 2, hd // 2, cos, sin)
+    v = _np_mm(h, lins[2], tokens)
+    g = _np_mm(h, lins[3], tokens)
+    o = _attention_numpy(q, k, v, tokens, 4, 2, hd, False) / (1 + np.exp(-g))
+    x1 = x + np.tile(mod[2], tokens) * _np_mm(o, lins[4], tokens)
+    h2 = _np_rms(x1, vc["norm2"], H, cfg.eps, mod[3], mod[4])
+    gg, uu = _np_mm(h2, lins[5], tokens), _np_mm(h2, lins[6], tokens)
+    want = x1 + np.tile(mod[5], tokens) * _np_mm(gg / (1 + np.exp(-gg)) * uu, lins[7], tokens)
+    assert np.abs(got - want).max() < 1e-10 * np.abs(want).max()
+    # zero gates (table = -temb on the gate rows): the block is the identity
+    table = vc["table"].copy().reshape(6, H)
+    table[2], table[5] = -vc["temb"].reshape(6, H)[2], -vc["temb"].reshape(6, H)[5]
+    same = O.krea_block(cfg, tokens, x, lins, vc["norm1"], vc["norm2"], vc["norm_q"], vc["norm_k"], table.ravel(),
+                        vc["temb"], cos, sin)
+    assert np.array_equal(same, x)
+
+
+def _double_inputs(rng, cfg):
+    H, M, hd = cfg.hidden, cfg.mlp, cfg.head_dim
+    v = lambda n, s: rng.uniform(-s, s, n).astype(np.float32)  # noqa: E731
+    return [dict(qkv=_draw_linear(rng, 3 * H, H), proj=_draw_linear(rng, H, H), up=_draw_linear(rng, M, H),
+                 down=_draw_linear(rng, H, M), norm1=v(H, .5), norm2=v(H, .5), norm_q=v(hd, .5), norm_k=v(hd, .5),
+                 table=v(6 * H, .3)) for _ in range(2)]
+
+
+def test_double_block_oracle_matches_numpy_composition():
+    cfg = _Cfg(hidden=64, mlp=128, heads=2, kv_heads=2, head_dim=32, eps=1e-6)
+    H, hd, heads, tt, rows, cols = 64, 32, 2, 5, 3, 4
+    ti = rows * cols
+    rng = np.random.default_rng(2)
+    wt, wi = _double_inputs(rng, cfg)
+    tvec = rng.uniform(-.3, .3, 6 * H).astype(np.float32)
+    cos, sin, _ = O.rope_tables(O.rope_positions(0, rows, cols, 2), [16, 16], 10000.0)
+    xt, xi = rng.uniform(-2, 2, tt * H), rng.uniform(-2, 2, ti * H)
+    got_t, got_i = O.double_block(cfg, tt, ti, xt, xi, wt, wi, tvec, cos, sin)
+    qs, ks, vs, mods = [], [], [], []
+    for w, x, n, rot in ((wt, xt, tt, False), (wi, xi, ti, True)):
+        mod = (tvec.astype(np.float64) + w["table"]).reshape(6, H)
+        mods.append(mod)
+        qkv = _np_mm(_np_rms(x, w["norm1"], H, cfg.eps, mod[0], mod[1]), w["qkv"], n).reshape(n, 3, H)
+        q = _np_rms(qkv[:, 0].ravel(), w["norm_q"], hd, cfg.eps)
+        k = _np_rms(qkv[:, 1].ravel(), w["norm_k"], hd, cfg.eps)
+        if rot:
+            q, k = _np_rope(q, n, heads, hd // 2, cos, sin), _np_rope(k, n, heads, hd // 2, cos, sin)
+        qs.append(q)
+        ks.append(k)
+        vs.append(qkv[:, 2].ravel())
+    o = _attention_numpy(np.concatenate(qs), np.concatenate(ks), np.concatenate(vs), tt + ti, heads, heads, hd,
+                         False).reshape(tt + ti, H)
+    gelu = lambda u: 0.5 * u * (1 + np.tanh(np.sqrt(2 / np.pi) * (u + 0.044715 * u ** 3)))  # noqa: E731
+    for w, x, n, r0, mod, got in ((wt, xt, tt, 0, mods[0], got_t), (wi, xi, ti, tt, mods[1], got_i)):
+        x1 = x + np.tile(mod[2], n) * _np_mm(o[r0:r0 + n].ravel(), w["proj"], n)
+        h2 = _np_rms(x1, w["norm2"], H, cfg.eps, mod[3], mod[4])
+        want = x1 + np.tile(mod[5], n) * _np_mm(gelu(_np_mm(h2, w["up"], n)), w["down"], n)
+        assert np.abs(got - want).max() < 1e-10 * np.abs(want).max()
+    # the streams meet only in attention: new image MLP weights leave the text output unchanged
+    wi2 = dict(wi, up=_draw_linear(rng, cfg.mlp, H))
+    got_t2, got_i2 = O.double_block(cfg, tt, ti, xt, xi, wt, wi2, tvec, cos, sin)
+    assert np.array_equal(got_t2, got_t) and not np.array_equal(got_i2, got_i)

@@ -1,0 +1,284 @@
+"""Transformer blocks on the MI355X kernels, and per-block weight streaming from pinned host memory.
+
+- `positions`, `rope_tables`: src/kernels/rope.ts:14-36 (host-side, f64 angles stored as f32).
+- `block`: the Krea single-stream block of src/model/block.ts:91-105 (attend :40-65, mlp :74-81, modulation
+  :33-37), step for step through the operator API of we.py, freeing each temporary after its last use; the
+  sigmoid gate and SwiGLU write over their first input instead of a new buffer.
+- `DoubleBlock`: the double-stream DiT block (text and image streams with their own weights, one joint
+  attention), built from the same steps with a persistent workspace so a forward allocates nothing:
+    mod_s = tvec + table_s;  h_s = norm1_s(x_s) * (1 + prescale_s) + preshift_s
+    [q|k|v]_s = h_s . qkv_s^T (both streams write one [text + image, 3 hidden] buffer, text rows first)
+    q_s, k_s: per-head RMSNorm, then RoPE on the image rows (in place in that buffer)
+    o = attention(q, k, v) read straight from the fused rows;  x1_s = x_s + pregate_s * (o_s . proj_s^T)
+    out_s = x1_s + postgate_s * down_s(gelu_tanh(up_s(norm2_s(x1_s) * (1 + postscale_s) + postshift_s)))
+  The GELU runs in the up projection's epilogue.
+- `BlockStreamer`: src/model/weights.ts:94-131 loads every block before the first step and paces uploads
+  with onSubmittedWorkDone; src/gpu/run-ahead.ts:7-21 keeps one block of CPU encoding ahead. Here a block's
+  weights live in pinned host memory and are copied on the copy stream into one of two device slots while
+  the block before computes from the other slot.
+"""
+import numpy as np
+
+import we
+
+MOD = ("prescale", "preshift", "pregate", "postscale", "postshift", "postgate")  # src/model/block.ts:30
+
+
+class BlockConfig:
+    """src/model/block.ts:6 (hidden, mlp, heads, kvHeads, headDim, eps)."""
+
+    def __init__(self, hidden, mlp, heads, kv_heads, head_dim, eps=1e-5):
+        self.hidden, self.mlp, self.heads, self.kv_heads, self.head_dim, self.eps = (hidden, mlp, heads, kv_heads,
+                                                                                      head_dim, eps)
+
+
+KREA_BLOCK = BlockConfig(6144, 16384, 48, 12, 128, 1e-5)  # src/model/block.ts:8
+DIT_DOUBLE_BLOCK = BlockConfig(3072, 12288, 24, 24, 128, 1e-6)  # 24 heads x 128, RMSNorm eps 1e-6
+
+
+# ------------------------------------------------------------------------------------------------ RoPE tables
+
+def positions(text_tokens, rows, columns):
+    """src/kernels/rope.ts:14-18: text tokens at (0, 0, 0), image token i at (0, i // columns, i % columns)."""
+    text = np.zeros((text_tokens, 3))
+    i = np.arange(rows * columns)
+    image = np.stack([np.zeros(rows * columns), i // columns, i % columns], axis=1)
+    return np.concatenate([text, image]).astype(np.float64)
+
+
+def rope_tables(pos, axes, theta):
+    """src/kernels/rope.ts:20-36: per axis of dim D, angle = pos * theta^(-2j / D), cos/sin as f32 [tokens, pairs]."""
+    if any(d % 2 for d in axes):
+        raise ValueError("Every RoPE axis needs an even number of dims")
+    pos = np.asarray(pos, np.float64)
+    cols = []
+    for axis, dim in enumerate(axes):
+        j = np.arange(dim // 2, dtype=np.float64)
+        cols.append(pos[:, axis:axis + 1] * theta ** (-(2 * j) / dim))
+    angle = np.concatenate(cols, axis=1)
+    return np.cos(angle).astype(np.float32), np.sin(angle).astype(np.float32), sum(axes) // 2
+
+
+# ------------------------------------------------------------------------------------------ Krea single stream
+
+class BlockWeights:
+    """src/model/block.ts:11-28: the eight linears (we.Linear), norm1, norm2, normQ, normK and table buffers."""
+
+    def __init__(self, wq, wk, wv, gate, wo, mlp_gate, mlp_up, mlp_down, norm1, norm2, norm_q, norm_k, table):
+        self.wq, self.wk, self.wv, self.gate, self.wo = wq, wk, wv, gate, wo
+        self.mlp_gate, self.mlp_up, self.mlp_down = mlp_gate, mlp_up, mlp_down
+        self.norm1, self.norm2, self.norm_q, self.norm_k, self.table = norm1, norm2, norm_q, norm_k, table
+
+
+def modulation(graph, tvec, table, hidden):
+    """src/model/block.ts:33-37: mod = tvec + table; the six vectors as slices of it."""
+    mod = we.add(graph, tvec, table, 6 * hidden)
+    return {name: we.Graph.slice(mod, i * hidden * 4, hidden * 4) for i, name in enumerate(MOD)}, mod
+
+
+def _used(graph, x, f):
+    """src/model/block.ts:68-72: f(x), then x is freed."""
+    y = f(x)
+    graph.free(x)
+    return y
+
+
+def _attend(graph, w, cfg, h, rows, rope, dtype):
+    """src/model/block.ts:40-65. The per-head norm and the RoPE of q and k run as one pass, in place."""
+    def projected(lin, n, norm_w):
+        y = we.linear(graph, h, lin, rows, x_dtype=dtype, y_dtype=dtype)
+        graph.qk_norm_rope(rows, n, cfg.head_dim, cfg.eps, 1.0, norm_w, 0 if rope else rows, False,
+                           rope.cos if rope else None, rope.sin if rope else None, dtype, y, y)
+        return y
+
+    q = projected(w.wq, cfg.heads, w.norm_q)
+    k = projected(w.wk, cfg.kv_heads, w.norm_k)
+    v = we.linear(graph, h, w.wv, rows, x_dtype=dtype, y_dtype=dtype)
+    o = we.attention(graph, q, k, v, we.AttentionShape(rows, cfg.heads, cfg.kv_heads, cfg.head_dim), dtype)
+    for b in (q, k, v):
+        graph.free(b)
+    g = we.linear(graph, h, w.gate, rows, x_dtype=dtype, y_dtype=dtype)
+    graph.elementwise(we.OP_SIGMOID_GATE, rows * cfg.hidden, 1, dtype, o, g, None, o)  # o * sigmoid(g), in place
+    graph.free(g)
+    return _used(graph, o, lambda y: we.linear(graph, y, w.wo, rows, x_dtype=dtype, y_dtype=dtype))
+
+
+def _mlp(graph, w, cfg, h, rows, dtype):
+    """src/model/block.ts:74-81"""
+    gate = we.linear(graph, h, w.mlp_gate, rows, x_dtype=dtype, y_dtype=dtype)
+    up = we.linear(graph, h, w.mlp_up, rows, x_dtype=dtype, y_dtype=dtype)
+    graph.elementwise(we.OP_SWIGLU, rows * cfg.mlp, 1, dtype, gate, up, None, gate)  # silu(gate) * up, in place
+    graph.free(up)
+    return _used(graph, gate, lambda y: we.linear(graph, y, w.mlp_down, rows, x_dtype=dtype, y_dtype=dtype))
+
+
+def block(graph, w, cfg, x, tvec, rope, dtype=we.F32):
+    """src/model/block.ts:91-105: one Krea single-stream block; x [tokens, hidden] -> new [tokens, hidden]."""
+    t, hidden = rope.tokens, cfg.hidden
+    mod, mod_buf = modulation(graph, tvec, w.table, hidden)
+    h = we.norm(graph, x, w.norm1, t, hidden, we.Mod(mod["prescale"], mod["preshift"]), cfg.eps, 1.0, dtype)
+    a = _used(graph, h, lambda y: _attend(graph, w, cfg, y, t, rope, dtype))
+    x1 = _used(graph, a, lambda y: we.gated_add(graph, x, y, mod["pregate"], t * hidden, hidden, dtype))
+    h2 = we.norm(graph, x1, w.norm2, t, hidden, we.Mod(mod["postscale"], mod["postshift"]), cfg.eps, 1.0, dtype)
+    m = _used(graph, h2, lambda y: _mlp(graph, w, cfg, y, t, dtype))
+    out = we.gated_add(graph, x1, m, mod["postgate"], t * hidden, hidden, dtype)
+    for b in (m, x1, mod_buf):
+        graph.free(b)
+    return out
+
+
+# ------------------------------------------------------------------------------------------ double stream (DiT)
+
+class StreamWeights:
+    """One stream's weights: qkv [3 hidden, hidden], proj [hidden, hidden], up [mlp, hidden], down [hidden, mlp]
+    (we.Linear, fp8), and f32 vectors norm1, norm2 [hidden], norm_q, norm_k [head_dim], table [6 hidden]."""
+
+    def __init__(self, qkv, proj, up, down, norm1, norm2, norm_q, norm_k, table):
+        self.qkv, self.proj, self.up, self.down = qkv, proj, up, down
+        self.norm1, self.norm2, self.norm_q, self.norm_k, self.table = norm1, norm2, norm_q, norm_k, table
+
+
+class DoubleBlock:
+    """The double-stream block at fixed token counts, with its workspace allocated once."""
+
+    def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16):
+        if cfg.heads != cfg.kv_heads or cfg.heads * cfg.head_dim != cfg.hidden:
+            raise ValueError("the double-stream block needs heads == kvHeads and heads * headDim == hidden")
+        self.graph, self.cfg, self.dtype = graph, cfg, dtype
+        self.rows = (txt_tokens, img_tokens)
+        self.row0 = (0, txt_tokens)
+        self.tokens = txt_tokens + img_tokens
+        H, e = cfg.hidden, we.ELEM_BYTES[dtype]
+        big = max(self.rows)
+        self.qkv = graph.buffer(self.tokens * 3 * H * e)
+        self.o = graph.buffer(self.tokens * H * e)
+        self.h = graph.buffer(big * H * e)
+        self.a = graph.buffer(big * H * e)
+        self.u = graph.buffer(big * cfg.mlp * e)
+        self.x1 = [graph.buffer(r * H * e) for r in self.rows]
+        self.mod = [graph.buffer(6 * H * 4) for _ in self.rows]
+
+    def free(self):
+        for b in [self.qkv, self.o, self.h, self.a, self.u] + self.x1 + self.mod:
+            self.graph.free(b)
+
+    def forward(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img):
+        """x_s, out_s: [rows_s, hidden] of the block's dtype; tvec f32 [6 hidden]; rope_img: we.Rope over the
+        image tokens (interleaved pairs). out_s may not alias x_s."""
+        g, cfg, dt = self.graph, self.cfg, self.dtype
+        H, hd, heads, e = cfg.hidden, cfg.head_dim, cfg.heads, we.ELEM_BYTES[dt]
+        sl = we.Graph.slice
+        ws, xs, outs = (w_txt, w_img), (x_txt, x_img), (out_txt, out_img)
+        for s in range(2):
+            w, rows, r0 = ws[s], self.rows[s], self.row0[s]
+            g.elementwise(we.OP_ADD, 6 * H, 1, we.F32, tvec, w.table, None, self.mod[s])
+            mod = self.mod[s]
+            g.rmsnorm(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1, sl(mod, 0, H * 4), sl(mod, H * 4, H * 4), self.h)
+            p = we.matmul_params(rows, 3 * H, H, w.qkv.scale, y_offset=r0 * 3 * H, graph=g)
+            g.matmul(p, dt, self.h, we.FP8, w.qkv.buffer, dt, self.qkv)
+            rotate = s == 1
+            for part, norm_w in ((0, w.norm_q), (1, w.norm_k)):
+                base = sl(self.qkv, (r0 * 3 * H + part * H) * e, 0)
+                g.qk_norm_rope(rows, heads, hd, cfg.eps, 1.0, norm_w, 0 if rotate else rows, False,
+                               rope_img.cos if rotate else None, rope_img.sin if rotate else None, dt, base, base,
+                               x_stride=3 * H, out_stride=3 * H)
+        g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
+                    sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
+        for s in range(2):
+            w, rows, r0, mod = ws[s], self.rows[s], self.row0[s], self.mod[s]
+            p = we.matmul_params(rows, H, H, w.proj.scale, x_offset=r0 * H, graph=g)
+            g.matmul(p, dt, self.o, we.FP8, w.proj.buffer, dt, self.a)
+            g.elementwise(we.OP_GATED_ADD, rows * H, H, dt, xs[s], self.a, sl(mod, 2 * H * 4, H * 4), self.x1[s])
+            g.rmsnorm(rows, H, cfg.eps, 1.0, dt, self.x1[s], w.norm2, sl(mod, 3 * H * 4, H * 4),
+                      sl(mod, 4 * H * 4, H * 4), self.h)
+            g.matmul(we.matmul_params(rows, cfg.mlp, H, w.up.scale, graph=g), dt, self.h, we.FP8, w.up.buffer, dt,
+                     self.u, flags=we.EPI_GELU)
+            g.matmul(we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, self.u, we.FP8, w.down.buffer, dt,
+                     self.a)
+            g.elementwise(we.OP_GATED_ADD, rows * H, H, dt, self.x1[s], self.a, sl(mod, 5 * H * 4, H * 4), outs[s])
+
+
+# ------------------------------------------------------------------------------------------ weight streaming
+
+def _align(n, a=256):
+    return (n + a - 1) // a * a
+
+
+class StreamLayout:
+    """Byte layout of one double-stream block's weights, identical in pinned host memory and in a device
+    slot: per stream qkv, proj, up, down (fp8), then norm1, norm2, norm_q, norm_k, table (f32)."""
+
+    def __init__(self, cfg):
+        H, M, hd = cfg.hidden, cfg.mlp, cfg.head_dim
+        self.cfg = cfg
+        self.fields, off = [], 0
+        for s in ("txt", "img"):
+            for name, nbytes in (("qkv", 3 * H * H), ("proj", H * H), ("up", M * H), ("down", H * M),
+                                 ("norm1", 4 * H), ("norm2", 4 * H), ("norm_q", 4 * hd), ("norm_k", 4 * hd),
+                                 ("table", 24 * H)):
+                self.fields.append((s, name, off, nbytes))
+                off = _align(off + nbytes)
+        self.nbytes = off
+        self.fp8_bytes = 2 * (3 * H * H + H * H + 2 * M * H)
+
+    def weights(self, base, scales):
+        """StreamWeights (text, image) over the buffer at `base`; scales[s][name] = per-tensor fp8 scale."""
+        views = {}
+        for s, name, off, nbytes in self.fields:
+            views[(s, name)] = we.Graph.slice(base, off, nbytes)
+        cfg = self.cfg
+        H, M = cfg.hidden, cfg.mlp
+        out = []
+        for s in ("txt", "img"):
+            lin = lambda name, n, k: we.Linear(views[(s, name)], "fp8", scales[s][name], n, k)  # noqa: E731
+            out.append(StreamWeights(lin("qkv", 3 * H, H), lin("proj", H, H), lin("up", M, H), lin("down", H, M),
+                                     views[(s, "norm1")], views[(s, "norm2")], views[(s, "norm_q")],
+                                     views[(s, "norm_k")], views[(s, "table")]))
+        return out
+
+    def fill(self, dst, rng, vec_scale=0.3):
+        """Random-init weights into a uint8 view `dst` of nbytes: fp8 codes uniform over the 254 finite ones,
+        norm weights and tables uniform in +-vec_scale."""
+        for s, name, off, nbytes in self.fields:
+            if name in ("qkv", "proj", "up", "down"):
+                b = rng.integers(0, 254, nbytes, dtype=np.uint8)
+                dst[off:off + nbytes] = b + (b >= 0x7f) + (b >= 0xfe)  # skip 0x7f and 0xff
+            else:
+                dst[off:off + nbytes] = ((rng.random(nbytes // 4) * 2 - 1) * vec_scale).astype(np.float32).view(
+                    np.uint8)
+
+
+class BlockStreamer:
+    """Double-buffered weight streaming: block i's weights are copied from its pinned host buffer into device
+    slot i % 2 on the copy stream, once the block that last used that slot has been queued; the compute
+    stream waits for the copy of block i only when it reaches block i."""
+
+    def __init__(self, graph, layout, slots=2):
+        self.graph, self.layout = graph, layout
+        self.slots = [graph.buffer(layout.nbytes) for _ in range(slots)]
+
+    def run(self, pinned, compute):
+        """pinned: host buffers of the blocks (we.Graph.host_alloc results); compute(i, slot_buffer) queues
+        block i's work. Returns after queuing everything."""
+        g, n = self.graph, len(self.slots)
+        tickets = {}
+        for i in range(min(n, len(pinned))):
+            tickets[i] = g.stream_copy(self.slots[i], pinned[i], self.layout.nbytes, 0)
+        for i in range(len(pinned)):
+            g.wait_ticket(tickets.pop(i))
+            compute(i, self.slots[i % n])
+            if i + n < len(pinned):
+                done = g.record_compute()
+                tickets[i + n] = g.stream_copy(self.slots[i % n], pinned[i + n], self.layout.nbytes, done)
+
+    def free(self):
+        for b in self.slots:
+            self.graph.free(b)
+
+
+def rope_for_image(graph, rows, columns, axes=(64, 64), theta=10000.0):
+    """2D-axial RoPE of a rows x columns image grid ((row, column) axes), as a we.Rope over the image tokens."""
+    pos = positions(0, rows, columns)[:, 1:]
+    cos, sin, pairs = rope_tables(pos, axes, theta)
+    return we.Rope(graph.buffer(cos), graph.buffer(sin), pairs, rows * columns)
+

@@ -173,7 +173,8 @@ int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units,
 // ------------------------------------------------------------------------------------------ buffers
 
 int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
-  if (!ctx || !out) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!out) return fail(ctx, WE_EINVAL, "output pointer is null");
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   const size_t size = round_size(bytes);
   void* p = nullptr;
@@ -249,7 +250,8 @@ int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size
 }
 
 int we_mark(we_ctx* ctx, size_t* mark) {
-  if (!ctx || !mark) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!mark) return fail(ctx, WE_EINVAL, "output pointer is null");
   *mark = ctx->owned.size();
   return WE_OK;
 }
@@ -287,7 +289,8 @@ int we_sync(we_ctx* ctx) {
 // ------------------------------------------------------------------------------------------ pinned host / streaming
 
 int we_host_alloc(we_ctx* ctx, size_t bytes, void** out) {
-  if (!ctx || !out) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!out) return fail(ctx, WE_EINVAL, "output pointer is null");
   void* p = nullptr;
   hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
   if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -307,7 +310,8 @@ int we_host_free(we_ctx* ctx, void* ptr) {
 }
 
 int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket) {
-  if (!ctx || !ticket) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!ticket) return fail(ctx, WE_EINVAL, "output pointer is null");
   int rc = check_span(ctx, dst, bytes, "stream destination");
   if (rc) return rc;
   auto it = ctx->pinned.upper_bound((uintptr_t)pinned_src);
@@ -334,12 +338,14 @@ int we_wait_ticket(we_ctx* ctx, uint64_t ticket) {
 }
 
 int we_record_compute(we_ctx* ctx, uint64_t* ticket) {
-  if (!ctx || !ticket) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!ticket) return fail(ctx, WE_EINVAL, "output pointer is null");
   return new_ticket(ctx, ctx->compute, ticket);
 }
 
 int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
-  if (!ctx || !done) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!done) return fail(ctx, WE_EINVAL, "output pointer is null");
   int rc = ticket_valid(ctx, ticket);
   if (rc) return rc;
   hipError_t e = hipEventQuery(ticket_event(ctx, ticket));
@@ -356,7 +362,8 @@ int we_timer_start(we_ctx* ctx) {
 }
 
 int we_timer_stop(we_ctx* ctx, float* ms) {
-  if (!ctx || !ms) return WE_EINVAL;
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!ms) return fail(ctx, WE_EINVAL, "output pointer is null");
   HIP_OK(ctx, hipEventRecord(ctx->t1, ctx->compute), "hipEventRecord");
   HIP_OK(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");
   HIP_OK(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1), "hipEventElapsedTime");

@@ -236,6 +236,11 @@ class Graph:
         self.check(self.lib.we_host_alloc(self.ctx, nbytes, ctypes.byref(p)))
         return p.value
 
+    @staticmethod
+    def host_view(ptr, nbytes):
+        """A numpy uint8 view of pinned host memory from host_alloc (valid until host_free)."""
+        return np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(ptr))
+
     def host_free(self, ptr):
         self.check(self.lib.we_host_free(self.ctx, ctypes.c_void_p(ptr)))
 
