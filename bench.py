@@ -15,6 +15,9 @@ is launched on):
     weight copies rotate (> 256 MB) so no launch reads its weights from the Infinity Cache; M = 8 and 16
     are reported beside it;
   * the dense bf16 GEMM at the DiT QKV shape and the small fp8 GEMM (M = 64);
+  * c5_double_block: the double-stream DiT block (512 text + 4096 image tokens, hidden 3072, 24 heads,
+    fp8 weights, bf16 activations) with its weights resident, the per-block weight copy from pinned host
+    memory alone (H2D GB/s), and 4 blocks streamed through two device slots (overlap efficiency);
   * traffic: HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this script, scaled by
     what the same counters read for the elementwise add kernel of known traffic that this script also
     launches (calibration); the measured values live in profiles/traffic.json;
@@ -31,6 +34,7 @@ import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "web-engine_amd"))
+import block as B  # noqa: E402
 import we  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 / f16 MFMA
@@ -142,6 +146,74 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20):
     return {"us": ms * 1e3, "tflops": flop / ms / 1e9}
 
 
+def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
+    """The double-stream DiT block (512 text + 4096 image tokens, hidden 3072, 24 heads of 128, MLP 12288, fp8
+    weights, bf16 activations): resident (weights already in HBM), the weight copies alone, and `layers`
+    blocks whose weights stream from pinned host memory (block i from buffer i % pinned_sets, every block a
+    full copy) through two device slots while the block before computes. Overlap efficiency =
+    (t_copy + t_compute - t_streamed) / min(t_copy, t_compute), per block."""
+    cfg, tt, rows, cols = B.DIT_DOUBLE_BLOCK, 512, 64, 64
+    ti, H = rows * cols, cfg.hidden
+    blk = B.DoubleBlock(g, cfg, tt, ti, we.BF16)
+    layout = B.StreamLayout(cfg)
+    host = np.empty(layout.nbytes, np.uint8)
+    layout.fill(host, rng)
+    scales = {s: {n: 0.02 / np.sqrt(cfg.mlp if n == "down" else H) for n in ("qkv", "proj", "up", "down")}
+              for s in ("txt", "img")}
+    rope = B.rope_for_image(g, rows, cols)
+    tvec = g.buffer((rng.uniform(-0.2, 0.2, 6 * H)).astype(np.float32))
+    xs = [(g.buffer(bf16_bits(rng.standard_normal(tt * H))), g.buffer(bf16_bits(rng.standard_normal(ti * H))))
+          for _ in range(2)]
+    resident = g.buffer(host)
+    w_res = layout.weights(resident, scales)
+
+    def forward(i, weights):
+        a, b = xs[i % 2], xs[(i + 1) % 2]
+        blk.forward(weights[0], weights[1], a[0], a[1], tvec, rope, b[0], b[1])
+
+    for i in range(2):
+        forward(i, w_res)
+    t_comp = time_launches(g, lambda i: forward(i, w_res), iters)
+    attn_ms = time_launches(g, lambda i: g.attention(tt + ti, 24, 24, 128, False, we.BF16, blk.qkv,
+                                                     we.Graph.slice(blk.qkv, H * 2, 0),
+                                                     we.Graph.slice(blk.qkv, 2 * H * 2, 0), blk.o, q_stride=3 * H,
+                                                     k_stride=3 * H, v_stride=3 * H, out_stride=H), iters)
+    g.free(resident)
+
+    pinned = [g.host_alloc(layout.nbytes) for _ in range(pinned_sets)]
+    for p in pinned:
+        g.host_view(p, layout.nbytes)[:] = host
+    streamer = B.BlockStreamer(g, layout)
+    # copies alone: the copy stream, ordered after a compute-stream event taken at the timer start
+    g.sync()
+    g.timer_start()
+    start = g.record_compute()
+    last = 0
+    for i in range(layers):
+        last = g.stream_copy(streamer.slots[i % 2], pinned[i % pinned_sets], layout.nbytes, start if i == 0 else last)
+    g.wait_ticket(last)
+    t_copy = g.timer_stop() / layers
+    # streamed blocks
+    g.sync()
+    g.timer_start()
+    streamer.run(pinned, lambda i, slot: forward(i, layout.weights(slot, scales)), start=g.record_compute(),
+                 blocks=layers)
+    t_stream = g.timer_stop() / layers
+    g.sync()
+    streamer.free()
+    for p in pinned:
+        g.host_free(p)
+    blk.free()
+    flop = 2.0 * (tt + ti) * H * (3 * H + H + 2 * cfg.mlp) + 4.0 * (tt + ti) ** 2 * H
+    attn_flop = 4.0 * (tt + ti) ** 2 * H
+    return {"tokens": f"{tt} text + {ti} image", "layers_streamed": layers, "flop_per_block": flop,
+            "resident_ms": t_comp, "resident_tflops": flop / t_comp / 1e9,
+            "attention_us": attn_ms * 1e3, "attention_tflops": attn_flop / attn_ms / 1e9,
+            "weight_bytes_per_block": layout.nbytes, "copy_ms_per_block": t_copy,
+            "h2d_gbs": layout.nbytes / t_copy / 1e6, "streamed_ms_per_block": t_stream,
+            "overlap_efficiency": (t_copy + t_comp - t_stream) / min(t_copy, t_comp)}
+
+
 def calibration_copy(g, nbytes=256 << 20):
     """A plain streaming kernel of known traffic (out = a + b over f32): reads 2 * nbytes, writes nbytes.
     Its FETCH_SIZE / WRITE_SIZE under rocprofv3 scale the counters of the kernels above."""
@@ -195,7 +267,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["mlp", "int4", "all"], default="all")
+    ap.add_argument("--only", choices=["mlp", "int4", "block", "all"], default="all")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build has no multi-GPU "
@@ -211,6 +283,9 @@ def main():
     int4 = bench_int4(g, rng) if args.only in ("int4", "all") else None
     print("[bench] int4 done", file=sys.stderr, flush=True)
     extra = {}
+    if args.only in ("block", "all"):
+        extra["c5_double_block"] = bench_block(g, rng)
+        print("[bench] block done", file=sys.stderr, flush=True)
     if args.only == "all":
         extra["c2_bf16_qkv_4096x9216x3072"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
         extra["c1_fp8_64x3072x3072"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16)

@@ -257,19 +257,23 @@ class BlockStreamer:
         self.graph, self.layout = graph, layout
         self.slots = [graph.buffer(layout.nbytes) for _ in range(slots)]
 
-    def run(self, pinned, compute):
-        """pinned: host buffers of the blocks (we.Graph.host_alloc results); compute(i, slot_buffer) queues
-        block i's work. Returns after queuing everything."""
+    def run(self, pinned, compute, start=0, blocks=None):
+        """pinned: host buffers of the blocks (we.Graph.host_alloc results); block i's weights are
+        pinned[i % len(pinned)]; blocks: how many blocks to run (default len(pinned)); compute(i, slot_buffer)
+        queues block i's work; start: a compute ticket the first copies wait for (0 = none). Returns after
+        queuing everything."""
         g, n = self.graph, len(self.slots)
+        blocks = len(pinned) if blocks is None else blocks
+        src = lambda i: pinned[i % len(pinned)]  # noqa: E731
         tickets = {}
-        for i in range(min(n, len(pinned))):
-            tickets[i] = g.stream_copy(self.slots[i], pinned[i], self.layout.nbytes, 0)
-        for i in range(len(pinned)):
+        for i in range(min(n, blocks)):
+            tickets[i] = g.stream_copy(self.slots[i], src(i), self.layout.nbytes, start)
+        for i in range(blocks):
             g.wait_ticket(tickets.pop(i))
             compute(i, self.slots[i % n])
-            if i + n < len(pinned):
+            if i + n < blocks:
                 done = g.record_compute()
-                tickets[i + n] = g.stream_copy(self.slots[i % n], pinned[i + n], self.layout.nbytes, done)
+                tickets[i + n] = g.stream_copy(self.slots[i % n], src(i + n), self.layout.nbytes, done)
 
     def free(self):
         for b in self.slots:
