@@ -350,3 +350,38 @@ def test_lora_down_split_over_long_k(graph):  # tests/gpu/lora.test.ts:120-146
     got = graph.read(we.linear(graph, graph.buffer(x), lin, m), dtype=np.float32, count=m * n)
     assert rms_rel(got, lora_reference(x, w_v, 1.0, down_v, up_v, s, m, n, k, r)) < 1e-6
     graph.release(mark)
+
+
+# ------------------------------------------------------------------ small M: K split over workgroups, reduced in-kernel
+
+@pytest.mark.parametrize("m,n,k,x_dt,y_dt,flags", [
+    (64, 3072, 3072, we.F16, we.F16, 0),                      # the single fp8 matmul at M = 64
+    (37, 70, 1024, we.BF16, we.F32, we.EPI_BIAS | we.EPI_GELU),
+    (1, 300, 2048, we.BF16, we.BF16, 0),
+    (64, 1000, 4096, we.F16, we.F32, we.EPI_ACCUMULATE),
+    (33, 129, 768, we.F16, we.F16, we.EPI_BIAS)])
+def test_small_m_split_k_reduction(graph, monkeypatch, m, n, k, x_dt, y_dt, flags):
+    """Small-M fp8 GEMMs split K across workgroups and the last slice of each tile adds the others. The
+    result matches the oracle, repeats bit for bit (slices are summed in slice order), and matches the
+    unsplit kernel within the same bar."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w = rng.integers(0, 254, n * k).astype(np.uint8)
+    w = (w + (w >= 0x7F)).astype(np.uint8)
+    bias = rng.normal(0, 1, n).astype(np.float32) if flags & we.EPI_BIAS else None
+    start = rng.standard_normal(m * n).astype(np.float32) if flags & we.EPI_ACCUMULATE else None
+    y_init = start if start is not None else None
+    p = we.matmul_params(m, n, k, 0.02, graph=graph)
+    runs = [run(graph, p, x_store, x_dt, w, we.FP8, y_dt, flags=flags, bias=bias, y_init=y_init) for _ in range(2)]
+    assert np.array_equal(runs[0], runs[1])
+    lin = O.matmul(O.matmul_params(m, n, k, 0.02), ox, x_oracle, O.FP8, w)
+    if bias is not None:
+        lin = lin + np.tile(bias.astype(np.float64), m)
+    want = np.array([O.lib.or_gelu_tanh(v) for v in lin]) if flags & we.EPI_GELU else lin
+    if start is not None:
+        want = want + start
+    tol = 1e-4 if flags & we.EPI_GELU else TOL[y_dt]
+    assert O.rel_error(runs[0], want) < tol
+    monkeypatch.setenv("WE_GEMM_SPLITK", "off")
+    unsplit = run(graph, p, x_store, x_dt, w, we.FP8, y_dt, flags=flags, bias=bias, y_init=y_init)
+    assert O.rel_error(unsplit, want) < tol

@@ -50,6 +50,10 @@ struct FastArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t flags, y_dtype;
   uint32_t vec_store;  // 1: y rows and y_offset allow 4-value vector stores
+  // split-K partial sums (rsplits > 1): slice z stores its raw sums at part + z * m * n (dense rows of n);
+  // splitk_reduce_kernel adds the slices and runs the epilogue
+  float* part;
+  uint32_t rsplits;
 };
 
 __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
@@ -411,12 +415,38 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     }
   }
 
+  if (a.rsplits > 1) {
+    // ---- split-K slice: raw sums (no scale) to the partial-sum plane of this slice
+    const size_t plane = (size_t)a.m * a.n;
+    const bool vec = (a.n & 3u) == 0u;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+      if (row >= a.m) continue;
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint32_t c0 = col0 + wn * WTN + j * 32 + 8 * q + 4 * h;
+          float* p = a.part + z * plane + (size_t)row * a.n + c0;
+          if (vec && c0 + 3 < a.n) {
+            *(f32x4*)p = f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (c0 + e < a.n) p[e] = acc[i][j][4 * q + e];
+          }
+        }
+    }
+    return;
+  }
+
   // ---- epilogue: lane (l32, h) holds row l32 of each 32-row sub-tile and, for q = 0..3, the columns
   // 8q + 4h .. 8q + 4h + 3 of each 32-column sub-tile (accumulator entries 4q .. 4q + 3)
   const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
-  const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;
+  const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;  // the reference's partial rows
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     const uint32_t row = row0 + wm * WTM + i * 32 + l32;
@@ -447,11 +477,76 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   }
 }
 
+// Sum of the split-K partial planes, then the epilogue of the GEMM (scale, bias, GELU, accumulate, output
+// type): one thread per 4 consecutive outputs of a row, slices added in slice order.
+template <int YT>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
+  const uint32_t groups = (a.n + 3) / 4;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)a.m * groups) return;
+  const uint32_t row = (uint32_t)(idx / groups), c0 = (uint32_t)(idx % groups) * 4;
+  const size_t plane = (size_t)a.m * a.n;
+  const float* p = a.part + (size_t)row * a.n + c0;
+  const bool full = c0 + 3 < a.n;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (full && (a.n & 3u) == 0u) {
+    // up to 8 slices' loads in flight at once, added in slice order
+    for (uint32_t z0 = 0; z0 < a.rsplits; z0 += 8) {
+      f32x4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (z0 + u < a.rsplits) t[u] = *(const f32x4*)(p + (z0 + u) * plane);
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (z0 + u < a.rsplits)
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] += t[u][e];
+    }
+  } else {
+    for (uint32_t z = 0; z < a.rsplits; z++, p += plane)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (c0 + e < a.n) v[e] += p[e];
+  }
+  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
+  const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
+  const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    float t = v[e] * a.scale;
+    if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
+    if (gelu) t = gelu_tanh(t);
+    v[e] = t;
+  }
+  const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride;
+  if (a.vec_store && full) {
+    store4<YT>(a, yrow + c0, v, accum);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], accum);
+  }
+}
+
 template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S, bool PP = false>
 static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
   a.tiles_n = (a.n + BN - 1) / BN;
   const dim3 grid(a.tiles_m * a.tiles_n, splits), block(WM * WN * 64);
+  if (a.rsplits > 1) {
+    // slices store raw f32 sums (the output type does not matter to them), then one reduce pass
+    hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32, PP>), grid, block, 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t threads = (size_t)a.m * ((a.n + 3) / 4);
+    const dim3 rg((unsigned)((threads + 255) / 256));
+    switch (a.y_dtype) {
+      case F32: hipLaunchKernelGGL(splitk_reduce_kernel<F32>, rg, dim3(256), 0, s, a); break;
+      case F16: hipLaunchKernelGGL(splitk_reduce_kernel<F16>, rg, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, rg, dim3(256), 0, s, a); break;
+    }
+    return hipGetLastError();
+  }
   switch (a.y_dtype) {
     case F32: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32, PP>), grid, block, 0, s, a); break;
     case F16: hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F16, PP>), grid, block, 0, s, a); break;
@@ -474,29 +569,102 @@ static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg,
   }
 }
 
-// Returns hipErrorNotSupported when the shape / dtypes / alignment are not for this path.
-hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
+namespace {
+
+// Do the operands qualify for the fast path? (16-bit activations, fp8 or matching 16-bit weights, 16-byte
+// aligned rows, K a multiple of 16, operand extents under the 32-bit buffer offsets.)
+bool fast_supported(const GemmLaunch& L, uint32_t kc) {
   const bool f16 = L.x_dtype == F16;
-  if (!(L.x_dtype == BF16 || L.x_dtype == F16)) return hipErrorNotSupported;
-  if (!(L.w_dtype == FP8 || (f16 ? L.w_dtype == F16 : L.w_dtype == BF16))) return hipErrorNotSupported;
-  const uint32_t splits = L.splits < 1 ? 1 : L.splits;
-  const uint32_t kc = splits > 1 ? L.kc : L.k;
+  if (!(L.x_dtype == BF16 || L.x_dtype == F16)) return false;
+  if (!(L.w_dtype == FP8 || (f16 ? L.w_dtype == F16 : L.w_dtype == BF16))) return false;
   const int wb = L.w_dtype == FP8 ? 1 : 2;
-  if (L.k % 16 || kc % 16) return hipErrorNotSupported;
+  if (L.k % 16 || kc % 16) return false;
   if (((uintptr_t)L.x + (uint64_t)L.x_offset * 2) % 16 || ((uintptr_t)L.w + (uint64_t)L.w_offset * wb) % 16 ||
       (L.x_stride * 2) % 16 || (L.w_stride * wb) % 16)
-    return hipErrorNotSupported;
+    return false;
   const uint64_t xb = L.k ? ((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2 : 0;
   const uint64_t wbytes = L.k ? ((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb : 0;
-  if (xb >= kInvalid || wbytes >= kInvalid) return hipErrorNotSupported;
+  return xb < kInvalid && wbytes < kInvalid;
+}
+
+constexpr uint32_t kCUs = 256;
+
+// Tile shape by predicted occupancy. A 256 x 256 tile (one per CU) is the fastest per FLOP when its tiles
+// fill whole waves of the 256 CUs; 128 x 128 tiles (two per CU) lose ~4% per tile but quantize 4x finer;
+// 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
+// faster layout for the DiT shapes (M = 512 .. 4096, N = 3072 .. 12288, K = 3072 / 12288).
+int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits) {
+  if (m <= 32) return GEMM_CFG_32x64;
+  if (m <= 64) return GEMM_CFG_64x64;
+  struct Cand {
+    int cfg;
+    uint32_t bm, bn, per_cu;
+    double base;
+  };
+  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_128x128, 128, 128, 2, 0.96},
+                        {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
+  int best = GEMM_CFG_128x128;
+  double best_score = -1.0;
+  for (const Cand& c : cands) {
+    if (c.bm == 256 && m < 256) continue;
+    const uint64_t tiles = (uint64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * splits;
+    const uint64_t slots = (uint64_t)kCUs * c.per_cu;
+    const uint64_t waves = (tiles + slots - 1) / slots;
+    const double score = c.base * (double)tiles / (double)(waves * slots);
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = c.cfg;
+    }
+  }
+  return best;
+}
+
+uint32_t cfg_bm(int cfg) {
+  return cfg == GEMM_CFG_32x64 ? 32 : cfg == GEMM_CFG_64x64 ? 64 : cfg == GEMM_CFG_128x128 ? 128 : 256;
+}
+uint32_t cfg_bn(int cfg) {
+  return cfg == GEMM_CFG_256x256 ? 256 : cfg == GEMM_CFG_256x128 || cfg == GEMM_CFG_128x128 ? 128 : 64;
+}
+
+}  // namespace
+
+GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits) {
+  GemmReducePlan p{1, L.k, 0};
+  if (L.generic || (L.splits > 1) || (L.flags & WE_EPI_SPLIT_K_BIT) || L.m == 0 || L.n == 0) return p;
+  if (L.m > 64 || L.k < 512 || !fast_supported(L, L.k)) return p;
+  const int cfg = L.cfg >= 0 ? L.cfg : pick_fast_cfg(L.m, L.n, 1);
+  const uint64_t tiles = (uint64_t)((L.m + cfg_bm(cfg) - 1) / cfg_bm(cfg)) * ((L.n + cfg_bn(cfg) - 1) / cfg_bn(cfg));
+  if (tiles >= kCUs / 2) return p;
+  uint32_t rs = (uint32_t)((kCUs + tiles - 1) / tiles);  // about one workgroup per CU (measured: 4 .. 12 slices
+                                                          // of M = 64, K = 3072 within 2%)
+  rs = rs < L.k / 256 ? rs : L.k / 256;                        // every slice keeps at least 256 of K
+  if (force_splits) rs = force_splits < L.k / BK ? force_splits : L.k / BK;
+  if (rs < 2) return p;
+  const uint32_t kc = (L.k + rs * BK - 1) / (rs * BK) * BK;
+  const uint32_t n_slices = (L.k + kc - 1) / kc;
+  if (n_slices < 2) return p;
+  p.rsplits = n_slices;
+  p.rkc = kc;
+  p.scratch_bytes = (size_t)n_slices * L.m * L.n * 4;
+  return p;
+}
+
+// Returns hipErrorNotSupported when the shape / dtypes / alignment are not for this path.
+hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
+  const bool reduce = L.rsplits > 1;
+  const uint32_t splits = reduce ? L.rsplits : (L.splits < 1 ? 1 : L.splits);
+  const uint32_t kc = reduce ? L.rkc : (splits > 1 ? L.kc : L.k);
+  if (!fast_supported(L, kc)) return hipErrorNotSupported;
+  const bool f16 = L.x_dtype == F16;
+  const int wb = L.w_dtype == FP8 ? 1 : 2;
   const int yb = L.y_dtype == F32 ? 4 : 2;
   FastArgs a{};
   a.x = (const char*)L.x + (uint64_t)L.x_offset * 2;
   a.w = (const char*)L.w + (uint64_t)L.w_offset * wb;
   a.y = L.y;
   a.bias = L.bias;
-  a.x_bytes = (uint32_t)xb;
-  a.w_bytes = (uint32_t)wbytes;
+  a.x_bytes = L.k ? (uint32_t)(((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2) : 0;
+  a.w_bytes = L.k ? (uint32_t)(((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb) : 0;
   a.m = L.m;
   a.n = L.n;
   a.k = L.k;
@@ -512,11 +680,12 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
                  ((uint64_t)L.y_stride * yb) % (4 * yb) == 0)
                     ? 1u
                     : 0u;
-  // Tile choice measured on MI355X at M = 4096: 256 x 256 tiles with the ping-pong schedule, for fp8 and
-  // 16-bit weights alike (also for N = 3072, where 192 tiles leave CUs idle but each tile streams
-  // K = 12288 at full rate).
-  int cfg = L.cfg >= 0 ? L.cfg : pick_gemm_cfg(L.m, L.n, splits);
-  if (L.cfg < 0 && L.m >= 256 && L.n >= 256) cfg = GEMM_CFG_256x256;
+  if (reduce) {
+    if (!L.scratch) return hipErrorInvalidValue;
+    a.part = (float*)L.scratch;
+    a.rsplits = splits;
+  }
+  const int cfg = L.cfg >= 0 ? L.cfg : pick_fast_cfg(L.m, L.n, splits);
   if (f16) {
     if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, stream);
     return launch_fast_types<true, F16>(a, splits, cfg, stream);

@@ -26,8 +26,20 @@ struct GemmLaunch {
   uint32_t flags;
   int cfg;      // -1: pick by shape
   int generic;  // 1: skip the fast path (tests of the general kernel)
+  // split-K for small M: K in rsplits slices of rkc, partial sums in scratch (rsplits * m * n f32), then a
+  // reduce pass that runs the epilogue
+  uint32_t rsplits, rkc;
+  void* scratch;
 };
 hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream);
+
+// The split-K plan of a launch on the fast path: rsplits > 1 when the output tiles alone would leave most
+// CUs idle (small M); the scratch it needs, in bytes.
+struct GemmReducePlan {
+  uint32_t rsplits, rkc;
+  size_t scratch_bytes;
+};
+GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits = 0);  // force_splits: sweeps
 // The straight-line fast path; hipErrorNotSupported when the operands do not qualify.
 hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream);
 int pick_gemm_cfg(uint32_t m, uint32_t n, uint32_t splits);

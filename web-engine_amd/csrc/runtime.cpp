@@ -39,6 +39,8 @@ struct we_ctx {
   uint64_t created = 0, reused = 0, created_bytes = 0;
   std::vector<hipEvent_t> tickets;
   uint64_t next_ticket = 1;
+  void* scratch = nullptr;  // kernel scratch (split-K partial sums), grown on demand
+  size_t scratch_bytes = 0;
   hipDeviceProp_t prop{};
 };
 
@@ -67,6 +69,26 @@ int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
     hipError_t e_ = (call);                         \
     if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
   } while (0)
+
+// Scratch for kernels of this context (split-K partial sums), at least `bytes`. Calls are ordered on the
+// compute stream, so one buffer serves them all; growing it waits for the work that may still read it.
+int ensure_scratch(we_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return WE_OK;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  if (ctx->scratch) {
+    HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+    HIP_OK(ctx, hipFree(ctx->scratch), "hipFree scratch");
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+  }
+  const size_t want = ((bytes < (16u << 20) ? (16u << 20) : bytes) + 4095) / 4096 * 4096;
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
+  ctx->scratch = p;
+  ctx->scratch_bytes = want;
+  return WE_OK;
+}
 
 size_t round_size(size_t bytes) { return ((bytes < 4 ? 4 : bytes) + 255) / 256 * 256; }
 
@@ -149,6 +171,7 @@ int we_ctx_destroy(we_ctx* ctx) {
   if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
   for (auto& kv : ctx->pinned) (void)hipHostFree((void*)kv.first);
   for (auto& e : ctx->tickets)
     if (e) (void)hipEventDestroy(e);
@@ -494,6 +517,21 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
   if (force && *force) L.cfg = atoi(force);
   const char* path = getenv("WE_GEMM_PATH");
   L.generic = (path && strcmp(path, "generic") == 0) ? 1 : 0;
+  L.rsplits = 1;
+  L.rkc = L.k;
+  L.scratch = nullptr;
+  const char* split_env = getenv("WE_GEMM_SPLITK");  // "off", or a slice count for sweeps
+  if (!(split_env && strcmp(split_env, "off") == 0)) {
+    const uint32_t force = split_env ? (uint32_t)strtoul(split_env, nullptr, 10) : 0u;
+    const we::GemmReducePlan rp = we::gemm_reduce_plan(L, force);
+    if (rp.rsplits > 1) {
+      const int rc = ensure_scratch(ctx, rp.scratch_bytes);
+      if (rc) return rc;
+      L.rsplits = rp.rsplits;
+      L.rkc = rp.rkc;
+      L.scratch = ctx->scratch;
+    }
+  }
   hipError_t e = we::gemm_launch(L, ctx->compute);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
   return WE_OK;
