@@ -21,6 +21,9 @@
 //     the other buffer; one barrier per tile.
 // f32 kernel (reference f32 API, 32x32x2 f32 MFMA, exact f32 products): same work split, a single LDS
 // buffer, P kept in f32.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "internal.h"
 
@@ -69,6 +72,98 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi, std::true_type /*f
 }
 __device__ __forceinline__ uint32_t pack2(float lo, float hi, std::false_type /*bf16*/) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+
+// One 64-key tile for QB blocks of 32 queries of one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// Every K and V^T fragment read from LDS feeds QB MFMAs. ks: the K tile (64 rows of DP values, 16-byte chunks
+// XOR-swizzled by (row >> KSH)); vt: the V^T tile (DP rows of 64 keys, keys in bit-2/3-swapped order, chunks
+// swizzled by (row >> 1) & 7). qw[qb]: first query of block qb; qi[qb]: this lane's query in it.
+template <int DP, bool IS_F16, int QB>
+__device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, const u32x4 (&qf)[QB][DP / 16],
+                                            f32x16 (&o)[QB][DP / 32], float (&m)[QB], float (&l)[QB], uint32_t k0,
+                                            const uint32_t (&qw)[QB], const uint32_t (&qi)[QB], int c, int hf,
+                                            const AttnArgs& a) {
+  constexpr int NCH = DP / 8;
+  constexpr int KSH = NCH == 16 ? 0 : NCH == 8 ? 1 : 2;
+  f32x16 sacc[QB][2];
+  static_for<0, QB>([&](auto Q) { sacc[Q][0] = f32x16{}; sacc[Q][1] = f32x16{}; });
+  static_for<0, 2>([&](auto B) {
+    constexpr int b = B;
+    const int r = 32 * b + c;
+    static_for<0, DP / 16>([&](auto S) {
+      constexpr int s = S;
+      const u32x4 af = *(const u32x4*)(ks + r * DP * 2 + (((2 * s + hf) ^ ((r >> KSH) & (NCH - 1))) << 4));
+      static_for<0, QB>([&](auto Q) { sacc[Q][b] = mfma_32x32x16<IS_F16>(af, qf[Q][s], sacc[Q][b]); });
+    });
+  });
+  u32x4 pf[QB][4];
+  static_for<0, QB>([&](auto Q) {
+    constexpr int qb = Q;
+    // scores in log2 units; keys past the end (or after the query, causal) get -inf
+    float x[32];
+    const bool mask = (k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw[qb]);
+    static_for<0, 32>([&](auto I) {
+      constexpr int i = I, b = i / 16, v = i % 16;
+      x[i] = sacc[qb][b][v] * a.scale_log2;
+      if (mask) {
+        const uint32_t key = k0 + 32 * b + 8 * (v / 4) + 4 * hf + (v % 4);
+        if (key >= a.tokens || (a.causal && key > qi[qb])) x[i] = -__builtin_inff();
+      }
+    });
+    float tmax = x[0];
+    static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
+    tmax = halves_max(tmax);
+    const float mn = fmaxf(m[qb], tmax);
+    const float ms = mn == -__builtin_inff() ? 0.0f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m[qb] - ms);
+    float ps = 0.0f;
+    static_for<0, 4>([&](auto S) {
+      constexpr int s = S;
+      float p[8];
+      static_for<0, 8>([&](auto I) {
+        p[I] = __builtin_amdgcn_exp2f(x[16 * (s / 2) + 8 * (s % 2) + I] - ms);
+        ps += p[I];
+      });
+      static_for<0, 4>([&](auto J) {
+        constexpr int j = J;
+        pf[qb][s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
+      });
+    });
+    l[qb] = l[qb] * alpha + ps;
+    m[qb] = mn;
+    static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
+  });
+  static_for<0, DP / 32>([&](auto D) {
+    constexpr int db = D;
+    const int r = 32 * db + c;
+    static_for<0, 4>([&](auto S) {
+      constexpr int s = S;
+      const u32x4 vf = *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
+      static_for<0, QB>([&](auto Q) { o[Q][db] = mfma_32x32x16<IS_F16>(vf, pf[Q][s], o[Q][db]); });
+    });
+  });
+}
+
+// O = O^T / l for this lane's query, as 16-bit values, 4 consecutive dims per store.
+template <int DP, bool IS_F16>
+__device__ __forceinline__ void attn_store16(const f32x16 (&o)[DP / 32], float l, uint32_t qi, uint32_t h, int hf,
+                                             const AttnArgs& a) {
+  const float inv = 1.0f / halves_sum(l);
+  if (qi >= a.tokens) return;
+  uint16_t* O = (uint16_t*)a.o + (size_t)qi * a.os + (size_t)h * a.dim;
+  static_for<0, DP / 32>([&](auto D) {
+    constexpr int db = D;
+    static_for<0, 4>([&](auto G) {
+      constexpr int g4 = G;
+      const uint32_t d = 32 * db + 8 * g4 + 4 * hf;
+      if (d < a.dim) {
+        const auto tag = std::integral_constant<bool, IS_F16>{};
+        const u32x2 w{pack2(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, tag),
+                      pack2(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv, tag)};
+        *(u32x2*)(O + d) = w;
+      }
+    });
+  });
 }
 
 // ------------------------------------------------------------------------------------ 16-bit kernel
@@ -153,10 +248,12 @@ __global__ void __launch_bounds__(ATT_NT, 2) attn16_kernel(AttnArgs a) {
     }
   };
 
-  f32x16 o[DP / 32];
-  static_for<0, DP / 32>([&](auto D) { o[D] = f32x16{}; });
-  float m = -__builtin_inff(), l = 0.0f;
-  const float sl2 = a.scale_log2;
+  f32x16 o1[1][DP / 32];
+  static_for<0, DP / 32>([&](auto D) { o1[0][D] = f32x16{}; });
+  float m1[1] = {-__builtin_inff()}, l1[1] = {0.0f};
+  const uint32_t qw1[1] = {qw}, qi1[1] = {qi};
+  u32x4 qf1[1][DP / 16];
+  static_for<0, DP / 16>([&](auto S) { qf1[0][S] = qf[S]; });
 
   if (nt > 0) {
     load_tile(0);
@@ -167,86 +264,142 @@ __global__ void __launch_bounds__(ATT_NT, 2) attn16_kernel(AttnArgs a) {
     if (t + 1 < nt) load_tile(t + 1);
     const uint32_t k0 = (uint32_t)t * ATT_BN;
     // a wave whose queries all precede the tile has nothing to add (causal)
-    const bool active = !(a.causal && k0 > qw + 31);
-    if (active) {
+    if (!(a.causal && k0 > qw + 31)) {
       const char* ks = lds + (t & 1) * STAGE;
-      const char* vt = ks + KS_BYTES;
-      f32x16 sacc[2];
-      static_for<0, 2>([&](auto B) {
-        constexpr int b = B;
-        sacc[b] = f32x16{};
-        const int r = 32 * b + c;
-        static_for<0, DP / 16>([&](auto S) {
-          constexpr int s = S;
-          const u32x4 af = *(const u32x4*)(ks + r * DP * 2 + (((2 * s + hf) ^ ((r >> KSH) & (NCH - 1))) << 4));
-          sacc[b] = mfma_32x32x16<IS_F16>(af, qf[s], sacc[b]);
-        });
-      });
-      // scores in log2 units; keys past the end (or after the query, causal) get -inf
-      float x[32];
-      const bool mask = (k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw);
-      static_for<0, 32>([&](auto I) {
-        constexpr int i = I, b = i / 16, v = i % 16;
-        x[i] = sacc[b][v] * sl2;
-        if (mask) {
-          const uint32_t key = k0 + 32 * b + 8 * (v / 4) + 4 * hf + (v % 4);
-          if (key >= a.tokens || (a.causal && key > qi)) x[i] = -__builtin_inff();
-        }
-      });
-      float tmax = x[0];
-      static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
-      tmax = halves_max(tmax);
-      const float mn = fmaxf(m, tmax);
-      const float ms = mn == -__builtin_inff() ? 0.0f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m - ms);
-      float ps = 0.0f;
-      u32x4 pf[4];
-      static_for<0, 4>([&](auto S) {
-        constexpr int s = S;
-        float p[8];
-        static_for<0, 8>([&](auto I) {
-          p[I] = __builtin_amdgcn_exp2f(x[16 * (s / 2) + 8 * (s % 2) + I] - ms);
-          ps += p[I];
-        });
-        static_for<0, 4>([&](auto J) {
-          constexpr int j = J;
-          pf[s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
-        });
-      });
-      l = l * alpha + ps;
-      m = mn;
-      static_for<0, DP / 32>([&](auto D) { o[D] *= alpha; });
-      static_for<0, DP / 32>([&](auto D) {
-        constexpr int db = D;
-        const int r = 32 * db + c;
-        static_for<0, 4>([&](auto S) {
-          constexpr int s = S;
-          const u32x4 vf = *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
-          o[db] = mfma_32x32x16<IS_F16>(vf, pf[s], o[db]);
-        });
-      });
+      attn_tile16<DP, IS_F16, 1>(ks, ks + KS_BYTES, qf1, o1, m1, l1, k0, qw1, qi1, c, hf, a);
     }
     if (t + 1 < nt) store_tile((t + 1) & 1);
     __syncthreads();
   }
+  attn_store16<DP, IS_F16>(o1[0], l1[0], qi, h, hf, a);
+}
 
-  const float inv = 1.0f / halves_sum(l);
-  if (qi < a.tokens) {
-    uint16_t* O = (uint16_t*)a.o + (size_t)qi * a.os + (size_t)h * a.dim;
-    static_for<0, DP / 32>([&](auto D) {
-      constexpr int db = D;
-      static_for<0, 4>([&](auto G) {
-        constexpr int g4 = G;
-        const uint32_t d = 32 * db + 8 * g4 + 4 * hf;
-        if (d < a.dim) {
-          const auto tag = std::integral_constant<bool, IS_F16>{};
-          const u32x2 w{pack2(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, tag),
-                        pack2(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv, tag)};
-          *(u32x2*)(O + d) = w;
-        }
-      });
-    });
+// ------------------------------------------------------------------------------------ V^T for the DMA path
+// VT[g][d][p] = V[key(p)][g][d], key(p) = p with bits 2 and 3 swapped inside its group of 16 (the order the
+// tile update reads V^T in), zero past the last token; p < tp (tokens rounded up to 64). One workgroup
+// moves 64 positions x 128 dims of one kv head through LDS.
+__global__ void __launch_bounds__(256) attn_vt_kernel(const uint16_t* v, uint32_t vs, uint32_t tokens, uint32_t tp,
+                                                      uint16_t* vt) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][136];
+  const int tid = threadIdx.x;
+  const uint32_t p0 = blockIdx.x * 64, g = blockIdx.y;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int idx = tid + 256 * i, r = idx >> 4, ch = idx & 15;
+    const uint32_t p = p0 + r;
+    const uint32_t key = (p & ~15u) | (p & 3u) | ((p & 4u) << 1) | ((p & 8u) >> 1);
+    u32x4 val = u32x4{0u, 0u, 0u, 0u};
+    if (key < tokens) val = *(const u32x4*)(v + (size_t)key * vs + (size_t)g * 128 + ch * 8);
+    *(u32x4*)&tile[r][ch * 8] = val;
   }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int idx = tid + 256 * i, d = idx >> 3, ch = idx & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) w[e] = (uint32_t)tile[ch * 8 + 2 * e][d] | ((uint32_t)tile[ch * 8 + 2 * e + 1][d] << 16);
+    *(u32x4*)(vt + ((size_t)g * 128 + d) * tp + p0 + ch * 8) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// ------------------------------------------------------------------------------------ 16-bit, DMA ring
+// Head dim 128. A workgroup owns 256 queries: 8 waves of 32 (QB = 1, two waves per SIMD). QB = 2 (4 waves of
+// 64, each K and V^T fragment feeding two MFMAs) needs more than 256 VGPRs and spills; measured 2.5x slower,
+// it is not launched. K tiles and V^T tiles (from attn_vt_kernel) reach LDS
+// through direct-to-LDS loads into a 3-stage ring: the tile two ahead is issued right after the barrier that
+// opens each tile, so its latency is hidden behind two tiles of MFMAs, with no staging registers.
+constexpr int DMA_BM = 256;
+constexpr int DMA_NS = 3;
+typedef __attribute__((address_space(3))) void att_lds_t;
+constexpr uint32_t kAttInvalid = 0x80000000u;
+
+template <bool IS_F16, int QB>
+__global__ void __launch_bounds__(512 / QB, 1) attn_dma_kernel(AttnArgs a, const uint16_t* vtg, uint32_t tp,
+                                                               uint32_t kv_heads) {
+  constexpr int DP = 128;
+  constexpr int NW = 8 / QB;                 // waves
+  constexpr int IPW = 16 / NW;               // load instructions per wave per tile, each of K and V^T
+  constexpr int KS_BYTES = ATT_BN * DP * 2;  // 16 KB
+  constexpr int STAGE = 2 * KS_BYTES;        // K + V^T
+  __shared__ __attribute__((aligned(1024))) char lds[DMA_NS * STAGE];
+
+  uint32_t qblk, h;
+  block_coords(a, qblk, h);
+  const uint32_t g = h / a.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hf = lane >> 5;
+  const uint32_t q0 = qblk * DMA_BM;
+  uint32_t qw[QB], qi[QB];
+  static_for<0, QB>([&](auto Q) {
+    qw[Q] = q0 + 32 * QB * wave + 32 * Q;
+    qi[Q] = qw[Q] + c;
+  });
+  const uint16_t* Qp = (const uint16_t*)a.q;
+
+  u32x4 qf[QB][DP / 16];
+  static_for<0, QB>([&](auto Q) {
+    static_for<0, DP / 16>([&](auto S) {
+      constexpr int s = S;
+      const uint32_t d = 16 * s + 8 * hf;
+      qf[Q][s] = u32x4{0, 0, 0, 0};
+      if (qi[Q] < a.tokens) qf[Q][s] = *(const u32x4*)(Qp + (size_t)qi[Q] * a.qs + (size_t)h * DP + d);
+    });
+  });
+
+  const uint32_t kv_end = a.causal ? min(a.tokens, q0 + DMA_BM) : a.tokens;
+  const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
+  const uint32_t k_bytes = ((a.tokens - 1) * a.ks + kv_heads * DP) * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.k, (short)0, (int)k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vtg, (short)0, (int)(kv_heads * DP * tp * 2), 0x00020000);
+  // instruction j (0 .. 15) fills K rows 4j .. 4j + 3, or V^T rows 8j .. 8j + 7; wave w issues j = w + NW u
+  auto issue = [&](int t, int stage) {
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    char* base = lds + stage * STAGE;
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ (row & 15);
+      const uint32_t key = k0 + row;
+      const uint32_t off = key < a.tokens ? (key * a.ks + g * DP + logical * 8) * 2 : kAttInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (att_lds_t*)(base + j * 1024), 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 8 * j + (lane >> 3), phys = lane & 7, logical = phys ^ ((row >> 1) & 7);
+      const uint32_t off = ((g * DP + row) * tp + k0 + logical * 8) * 2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (att_lds_t*)(base + KS_BYTES + j * 1024), 16, off, 0, 0, 0);
+    }
+  };
+
+  f32x16 o[QB][DP / 32];
+  float m[QB], l[QB];
+  static_for<0, QB>([&](auto Q) {
+    static_for<0, DP / 32>([&](auto D) { o[Q][D] = f32x16{}; });
+    m[Q] = -__builtin_inff();
+    l[Q] = 0.0f;
+  });
+  if (nt > 0) issue(0, 0);
+  if (nt > 1) issue(1, 1);
+  int st = 0;
+  for (int t = 0; t < nt; t++) {
+    // own loads of tile t done (tile t + 1's 2 IPW may still be in flight), then everyone's
+    if (t + 1 < nt) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // tile t + 2 goes to the stage tile t - 1 used; every wave has finished reading it
+    if (t + 2 < nt) issue(t + 2, st == 0 ? 2 : st - 1);
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    if (!(a.causal && k0 > qw[QB - 1] + 31)) {
+      const char* ks = lds + st * STAGE;
+      attn_tile16<DP, IS_F16, QB>(ks, ks + KS_BYTES, qf, o, m, l, k0, qw, qi, c, hf, a);
+    }
+    st = st == DMA_NS - 1 ? 0 : st + 1;
+  }
+  static_for<0, QB>([&](auto Q) { attn_store16<DP, IS_F16>(o[Q], l[Q], qi[Q], h, hf, a); });
 }
 
 // ------------------------------------------------------------------------------------ f32 kernel
@@ -379,6 +532,14 @@ hipError_t launch_attn(Kern kern, const AttnArgs& a, hipStream_t s) {
 
 }  // namespace
 
+size_t attention_scratch_bytes(const AttnLaunch& L) {
+  if (L.dtype == F32 || L.dim != 128 || L.tokens == 0 || L.heads == 0) return 0;
+  const char* path = getenv("WE_ATTN_PATH");
+  if (path && strcmp(path, "registers") == 0) return 0;
+  const size_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
+  return (size_t)L.kv_heads * 128 * tp * 2;
+}
+
 hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
   if (L.tokens == 0 || L.heads == 0) return hipSuccess;
   AttnArgs a;
@@ -394,9 +555,23 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
   a.ks = L.k_stride;
   a.vs = L.v_stride;
   a.os = L.out_stride;
-  a.nqb = (L.tokens + ATT_BM - 1) / ATT_BM;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)L.dim);
   a.causal = L.causal;
+  if (L.scratch && attention_scratch_bytes(L) > 0) {
+    // head dim 128, 16-bit: V^T pre-pass, then the DMA-ring kernel
+    const uint32_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
+    uint16_t* vt = (uint16_t*)L.scratch;
+    hipLaunchKernelGGL(attn_vt_kernel, dim3(tp / 64, L.kv_heads), dim3(256), 0, s, (const uint16_t*)L.v, L.v_stride,
+                       L.tokens, tp, vt);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    a.nqb = (L.tokens + DMA_BM - 1) / DMA_BM;
+    const dim3 grid(a.nqb * L.heads);
+    if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+    else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+    return hipGetLastError();
+  }
+  a.nqb = (L.tokens + ATT_BM - 1) / ATT_BM;
   const int dp = L.dim <= 32 ? 32 : L.dim <= 64 ? 64 : 128;
   switch (L.dtype) {
     case BF16:

@@ -67,7 +67,10 @@ struct AttnLaunch {
   uint32_t tokens, heads, kv_heads, dim;
   uint32_t q_stride, k_stride, v_stride, out_stride;  // elements between consecutive tokens
   int causal;
+  void* scratch;  // attention_scratch_bytes(L) bytes, or null (the register-staged kernel)
 };
+// Scratch the fast path needs (V^T of a head dim 128, 16-bit attention), 0 when it does not apply.
+size_t attention_scratch_bytes(const AttnLaunch& L);
 hipError_t attention_launch(const AttnLaunch& L, hipStream_t stream);
 
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);

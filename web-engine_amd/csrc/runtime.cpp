@@ -39,7 +39,7 @@ struct we_ctx {
   uint64_t created = 0, reused = 0, created_bytes = 0;
   std::vector<hipEvent_t> tickets;
   uint64_t next_ticket = 1;
-  void* scratch = nullptr;  // kernel scratch (split-K partial sums), grown on demand
+  void* scratch = nullptr;  // kernel scratch (split-K partial sums, attention V^T), grown on demand
   size_t scratch_bytes = 0;
   hipDeviceProp_t prop{};
 };
@@ -70,7 +70,7 @@ int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
     if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
   } while (0)
 
-// Scratch for kernels of this context (split-K partial sums), at least `bytes`. Calls are ordered on the
+// Scratch for kernels of this context (split-K partial sums, attention V^T), at least `bytes`. Calls are ordered on the
 // compute stream, so one buffer serves them all; growing it waits for the work that may still read it.
 int ensure_scratch(we_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return WE_OK;
@@ -621,7 +621,13 @@ int we_attention(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t kv_heads
     if (rc) return rc;
   }
   we::AttnLaunch L{q, k, v, out, dtype, tokens, heads, kv_heads, dim, (uint32_t)qs, (uint32_t)ks, (uint32_t)vs,
-                   (uint32_t)os, causal ? 1 : 0};
+                   (uint32_t)os, causal ? 1 : 0, nullptr};
+  const size_t need = we::attention_scratch_bytes(L);
+  if (need) {
+    const int rc = ensure_scratch(ctx, need);
+    if (rc) return rc;
+    L.scratch = ctx->scratch;
+  }
   hipError_t e = we::attention_launch(L, ctx->compute);
   return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "attention launch");
 }
