@@ -94,6 +94,18 @@ int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done);
 int we_timer_start(we_ctx* ctx);
 int we_timer_stop(we_ctx* ctx, float* ms);
 
+/* ---- HIP graphs of the compute stream: no counterpart in the reference (WebGPU records a command buffer
+ * per submit). For launch-bound loops (decode steps, small GEMMs) and callers that replay a fixed sequence:
+ * we_graph_begin starts capturing the kernels later calls queue on the compute stream; we_graph_end
+ * instantiates them; we_graph_launch replays them in stream order. Between begin and end only kernel-
+ * queuing calls and we_buf_copy are allowed: allocation, host transfers, syncs, tickets and timers fail.
+ * A replay reads and writes the buffers the captured calls named, with their contents at replay time. */
+typedef struct we_graph we_graph;
+int we_graph_begin(we_ctx* ctx);
+int we_graph_end(we_ctx* ctx, we_graph** graph);
+int we_graph_launch(we_ctx* ctx, we_graph* graph);
+int we_graph_destroy(we_ctx* ctx, we_graph* graph);
+
 /* ---- matmul: matmulParams (src/kernels/matmul.ts:198-212) and kSplitFor (src/model/ops.ts:42-45) ---- */
 /* negative stride/offset = the reference's default; fails with "<name> must be a multiple of 4, got v" */
 int we_matmul_params_make(we_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, float scale, int64_t x_stride,

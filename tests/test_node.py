@@ -37,6 +37,8 @@ EXPORTS = {
     "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_rmsnorm": "rmsnorm", "we_rope": "rope",
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
+    "we_graph_begin": "graphBegin", "we_graph_end": "graphEnd", "we_graph_launch": "graphLaunch",
+    "we_graph_destroy": "graphDestroy",
 }
 
 

@@ -40,6 +40,7 @@ struct we_ctx {
   std::vector<hipEvent_t> tickets;
   uint64_t next_ticket = 1;
   void* scratch = nullptr;  // kernel scratch (split-K partial sums, attention V^T), grown on demand
+  bool capturing = false;   // between we_graph_begin and we_graph_end
   size_t scratch_bytes = 0;
   hipDeviceProp_t prop{};
 };
@@ -74,6 +75,8 @@ int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
 // compute stream, so one buffer serves them all; growing it waits for the work that may still read it.
 int ensure_scratch(we_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return WE_OK;
+  if (ctx->capturing)
+    return fail(ctx, WE_EINVAL, "scratch must grow to %zu bytes: run the call once before capturing it", bytes);
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   if (ctx->scratch) {
     HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
@@ -168,6 +171,11 @@ int we_ctx_create(int device, we_ctx** out) {
 int we_ctx_destroy(we_ctx* ctx) {
   if (!ctx) return WE_OK;
   (void)hipSetDevice(ctx->device);
+  if (ctx->capturing) {
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(ctx->compute, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+    ctx->capturing = false;
+  }
   if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
@@ -197,6 +205,7 @@ int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units,
 
 int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!out) return fail(ctx, WE_EINVAL, "output pointer is null");
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   const size_t size = round_size(bytes);
@@ -225,6 +234,7 @@ int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
 
 int we_buf_free(we_ctx* ctx, void* buf) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   auto it = ctx->allocs.find((uintptr_t)buf);
   if (it == ctx->allocs.end()) return fail(ctx, WE_EINVAL, "we_buf_free: not a buffer of this context");
   for (size_t i = 0; i < ctx->owned.size(); i++)
@@ -238,6 +248,7 @@ int we_buf_free(we_ctx* ctx, void* buf) {
 
 int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t bytes) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (bytes == 0) return WE_OK;
   if (!src) return fail(ctx, WE_EINVAL, "upload source is null");
   int rc = check_span(ctx, (char*)buf + offset, bytes, "upload destination");
@@ -250,6 +261,7 @@ int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t
 
 int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size_t bytes) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (bytes == 0) return WE_OK;
   if (!dst) return fail(ctx, WE_EINVAL, "download destination is null");
   int rc = check_span(ctx, (const char*)buf + offset, bytes, "download source");
@@ -274,6 +286,7 @@ int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size
 
 int we_mark(we_ctx* ctx, size_t* mark) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!mark) return fail(ctx, WE_EINVAL, "output pointer is null");
   *mark = ctx->owned.size();
   return WE_OK;
@@ -281,6 +294,7 @@ int we_mark(we_ctx* ctx, size_t* mark) {
 
 int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (mark > ctx->owned.size()) return fail(ctx, WE_EINVAL, "mark %zu is past the %zu live buffers", mark, ctx->owned.size());
   std::vector<void*> later(ctx->owned.begin() + (long)mark, ctx->owned.end());
   ctx->owned.resize(mark);
@@ -303,6 +317,7 @@ int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created
 
 int we_sync(we_ctx* ctx) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
   HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "compute stream");
@@ -313,6 +328,7 @@ int we_sync(we_ctx* ctx) {
 
 int we_host_alloc(we_ctx* ctx, size_t bytes, void** out) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!out) return fail(ctx, WE_EINVAL, "output pointer is null");
   void* p = nullptr;
   hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
@@ -324,6 +340,7 @@ int we_host_alloc(we_ctx* ctx, size_t bytes, void** out) {
 
 int we_host_free(we_ctx* ctx, void* ptr) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   auto it = ctx->pinned.find((uintptr_t)ptr);
   if (it == ctx->pinned.end()) return fail(ctx, WE_EINVAL, "we_host_free: not pinned memory of this context");
   HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
@@ -334,6 +351,7 @@ int we_host_free(we_ctx* ctx, void* ptr) {
 
 int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!ticket) return fail(ctx, WE_EINVAL, "output pointer is null");
   int rc = check_span(ctx, dst, bytes, "stream destination");
   if (rc) return rc;
@@ -354,6 +372,7 @@ int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes,
 
 int we_wait_ticket(we_ctx* ctx, uint64_t ticket) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   int rc = ticket_valid(ctx, ticket);
   if (rc) return rc;
   HIP_OK(ctx, hipStreamWaitEvent(ctx->compute, ticket_event(ctx, ticket), 0), "hipStreamWaitEvent");
@@ -362,12 +381,14 @@ int we_wait_ticket(we_ctx* ctx, uint64_t ticket) {
 
 int we_record_compute(we_ctx* ctx, uint64_t* ticket) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!ticket) return fail(ctx, WE_EINVAL, "output pointer is null");
   return new_ticket(ctx, ctx->compute, ticket);
 }
 
 int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!done) return fail(ctx, WE_EINVAL, "output pointer is null");
   int rc = ticket_valid(ctx, ticket);
   if (rc) return rc;
@@ -378,14 +399,66 @@ int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
   return WE_OK;
 }
 
+struct we_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+int we_graph_begin(we_ctx* ctx) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "a graph is already being captured");
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipStreamBeginCapture(ctx->compute, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  ctx->capturing = true;
+  return WE_OK;
+}
+
+int we_graph_end(we_ctx* ctx, we_graph** graph) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!graph) return fail(ctx, WE_EINVAL, "output pointer is null");
+  if (!ctx->capturing) return fail(ctx, WE_EINVAL, "no graph is being captured");
+  ctx->capturing = false;
+  hipGraph_t g = nullptr;
+  HIP_OK(ctx, hipStreamEndCapture(ctx->compute, &g), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_fail(ctx, e, "hipGraphInstantiate");
+  }
+  *graph = new we_graph{g, exec};
+  return WE_OK;
+}
+
+int we_graph_launch(we_ctx* ctx, we_graph* graph) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!graph) return fail(ctx, WE_EINVAL, "graph is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  HIP_OK(ctx, hipGraphLaunch(graph->exec, ctx->compute), "hipGraphLaunch");
+  return WE_OK;
+}
+
+int we_graph_destroy(we_ctx* ctx, we_graph* graph) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!graph) return WE_OK;
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  (void)hipGraphExecDestroy(graph->exec);
+  (void)hipGraphDestroy(graph->graph);
+  delete graph;
+  return WE_OK;
+}
+
 int we_timer_start(we_ctx* ctx) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   HIP_OK(ctx, hipEventRecord(ctx->t0, ctx->compute), "hipEventRecord");
   return WE_OK;
 }
 
 int we_timer_stop(we_ctx* ctx, float* ms) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (!ms) return fail(ctx, WE_EINVAL, "output pointer is null");
   HIP_OK(ctx, hipEventRecord(ctx->t1, ctx->compute), "hipEventRecord");
   HIP_OK(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");

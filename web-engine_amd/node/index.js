@@ -139,6 +139,23 @@ class Graph {
   recordCompute() {
     return addon.recordCompute(this.ctx);
   }
+
+  // ---- HIP graphs of the compute stream: capture a fixed sequence of graph steps once, replay it
+  graphBegin() {
+    addon.graphBegin(this.ctx);
+  }
+
+  graphEnd() {
+    return addon.graphEnd(this.ctx);
+  }
+
+  graphLaunch(graph) {
+    addon.graphLaunch(this.ctx, graph);
+  }
+
+  graphDestroy(graph) {
+    addon.graphDestroy(this.ctx, graph);
+  }
 }
 
 /** src/kernels/matmul.ts:198-212: the 13 x u32 Params image, with the same defaults and errors. */

@@ -583,6 +583,43 @@ static napi_value TimerStop(napi_env env, napi_callback_info info) {
   return num(env, ms);
 }
 
+static napi_value GraphBegin(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_graph_begin(ctx));
+}
+
+static napi_value GraphEnd(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  we_graph* g = NULL;
+  int rc = we_graph_end(ctx, &g);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return big(env, g);
+}
+
+static napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  we_graph* g = ptr_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_graph_launch(ctx, g));
+}
+
+static napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  we_graph* g = ptr_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_graph_destroy(ctx, g));
+}
+
 static napi_value LastError(napi_env env, napi_callback_info info) {
   args_t a;
   get_args(env, info, &a, 0);
@@ -609,6 +646,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
       {"timerStart", TimerStart}, {"timerStop", TimerStop},
+      {"graphBegin", GraphBegin}, {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphDestroy", GraphDestroy},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
     napi_value f;

@@ -85,6 +85,10 @@ SIGNATURES = {
     "we_layer_sum": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "we_unpack_fp8": (_I, [_P, _P, _SZ, _P, _P]),
     "we_dequant_int4": (_I, [_P, _P, _P, _U32, _U32, _U32, _P]),
+    "we_graph_begin": (_I, [_P]),
+    "we_graph_end": (_I, [_P, _P]),
+    "we_graph_launch": (_I, [_P, _P]),
+    "we_graph_destroy": (_I, [_P, _P]),
 }
 
 _lib = None
@@ -262,6 +266,21 @@ class Graph:
         d = ctypes.c_int()
         self.check(self.lib.we_ticket_done(self.ctx, ticket, ctypes.byref(d)))
         return bool(d.value)
+
+    # ---- HIP graphs of the compute stream
+    def graph_begin(self):
+        self.check(self.lib.we_graph_begin(self.ctx))
+
+    def graph_end(self):
+        g = ctypes.c_void_p()
+        self.check(self.lib.we_graph_end(self.ctx, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph):
+        self.check(self.lib.we_graph_launch(self.ctx, ctypes.c_void_p(graph)))
+
+    def graph_destroy(self, graph):
+        self.check(self.lib.we_graph_destroy(self.ctx, ctypes.c_void_p(graph)))
 
     # ---- timing
     def timer_start(self):
