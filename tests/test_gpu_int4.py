@@ -104,6 +104,26 @@ def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
     rng = np.random.default_rng(k)
     words, scales, x, _ = make(rng, 1, n, k, 64)
     fast = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
-    monkeypatch.setenv("WE_INT4_GENERIC", "1")
+    monkeypatch.setenv("WE_INT4_PATH", "generic")
     general = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
     assert O.rel_error(fast, general) < 1e-6
+
+
+@pytest.mark.parametrize("m,n,k,group,x_dt", [
+    (2, 80, 256, 64, we.F16), (8, 100, 2304, 64, we.F16), (16, 64, 3584, 64, we.F16), (13, 200, 4096, 128, we.F16),
+    (16, 33, 192, 64, we.BF16), (5, 70, 3072, 256, we.F16), (16, 130, 3584, 64, we.BF16), (1, 96, 1024, 64, we.F16),
+    (4, 64, 18944, 512, we.F16), (9, 190, 64, 64, we.F16)])
+def test_shared_x_kernel_matches_general_kernel(graph, m, n, k, group, x_dt, monkeypatch):
+    """2 <= M <= 16 with 16-bit x runs the shared-x kernel (64 columns per workgroup, x rows and weights
+    through one LDS ring, 16 waves); forced at M = 1 as well here, with ragged N, K of one block up to
+    18944 and scale groups of 64-512. It must match the oracle and the general kernel (same exact products,
+    1e-6 for the summation order)."""
+    rng = np.random.default_rng(m * 100 + k)
+    words, scales, x, ox = make(rng, m, n, k, group, x_dt)
+    want = O.matmul(O.matmul_params(m, n, k, 1.0), ox, x, O.INT4, words, scales=scales, group=group)
+    monkeypatch.setenv("WE_INT4_PATH", "generic")
+    general = run(graph, m, n, k, group, words, scales, x, x_dt, we.F32)
+    monkeypatch.setenv("WE_INT4_PATH", "shared")
+    got = run(graph, m, n, k, group, words, scales, x, x_dt, we.F32)
+    assert O.rel_error(got, want) < 1e-5
+    assert O.rel_error(got, general) < 1e-6

@@ -4,7 +4,8 @@
 // s: f16 [N, K/group]. The per-group scale multiplies the f32 partial sum of that group, so the
 // dequantized value q * s is never rounded to 16 bits.
 //
-// Both kernels are bound by the HBM stream of W (0.5 B per weight). Shared structure:
+// All three kernels are bound by the HBM stream of W (0.5 B per weight). The general and decode kernels
+// share this structure (the shared-x kernel for 2 <= M <= 16 at the end differs in the work split):
 //  * A workgroup of 4 waves owns 16 output columns n and one block of 16 rows m; wave w takes a quarter
 //    of the 64-k blocks (a wavefront-level split-K); the four f32 partial tiles are summed through LDS.
 //    At K = 3584, N = 18944 that is 1184 workgroups / 4736 waves.
@@ -20,8 +21,9 @@
 //    accumulator entries of that block's partial.
 // The general kernel (any M, f32 / f16 / bf16 x) stages all of a wave's weights at once and reads x
 // fragments from global memory two blocks ahead; the decode kernel further down (x fits in LDS) is the
-// one the M = 1 decode shape runs.
+// one the M = 1 decode shape runs; the shared-x kernel runs 2 <= M <= 16 with 16-bit x.
 #include <cstdlib>
+#include <cstring>
 
 #include "common.h"
 #include "internal.h"
@@ -139,6 +141,18 @@ constexpr int INT4_CH = 14;  // 64-k blocks whose weights a wave stages at once 
 constexpr int INT4_XPF = 2;  // blocks of x fragments in flight ahead of the MFMAs
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
+
+// 16-byte direct-to-LDS buffer load issued as inline asm: lane i writes dst + 16 i. The compiler does not
+// see it, so it adds no waits of its own for the LDS it fills (it otherwise waits for every such load in
+// flight before any LDS read it cannot tell apart); the kernels that use it wait with explicit vmcnt
+// counts. The compiler's waits for its own register loads stay correct: it can only undercount the loads
+// in flight after one, which makes a wait stricter. M0 is set here; nothing else in those kernels reads it.
+__device__ __forceinline__ void dma16(const __amdgpu_buffer_rsrc_t& r, void* dst, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"((uint32_t)(uintptr_t)(lds_ptr_t*)dst), "v"(voff), "s"(r)
+               : "memory");
+}
 
 template <int XT>
 __global__ void __launch_bounds__(256) int4_gemv_kernel(Int4Args a) {
@@ -448,6 +462,160 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
   if (row < a.m && col < a.n) int4_store(a, row, col, sum);
 }
 
+// ------------------------------------------------------------------------------------------------------
+// Shared-x kernel (2 <= M <= 16, 16-bit x, K / group <= 64): a workgroup of 8 waves owns 64 columns over
+// ALL of K. The waves walk K in lock step through an NBUF-slot LDS ring; a slot holds one chunk of 4
+// blocks (256 k): the 16 x rows (16 x 512 B, rows >= M read as zeros) and the 64 x 4 weight blocks (four
+// 2 KB images of the decode kernel's layout). x thus crosses L2 -> LDS once per 64 columns.
+// Wave w multiplies column tile w % 4 with the blocks i = w / 4 (mod WPT) of every chunk; the WPT partial
+// tiles of a column tile are summed through LDS at the end. Several waves per tile keep several waves on
+// each SIMD at the decode shapes' 296 workgroups: with one wave per SIMD the dependent LDS read ->
+// unpack -> MFMA chain of every block was exposed.
+// Per chunk the workgroup issues 1024 16-byte loads, 1024 / threads per lane, all direct-to-LDS (out-of-
+// range ones read zeros), so the waits are constants. No load in the loop targets a register (the compiler would
+// add its own, stricter waits for those). The scale tile (64 rows x K / group halves) is staged once.
+// Step ci: wait for chunk ci (own loads), barrier (everyone's loads landed, everyone is done with the slot
+// of chunk ci - 1), issue chunk ci + NBUF - 1 into that slot, then unpack and multiply chunk ci.
+// x rows in a slot: row m at m * 512, 16-byte piece p at position p ^ (m & 15) (conflict-free b128 reads).
+constexpr int SK_XB = 16 * 512;            // x rows of one chunk: 8 KB
+constexpr int SK_WB = 16 * PIPE_CB * 32;   // one column tile's weights per chunk: 2 KB
+constexpr int SK_SMAX = 64 * 64 * 2;       // scale tile: 64 rows x at most 64 groups
+
+constexpr int SK_NBUF = 3;  // ring slots (56 KB of LDS with the scale tile: two workgroups per CU)
+constexpr int SK_WPT = 4;   // waves per column tile (16 per workgroup)
+
+template <int XT>
+__global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args a) {
+  constexpr int WPT = SK_WPT;
+  constexpr bool IS_F16 = XT == F16;
+  constexpr int NT = 256 * WPT;           // threads
+  constexpr int SLOT = SK_XB + 4 * SK_WB;  // 1024 pieces of 16 B
+  constexpr int LPC = SLOT / 16 / NT;      // loads per lane per chunk
+  constexpr int BPW = PIPE_CB / WPT;       // blocks per wave per chunk
+  __shared__ __attribute__((aligned(1024))) char ring[SK_NBUF * SLOT];
+  __shared__ __attribute__((aligned(16))) char ss[SK_SMAX];
+  static_assert(SK_NBUF * SLOT >= 4 * WPT * 64 * 16, "reduction area");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int tile = wave & 3, phase = wave >> 2;
+  const uint32_t n0 = blockIdx.x * 64, nw = n0 + 16 * tile;
+  const uint32_t nblk = a.k / 64;
+  const int nch = (int)((nblk + PIPE_CB - 1) / PIPE_CB);
+  const uint32_t gshift = a.gshift;
+  const uint32_t row_bytes = a.k / 2;
+
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, (int)a.s_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
+
+  // piece P = j NT + tid of a slot: P < 512 are x rows (row P / 32, position P % 32), the rest the four
+  // weight images (tile (P - 512) / 128, rows nw .. nw + 16); whether a load is x or W is wave-uniform
+  uint32_t src[LPC];
+  int blk[LPC];
+#pragma unroll
+  for (int j = 0; j < LPC; j++) {
+    const int P = j * NT + tid;
+    if (P < 512) {
+      const int m = P >> 5, p = (P & 31) ^ (m & 15);
+      src[j] = (uint32_t)m < a.m ? (a.x_offset + m * a.x_stride) * 2 + p * 16 : kInvalid;
+      blk[j] = p >> 3;
+    } else {
+      const int T = (P - 512) >> 7, p = (P - 512) & 127, r = p >> 3, q = (p & 7) ^ (r & 7);
+      const uint32_t row = n0 + 16 * T + r;
+      src[j] = row < a.n ? row * row_bytes + q * 16 : kInvalid;
+      blk[j] = q >> 1;
+    }
+  }
+
+  auto issue = [&](int ci, auto S) {  // chunk ci (possibly past the end) into slot S
+    constexpr int s = decltype(S)::value;
+    const uint32_t c = (uint32_t)ci * PIPE_CB;
+    char* slot = ring + s * SLOT;
+#pragma unroll
+    for (int j = 0; j < LPC; j++) {
+      char* dst = slot + (j * NT + wave * 64) * 16;
+      if (j * NT + wave * 64 < 512) dma16(rx, dst, c + blk[j] < nblk ? src[j] + c * 128 : kInvalid);
+      else dma16(rw, dst, c + blk[j] < nblk ? src[j] + c * 32 : kInvalid);
+    }
+  };
+
+  // scale tile s[n0 .. n0 + 64, :] (contiguous): 16-byte pieces straight to LDS, or halves through
+  // registers on the last column tile (a 16-byte load that straddles the end of the buffer reads nothing)
+  const uint32_t ng = a.k / a.group;
+  const bool s_whole = n0 + 64 <= a.n;
+  constexpr int SH = SK_SMAX / 2 / NT;
+  uint16_t sh[SH];
+  if (s_whole) {
+    if (wave < 8) dma16(rs, ss + wave * 1024, (uint32_t)tid < ng * 8 ? n0 * ng * 2 + tid * 16 : kInvalid);
+  } else {
+#pragma unroll
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + NT * j;
+      sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < 64 * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
+    }
+  }
+  static_for<0, SK_NBUF - 1>([&](auto CI) { issue(decltype(CI)::value, CI); });
+  if (!s_whole) {
+#pragma unroll
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + NT * j;
+      if (i < 64 * ng) *(uint16_t*)(ss + i * 2) = sh[j];
+    }
+  }
+  const char* srow = ss + (16 * tile + l16) * ng * 2;  // visible after the first step's barrier
+
+  const uint32_t x_rd = l16 * 512, x_sw = l16;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto step = [&](int ci, auto S) {
+    constexpr int s = decltype(S)::value;
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((SK_NBUF - 2) * LPC) : "memory");
+    issue(ci + SK_NBUF - 1, std::integral_constant<int, (s + SK_NBUF - 1) % SK_NBUF>{});
+    const uint32_t c = (uint32_t)ci * PIPE_CB;
+    const char* slot = ring + s * SLOT;
+    const char* wsl = slot + SK_XB + tile * SK_WB;
+#pragma unroll
+    for (int ii = 0; ii < BPW; ii++) {
+      const int i = WPT * ii + phase;
+      if (c + i < nblk) {
+        const u32x2 wq2 = *(const u32x2*)(wsl + l16 * 128 + (((2 * i + (g >> 1)) ^ (l16 & 7)) * 16) + (g & 1) * 8);
+        f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const u32x4 xa = *(const u32x4*)(slot + x_rd + (((8 * i + 2 * g + e) ^ x_sw) * 16));
+          const u32x4 wf = IS_F16 ? int4x8_to_f16(wq2[e], 0x00f0000fu) : int4x8_to_bf16(wq2[e]);
+          part = mfma16<IS_F16>(xa, wf, part);
+        }
+        acc += part * f16_to_f32(*(const uint16_t*)(srow + ((c + i) >> gshift) * 2));
+      }
+    }
+  };
+  for (int ci = 0; ci < nch; ci += SK_NBUF) {
+    static_for<0, SK_NBUF>([&](auto S) {
+      if (ci + decltype(S)::value < nch) step(ci + decltype(S)::value, S);
+    });
+  }
+  // the ring's last loads (chunks past the end, zeros) land before the ring is reused for the sums
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // lane l of wave (tile, phase) holds column nw + l % 16, rows 4 (l / 16) + (0..3), summed over the
+  // blocks of its phase; it stores rows 4 (l / 16) + (4 / WPT) phase + .. of the sum over all phases
+  f32x4_t* red = (f32x4_t*)ring;  // [4 WPT waves][64 lanes]
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  const uint32_t col = nw + l16;
+#pragma unroll
+  for (int rr = 0; rr < 4 / WPT; rr++) {
+    const int r = (4 / WPT) * phase + rr;
+    const uint32_t row = 4 * g + r;
+    float sum = 0.0f;
+#pragma unroll
+    for (int p = 0; p < WPT; p++) sum += red[(tile + 4 * p) * 64 + lane][r];
+    if (row < a.m && col < a.n) int4_store(a, row, col, sum);
+  }
+}
+
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   const int xb = L.x_dtype == F32 ? 4 : 2;
   const uint64_t x_need = L.k ? ((uint64_t)L.x_offset + (uint64_t)(L.m - 1) * L.x_stride + L.k) * xb : 0;
@@ -477,9 +645,17 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   uint32_t gshift = 0;
   while ((64u << gshift) < L.group) gshift++;
   a.gshift = gshift;
-  const bool pipe = L.x_dtype != F32 && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.m <= 16 &&
-                    L.k / 64 <= 4 * (uint32_t)PIPE_MAXB && (64u << gshift) == L.group &&
-                    getenv("WE_INT4_GENERIC") == nullptr;
+  // "generic" / "shared" force a kernel (tests, measurements)
+  const char* path = getenv("WE_INT4_PATH");
+  const bool generic = path && !strcmp(path, "generic");
+  const bool ring = L.x_dtype != F32 && L.m <= 16 && (64u << gshift) == L.group && !generic;
+  const bool pipe = ring && !path && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.k / 64 <= 4 * (uint32_t)PIPE_MAXB;
+  if (ring && !pipe && L.k / L.group <= 64) {
+    dim3 gs((L.n + 63) / 64);
+    if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_shared_kernel<F16>, gs, dim3(256 * SK_WPT), 0, stream, a);
+    else hipLaunchKernelGGL(int4_gemv_shared_kernel<BF16>, gs, dim3(256 * SK_WPT), 0, stream, a);
+    return hipGetLastError();
+  }
   if (pipe) {
     if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_pipe_kernel<F16>, grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL(int4_gemv_pipe_kernel<BF16>, grid, dim3(256), 0, stream, a);
