@@ -168,7 +168,7 @@ def test_dtype_matrix(graph, x_dt, w_dt, y_dt):
 
 
 @pytest.mark.parametrize("path", ["fast", "generic"])
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("x_dt,w_dt", [(we.BF16, we.FP8), (we.BF16, we.BF16), (we.F16, we.FP8), (we.F16, we.F16)])
 def test_every_tile_config_with_ragged_edges(graph, cfg, x_dt, w_dt, path):
     """Both kernels (the straight-line fast path and the general one) in every tile shape, with partial

@@ -65,15 +65,6 @@ __device__ __forceinline__ void block_coords(const AttnArgs& a, uint32_t& qb, ui
   h = b / a.nqb;
 }
 
-// two f32 -> two 16-bit values in one word, round to nearest even (v_cvt_pk_bf16_f32 for bf16)
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::true_type /*f16*/) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
-}
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::false_type /*bf16*/) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
-}
-
 // One 64-key tile for QB blocks of 32 queries of one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
 // Every K and V^T fragment read from LDS feeds QB MFMAs. ks: the K tile (64 rows of DP values, 16-byte chunks
 // XOR-swizzled by (row >> KSH)); vt: the V^T tile (DP rows of 64 keys, keys in bit-2/3-swapped order, chunks

@@ -36,6 +36,16 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// two f32 -> two 16-bit values in one word (lo in bits 0-15), round to nearest even; one
+// v_cvt_pk_bf16_f32 for bf16
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::true_type /*f16*/) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, std::false_type /*bf16*/) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+
 // Load / store one value of a storage type as f32.
 template <int DT> __device__ __forceinline__ float load_as_f32(const void* p, size_t i);
 template <> __device__ __forceinline__ float load_as_f32<F32>(const void* p, size_t i) { return ((const float*)p)[i]; }
@@ -120,11 +130,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // PyTorch tanh GELU in the reference's form (src/kernels/elementwise.ts:25-29).
+// GELU, tanh form (src/kernels/elementwise.ts:25-29): 0.5 v (1 + tanh u) with u = sqrt(2/pi) (v + 0.044715 v^3),
+// evaluated as v / (1 + e^(-2u)) (the same function: (1 + tanh u) / 2 = 1 / (1 + e^(-2u))). The exponential is
+// v_exp_f32 (2^x, log2 e folded into the constant) and the reciprocal v_rcp_f32, both within about 1 ulp:
+// 5 VALU ops and 2 transcendentals, no division. It saturates without a clamp: e -> 0 gives v, e -> inf
+// gives -0.
 __device__ __forceinline__ float gelu_tanh(float v) {
-  float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-  u = fminf(fmaxf(u, -15.0f), 15.0f);
-  const float e = __expf(2.0f * u);
-  return 0.5f * v * (1.0f + (e - 1.0f) / (e + 1.0f));
+  constexpr float c = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+  const float p = __builtin_fmaf(v * v, 0.044715f * c, c);                // c (1 + 0.044715 v^2)
+  const float e = __builtin_amdgcn_exp2f(v * p);                         // e^(-2u)
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + __expf(-v)); }
 

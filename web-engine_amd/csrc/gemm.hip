@@ -382,6 +382,7 @@ static hipError_t launch_types(const GemmArgs& a, uint32_t splits, int cfg, hipS
       case GEMM_CFG_256x256:
         if constexpr (big_ok) return launch_cfg<256, 256, 2, 2, AT, BT>(a, splits, stream);
         else return launch_cfg<128, 128, 2, 2, AT, BT>(a, splits, stream);
+      case GEMM_CFG_256x192:  // no 192-column tile here: 256 x 128
       case GEMM_CFG_256x128:
         if constexpr (big_ok) return launch_cfg<256, 128, 2, 2, AT, BT>(a, splits, stream);
         else return launch_cfg<128, 128, 2, 2, AT, BT>(a, splits, stream);

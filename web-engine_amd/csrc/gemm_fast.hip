@@ -105,10 +105,8 @@ __device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float 
         t[e] += YT == BF16 ? bf16_to_f32((uint16_t)h) : f16_to_f32((uint16_t)h);
       }
     }
-    uint32_t hb[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) hb[e] = YT == BF16 ? f32_to_bf16(t[e]) : f32_to_f16(t[e]);
-    *p = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    const std::integral_constant<bool, YT == F16> tag;
+    *p = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
   }
 }
 
@@ -135,10 +133,13 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   constexpr int WB = B8 ? 1 : 2;                  // weight bytes per value
   constexpr int A_BYTES = BM * 128;               // x: BM rows x 64 k x 2 B
   constexpr int B_ROW = 64 * WB;                  // weight row bytes per stage
-  constexpr int B_BYTES = BN * B_ROW;
+  // the weight area is rounded up to whole load rounds of the workgroup; rows past BN load zeros (a
+  // 192-column tile fills 12 of 16 loads)
+  constexpr int B_INS = (BN * B_ROW / 1024 + NW - 1) / NW * NW;
+  constexpr int B_BYTES = B_INS * 1024;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int A_INS = A_BYTES / 1024, B_INS = B_BYTES / 1024;
-  static_assert(A_INS % NW == 0 && B_INS % NW == 0, "stage loads must split evenly over the waves");
+  constexpr int A_INS = A_BYTES / 1024;
+  static_assert(A_INS % NW == 0 && (BN * B_ROW) % 1024 == 0, "stage loads must split evenly over the waves");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && WTM >= 32, "wave tile");
   constexpr int A_PW = A_INS / NW, B_PW = B_INS / NW, L = A_PW + B_PW;  // loads per wave per stage
   constexpr int B_RPI = 1024 / B_ROW;                                     // weight rows per load
@@ -183,7 +184,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     const int r = ins * B_RPI + lane / B_CPR;
     const int c = (lane % B_CPR) ^ (B8 ? swz64(r) : swz128(r));
     const uint32_t col = col0 + r;
-    offb[j] = col < a.n ? (col * a.w_stride * WB + c * 16) : kInvalid;
+    offb[j] = r < BN && col < a.n ? (col * a.w_stride * WB + c * 16) : kInvalid;
     kb8[j] = c * 16 / WB;
   }
 
@@ -563,6 +564,8 @@ static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg,
     // and 16-bit weights
     case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, s);
     case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
+    // 256 x 192 (4 x 2 waves of 64 x 96, ping-pong): 4096 x 3072 outputs are exactly 256 tiles
+    case GEMM_CFG_256x192: return launch_fast_cfg<256, 192, 4, 2, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, s);
     case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
     case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);
     default: return launch_fast_cfg<32, 64, 1, 2, IS_F16, BT, 3>(a, splits, s);
@@ -596,20 +599,26 @@ constexpr uint32_t kCUs = 256;
 int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
   if (m <= 32) return GEMM_CFG_32x64;
   if (m <= 64) return GEMM_CFG_64x64;
-  // 16-bit weights double the B stage: 128 x 128 tiles then fit one per CU and lose to the ping-pong
-  // 256 x 256 tile at every measured shape (4096 x 9216 x 3072 bf16: 347 vs 274 us)
-  if (!w8) return (m >= 256 && n >= 256) ? GEMM_CFG_256x256 : GEMM_CFG_128x128;
+  // score = measured efficiency of the tile shape relative to 256 x 256 at equal occupancy, times the
+  // predicted fraction of workgroup slots busy over the launch (the last round of tiles is partly
+  // empty). Measured on MI355X in one process (fp8, M = 4096, steady clocks): 256 x 192 does ~0.85 of
+  // the work per unit time of 256 x 256 (4096 x 12288 x 3072 + GELU: 274 vs 254 us, 4 rounds vs 3), and
+  // wins where it fills the CUs better (4096 x 9216 x 3072: 207 vs 229 us; 4096 x 3072 x 3072: 71 vs
+  // 73 us; 4096 x 3072 x 12288: 251 vs 252 us).
+  // With 16-bit weights 128 x 128 tiles fit one per CU only and lose to the ping-pong tiles
+  // (4096 x 9216 x 3072 bf16: 347 vs 274 us), so only the two 256-row shapes compete there.
   struct Cand {
     int cfg;
     uint32_t bm, bn, per_cu;
     double base;
   };
-  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_128x128, 128, 128, 2, 0.96},
-                        {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
+  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, 0.85},
+                        {GEMM_CFG_128x128, 128, 128, 2, 0.96}, {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
   int best = GEMM_CFG_128x128;
   double best_score = -1.0;
   for (const Cand& c : cands) {
     if (c.bm == 256 && m < 256) continue;
+    if (!w8 && c.cfg != GEMM_CFG_256x256 && c.cfg != GEMM_CFG_256x192) continue;
     const uint64_t tiles = (uint64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * splits;
     const uint64_t slots = (uint64_t)kCUs * c.per_cu;
     const uint64_t waves = (tiles + slots - 1) / slots;
@@ -626,7 +635,10 @@ uint32_t cfg_bm(int cfg) {
   return cfg == GEMM_CFG_32x64 ? 32 : cfg == GEMM_CFG_64x64 ? 64 : cfg == GEMM_CFG_128x128 ? 128 : 256;
 }
 uint32_t cfg_bn(int cfg) {
-  return cfg == GEMM_CFG_256x256 ? 256 : cfg == GEMM_CFG_256x128 || cfg == GEMM_CFG_128x128 ? 128 : 64;
+  return cfg == GEMM_CFG_256x256   ? 256
+         : cfg == GEMM_CFG_256x192 ? 192
+         : cfg == GEMM_CFG_256x128 || cfg == GEMM_CFG_128x128 ? 128
+                                                               : 64;
 }
 
 }  // namespace

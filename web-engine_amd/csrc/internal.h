@@ -11,7 +11,14 @@
 
 namespace we {
 
-enum GemmCfgId { GEMM_CFG_256x256 = 0, GEMM_CFG_256x128 = 1, GEMM_CFG_128x128 = 2, GEMM_CFG_64x64 = 3, GEMM_CFG_32x64 = 4 };
+enum GemmCfgId {
+  GEMM_CFG_256x256 = 0,
+  GEMM_CFG_256x128 = 1,
+  GEMM_CFG_128x128 = 2,
+  GEMM_CFG_64x64 = 3,
+  GEMM_CFG_32x64 = 4,
+  GEMM_CFG_256x192 = 5
+};
 
 struct GemmLaunch {
   const void* x;
