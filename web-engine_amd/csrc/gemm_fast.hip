@@ -448,6 +448,51 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
   const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;  // the reference's partial rows
+  // Fast path (uniform branch): the wave's whole sub-tile lies inside y, 4-value stores are allowed, and
+  // there is no bias or accumulate: per row one base pointer, stores at constant offsets from it, GELU
+  // chosen outside the loops (the general path below computes every case per value).
+  const uint32_t wrow0 = row0 + wm * WTM, wcol0 = col0 + wn * WTN;
+  if (a.vec_store && !accum && !has_bias && wrow0 + WTM <= a.m && wcol0 + WTN <= a.n) {
+    auto fast = [&](auto GELU) {
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const size_t yrow = (size_t)a.y_offset + (zrow + wrow0 + i * 32 + l32) * (size_t)a.y_stride + wcol0 + 4 * h;
+        if constexpr (YT == F32) {
+          float* p = (float*)a.y + yrow;
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              f32x4 r;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const float t = acc[i][j][4 * q + e] * a.scale;
+                r[e] = decltype(GELU)::value ? gelu_tanh(t) : t;
+              }
+              *(f32x4*)(p + j * 32 + 8 * q) = r;
+            }
+        } else {
+          uint16_t* p = (uint16_t*)a.y + yrow;
+          const std::integral_constant<bool, YT == F16> tag;
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              float t[4];
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                t[e] = acc[i][j][4 * q + e] * a.scale;
+                if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
+              }
+              *(u32x2*)(p + j * 32 + 8 * q) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
+            }
+        }
+      }
+    };
+    if (gelu) fast(std::true_type{});
+    else fast(std::false_type{});
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     const uint32_t row = row0 + wm * WTM + i * 32 + l32;
