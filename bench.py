@@ -220,6 +220,7 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
     t_stream = g.timer_stop() / layers
     g.sync()
     streamer.free()
+    file_read = file_read_rate(layout, host, scales, pinned[0])
     for p in pinned:
         g.host_free(p)
     blk.free()
@@ -230,7 +231,25 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
             "attention_us": attn_ms * 1e3, "attention_tflops": attn_flop / attn_ms / 1e9,
             "weight_bytes_per_block": layout.nbytes, "copy_ms_per_block": t_copy,
             "h2d_gbs": layout.nbytes / t_copy / 1e6, "streamed_ms_per_block": t_stream,
-            "overlap_efficiency": (t_copy + t_comp - t_stream) / min(t_copy, t_comp)}
+            "overlap_efficiency": (t_copy + t_comp - t_stream) / min(t_copy, t_comp), "file_read": file_read}
+
+
+def file_read_rate(layout, host, scales, pinned, threads=8, reps=3):
+    """One block image written as a .safetensors file, then read by the native reader into pinned host memory
+    (fill_from_file): the rate a streamed model is fed at when the file is in the page cache."""
+    import tempfile
+    import weights as W
+    with tempfile.TemporaryDirectory() as d:
+        path = pathlib.Path(d) / "block.safetensors"
+        W.save(path, layout.file_tensors(host, scales, "double_blocks.0."))
+        best = float("inf")
+        with W.read_header(path) as st:
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                layout.fill_from_file(st, "double_blocks.0.", pinned, threads)
+                best = min(best, time.perf_counter() - t0)
+    return {"ms_per_block": best * 1e3, "gbs": layout.nbytes / best / 1e9, "threads": threads,
+            "source": "page cache (file just written)"}
 
 
 def calibration_copy(g, nbytes=256 << 20):

@@ -25,6 +25,9 @@ extern "C" {
 #define WE_ENOMEM 2       /* device or pinned-host allocation failed */
 #define WE_EHIP 3         /* a HIP runtime call failed; message carries hipGetErrorString */
 #define WE_EUNSUPPORTED 4 /* a dtype combination or mode this build does not implement */
+#define WE_EFORMAT 5      /* not a valid .safetensors file; message = the reference's SafetensorsError text */
+#define WE_EIO 6          /* a file could not be opened or read */
+#define WE_ENOTFOUND 7    /* no tensor of that name */
 
 /* dtype tags (activations, weights, outputs) */
 #define WE_F32 0
@@ -158,6 +161,35 @@ int we_layer_sum(we_ctx* ctx, uint32_t tokens, uint32_t layers, uint32_t dim, co
 int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale, float* out);
 int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, uint32_t rows, uint32_t k,
                     uint32_t group, float* out);
+
+/* ---- .safetensors files: readHeader / readTensor (src/weights/safetensors.ts:28-70) ----
+ * we_st_open reads and validates the header (8-byte LE size, JSON object of {dtype, shape, data_offsets}
+ * entries plus optional __metadata__) with the reference's checks and messages: "File is too small to be a
+ * .safetensors file", "Bad header size: n" (over 100,000,000 or past the end), "Header is not valid JSON",
+ * "Header is not an object", "<name>: unknown dtype <d>", "<name>: bad shape", "<name>: bad data_offsets",
+ * "<name>: has n bytes, its shape needs m bytes", "<name>: data goes past the end of the file", "<a> and <b>
+ * overlap" (WE_EFORMAT; we_last_error(NULL)). Tensors are listed in the order the reference's Map holds them;
+ * offsets are absolute file offsets. Nothing but the header is read until we_st_read, which reads bytes
+ * [begin, begin + bytes) of one tensor straight into dst (any host memory, e.g. from we_host_alloc) with up to
+ * `threads` parallel positional reads (0 = 8). A handle is read-only after open: reads may run concurrently.
+ * Strings and shapes returned stay valid until we_st_close. */
+typedef struct we_safetensors we_safetensors;
+typedef struct we_tensor_info {
+  const char* name;
+  const char* dtype; /* "F8_E4M3", "BF16", "F32", ... (DTYPE_BYTES, src/weights/safetensors.ts:8-11) */
+  uint32_t ndim;
+  const uint64_t* shape;
+  uint64_t offset; /* absolute file offset of the first byte */
+  uint64_t size;   /* bytes */
+} we_tensor_info;
+int we_st_open(const char* path, we_safetensors** out);
+int we_st_close(we_safetensors* st);
+int we_st_count(const we_safetensors* st, uint32_t* n);
+int we_st_info(const we_safetensors* st, uint32_t index, we_tensor_info* out);
+int we_st_find(const we_safetensors* st, const char* name, uint32_t* index); /* WE_ENOTFOUND: "Missing tensor <name>" */
+int we_st_metadata_count(const we_safetensors* st, uint32_t* n);             /* the string entries of __metadata__ */
+int we_st_metadata_at(const we_safetensors* st, uint32_t index, const char** key, const char** value);
+int we_st_read(const we_safetensors* st, uint32_t index, uint64_t begin, uint64_t bytes, void* dst, uint32_t threads);
 
 #ifdef __cplusplus
 }

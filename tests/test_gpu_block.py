@@ -278,3 +278,55 @@ def test_streamed_weights_give_the_resident_result(graph):
         for p in pinned:
             graph.host_free(p)
     assert np.array_equal(got, want)
+
+
+def test_blocks_streamed_from_a_file_give_the_resident_result(graph, tmp_path):
+    """Two blocks written to one .safetensors file (prefixes double_blocks.0. / .1.), read by the native reader
+    straight into pinned host memory and streamed through the device slots, equal the same blocks run from
+    resident copies of the in-memory weights, bit for bit."""
+    import weights as W
+    cfg, tt, rows, cols = B.BlockConfig(256, 512, 2, 2, 128, 1e-6), 16, 4, 8
+    ti, H = rows * cols, cfg.hidden
+    rng = np.random.default_rng(8)
+    tvec = graph.buffer(rng.uniform(-.2, .2, 6 * H).astype(np.float32))
+    rope = B.rope_for_image(graph, rows, cols)
+    blk = B.DoubleBlock(graph, cfg, tt, ti, we.BF16)
+    x0t = graph.buffer(O.bf16_rne(rng.standard_normal(tt * H).astype(np.float32)))
+    x0i = graph.buffer(O.bf16_rne(rng.standard_normal(ti * H).astype(np.float32)))
+    hosts = [_layout_weights(graph, cfg, rng) for _ in range(2)]
+    layout = hosts[0][0]
+    tensors = {}
+    for i, (_, host, scales) in enumerate(hosts):
+        tensors.update(layout.file_tensors(host, scales, f"double_blocks.{i}."))
+    W.save(tmp_path / "model.safetensors", tensors)
+
+    def chain(weights_of):
+        xs = [(x0t, x0i)] + [(graph.buffer(tt * H * 2), graph.buffer(ti * H * 2)) for _ in range(2)]
+
+        def compute(i, slot, scales):
+            w_t, w_i = layout.weights(slot, scales)
+            blk.forward(w_t, w_i, xs[i][0], xs[i][1], tvec, rope, xs[i + 1][0], xs[i + 1][1])
+
+        weights_of(compute)
+        return np.concatenate([graph.read(xs[2][0]), graph.read(xs[2][1])])
+
+    def resident(compute):
+        for i, (_, host, scales) in enumerate(hosts):
+            slot = graph.buffer(host)
+            compute(i, slot, scales)
+            graph.sync()
+            graph.free(slot)
+
+    pinned = [graph.host_alloc(layout.nbytes) for _ in hosts]
+    streamer = B.BlockStreamer(graph, layout)
+    try:
+        with W.read_header(tmp_path / "model.safetensors") as st:
+            file_scales = [layout.fill_from_file(st, f"double_blocks.{i}.", p) for i, p in enumerate(pinned)]
+        want = chain(resident)
+        got = chain(lambda compute: streamer.run(pinned, lambda i, slot: compute(i, slot, file_scales[i])))
+    finally:
+        graph.sync()
+        streamer.free()
+        for p in pinned:
+            graph.host_free(p)
+    assert np.array_equal(got, want)

@@ -1,7 +1,8 @@
 """The Node N-API addon (web-engine_amd/node): the binding a TypeScript host of the reference uses.
 
-CPU: the addon loads under `node`, exports one function per entry point of include/we.h, and its host logic
-(matmulParams image and messages, kSplitFor) equals the oracle's.
+CPU: the addon loads under `node`, exports one function per entry point of include/we.h, its host logic
+(matmulParams image and messages, kSplitFor) equals the oracle's, and index.js readHeader / readTensor read
+.safetensors files through the native reader with the reference's messages.
 GPU: tests/node_driver.js runs linear (fp8 + bias, fp8 + GELU, fp8 + LoRA, int4), norm, rotate, attention, the
 elementwise ops and a pinned-host stream copy through the addon; the results are checked here against the
 oracle with the bars of the matching C-ABI tests (test_gpu_matmul, test_gpu_int4, test_gpu_norm_rope,
@@ -38,7 +39,9 @@ EXPORTS = {
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
     "we_graph_begin": "graphBegin", "we_graph_end": "graphEnd", "we_graph_launch": "graphLaunch",
-    "we_graph_destroy": "graphDestroy",
+    "we_graph_destroy": "graphDestroy", "we_st_open": "stOpen", "we_st_close": "stClose", "we_st_count": "stCount",
+    "we_st_info": "stInfo", "we_st_find": "stFind", "we_st_metadata_count": "stMetadataCount",
+    "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead",
 }
 
 
@@ -102,6 +105,43 @@ def test_context_free_errors_throw_with_the_message():
                     'try { a.bufAlloc(null, 16); } catch (e) { r.push(e.message); }'
                     'console.log(JSON.stringify(r));')
     assert got == ["context is null", "context is null"]
+
+
+def test_safetensors_through_the_addon(tmp_path):
+    """readHeader / readTensor from index.js (the native reader) on files written here: tensors, offsets,
+    metadata, bytes (whole, limited, into a caller's array) and the reference's error messages and class."""
+    import weights as W
+    rng = np.random.default_rng(2)
+    big = rng.integers(0, 256, 20 * 1024 * 1024 + 7, dtype=np.uint8)
+    good = tmp_path / "good.safetensors"
+    W.save(good, {"a": ("F8_E4M3", [2, 2], bytes([1, 2, 3, 4])), "b": ("F32", [1], np.float32([1.5]).view(np.uint8)),
+                  "big": ("U8", [big.size], big)}, {"format": "pt"})
+    bad = tmp_path / "bad.safetensors"
+    text = b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}'
+    bad.write_bytes(len(text).to_bytes(8, "little") + text + bytes(4))
+    got = node_eval(
+        'const w = require("./index.js"); const st = w.readHeader(%s); const out = {};'
+        'out.tensors = [...st.tensors.values()]; out.metadata = st.metadata;'
+        'out.a = Array.from(w.readTensor(st, st.tensors.get("a"))); out.a2 = Array.from(w.readTensor(st, st.tensors.get("a"), 2));'
+        'const big = w.readTensor(st, st.tensors.get("big"), undefined, undefined, 8);'
+        'let sum = 0; for (let i = 0; i < big.length; i++) sum = (sum * 31 + big[i]) %% 1000000007; out.sum = sum;'
+        'const dst = new Uint8Array(4); w.readTensor(st, st.tensors.get("b"), undefined, dst);'
+        'out.b = Array.from(new Float32Array(dst.buffer)); st.close();'
+        'try { w.readHeader(%s); } catch (e) { out.err = [e.name, e.message, e instanceof w.SafetensorsError]; }'
+        'try { w.readHeader(%s); } catch (e) { out.missing = e.name; }'
+        'console.log(JSON.stringify(out));' % (json.dumps(str(good)), json.dumps(str(bad)),
+                                               json.dumps(str(tmp_path / "absent"))))
+    st = W.read_header(good)
+    assert got["tensors"] == [dict(name=t.name, dtype=t.dtype, shape=list(t.shape), offset=t.offset, size=t.size, index=i)
+                              for i, t in enumerate(st.tensors.values())]
+    assert got["metadata"] == {"format": "pt"}
+    assert got["a"] == [1, 2, 3, 4] and got["a2"] == [1, 2] and got["b"] == [1.5]
+    s = 0
+    for v in big.tolist():
+        s = (s * 31 + v) % 1000000007
+    assert got["sum"] == s
+    assert got["err"] == ["SafetensorsError", "a: has 4 bytes, its shape needs 8 bytes", True]
+    assert got["missing"] == "Error"
 
 
 # ------------------------------------------------------------------------------------------------ GPU

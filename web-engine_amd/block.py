@@ -236,6 +236,48 @@ class StreamLayout:
                                      views[(s, "norm_k")], views[(s, "table")]))
         return out
 
+    # tensor names of one block in a .safetensors file, after the block's prefix ("double_blocks.7."): per stream
+    # "<txt|img>_" + the name below; fp8 weights carry "<name>.weight" and "<name>.weight_scale" (F32 [1], or
+    # ".scale_weight"), norms [H] / [head_dim] and the modulation table [6, H] any float dtype
+    FILE_NAMES = {"qkv": "attn.qkv", "proj": "attn.proj", "up": "mlp.0", "down": "mlp.2", "norm1": "norm1.weight",
+                  "norm2": "norm2.weight", "norm_q": "attn.norm_q.weight", "norm_k": "attn.norm_k.weight",
+                  "table": "mod.table"}
+    FP8_FIELDS = ("qkv", "proj", "up", "down")
+
+    def _shape(self, name):
+        H, M, hd = self.cfg.hidden, self.cfg.mlp, self.cfg.head_dim
+        return {"qkv": (3 * H, H), "proj": (H, H), "up": (M, H), "down": (H, M), "norm1": (H,), "norm2": (H,),
+                "norm_q": (hd,), "norm_k": (hd,), "table": (6, H)}[name]
+
+    def fill_from_file(self, st, prefix, dst, threads=0):
+        """One block's weights from an open weights.Safetensors into the host image at address `dst` (pinned
+        memory, so the streamer copies them to HBM as they are): fp8 weights are read from the file straight
+        into place, small float tensors are converted to f32. Returns the scales (for `weights`)."""
+        import weights as W
+        scales = {"txt": {}, "img": {}}
+        for s, name, off, nbytes in self.fields:
+            fname = f"{prefix}{s}_{self.FILE_NAMES[name]}"
+            if name in self.FP8_FIELDS:
+                n, k = self._shape(name)
+                scales[s][name] = W.load_linear_fp8(st, fname, n, k, int(dst) + off, threads)
+            else:
+                W.load_floats_into(st, fname, nbytes // 4, int(dst) + off)
+        return scales
+
+    def file_tensors(self, image, scales, prefix):
+        """The tensors of one block image (a uint8 array of nbytes) under the names fill_from_file reads, for
+        weights.save."""
+        out = {}
+        for s, name, off, nbytes in self.fields:
+            fname = f"{prefix}{s}_{self.FILE_NAMES[name]}"
+            data = image[off:off + nbytes]
+            if name in self.FP8_FIELDS:
+                out[fname + ".weight"] = ("F8_E4M3", self._shape(name), data)
+                out[fname + ".weight_scale"] = ("F32", (1,), np.array([scales[s][name]], np.float32).view(np.uint8))
+            else:
+                out[fname] = ("F32", self._shape(name), data)
+        return out
+
     def fill(self, dst, rng, vec_scale=0.3):
         """Random-init weights into a uint8 view `dst` of nbytes: fp8 codes uniform over the 254 finite ones,
         norm weights and tables uniform in +-vec_scale."""

@@ -61,6 +61,14 @@ int fail(we_ctx* ctx, int code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+namespace we {
+void set_no_ctx_error(const char* msg) { g_no_ctx_err = msg; }
+}  // namespace we
+
+namespace {
+
 int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
   return fail(ctx, WE_EHIP, "%s: %s", what, hipGetErrorString(e));
 }

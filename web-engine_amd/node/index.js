@@ -246,9 +246,52 @@ const add = (graph, x, h, n, dtype = F32) => elementwise(graph, OP.ADD, [x, h], 
 const gelu = (graph, x, n, dtype = F32) => elementwise(graph, OP.GELU_TANH, [x], n, 1, dtype);
 const silu = (graph, x, n, dtype = F32) => elementwise(graph, OP.SILU, [x], n, 1, dtype);
 
+// ---- .safetensors files: readHeader / readTensor (src/weights/safetensors.ts:28-70), on a path ----
+// The header is read and checked natively (libwe's we_st_*), with the reference's messages; tensor bytes are
+// read on request, with parallel positional reads, into a Uint8Array or straight into pinned host memory.
+class SafetensorsError extends Error {
+  constructor(message) {
+    super(message);
+    this.name = "SafetensorsError";
+  }
+}
+
+function readHeader(path) {
+  let handle;
+  try {
+    handle = addon.stOpen(path);
+  } catch (e) {
+    if (e.name === "SafetensorsError") throw new SafetensorsError(e.message);
+    throw e;
+  }
+  const tensors = new Map();
+  const n = addon.stCount(handle);
+  for (let i = 0; i < n; i++) {
+    const t = addon.stInfo(handle, i);
+    tensors.set(t.name, { name: t.name, dtype: t.dtype, shape: t.shape, offset: t.offset, size: t.size, index: i });
+  }
+  const metadata = {};
+  const m = addon.stMetadataCount(handle);
+  for (let i = 0; i < m; i++) {
+    const [k, v] = addon.stMetadataAt(handle, i);
+    metadata[k] = v;
+  }
+  return { tensors, metadata, handle, close: () => addon.stClose(handle) };
+}
+
+/** The raw bytes of one tensor, or only its first `limit` bytes; `dst` (a Uint8Array, or a BigInt pinned host
+ * address) receives them when given. */
+function readTensor(st, tensor, limit, dst, threads) {
+  const n = Math.min(limit === undefined ? tensor.size : limit, tensor.size);
+  const out = dst === undefined ? new Uint8Array(n) : dst;
+  addon.stRead(st.handle, tensor.index, 0, n, out, threads || 0);
+  return out;
+}
+
 module.exports = {
   addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP,
   matmulParams, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
+  SafetensorsError, readHeader, readTensor,
   lastError: (graph) => addon.lastError(graph ? graph.ctx : null),
 };

@@ -620,6 +620,176 @@ static napi_value GraphDestroy(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_graph_destroy(ctx, g));
 }
 
+/* ---- .safetensors files: readHeader / readTensor (src/weights/safetensors.ts:28-70) ---- */
+
+/* throws Error(we_last_error(NULL)); a malformed file's error is named SafetensorsError, as the reference's */
+static napi_value st_status(napi_env env, int rc) {
+  if (rc == WE_OK) return undefined(env);
+  napi_value msg, err;
+  napi_create_string_utf8(env, we_last_error(NULL), NAPI_AUTO_LENGTH, &msg);
+  napi_create_error(env, NULL, msg, &err);
+  if (rc == WE_EFORMAT) {
+    napi_value name;
+    napi_create_string_utf8(env, "SafetensorsError", NAPI_AUTO_LENGTH, &name);
+    napi_set_named_property(env, err, "name", name);
+  }
+  napi_throw(env, err);
+  return NULL;
+}
+
+static int str_arg(args_t* a, size_t i, char* buf, size_t cap) {
+  size_t len = 0;
+  if (napi_get_value_string_utf8(a->env, a->argv[i], buf, cap, &len) != napi_ok) {
+    napi_throw_type_error(a->env, NULL, "expected a string");
+    a->bad = 1;
+    return 0;
+  }
+  if (len + 1 >= cap) {
+    napi_throw_range_error(a->env, NULL, "string argument too long");
+    a->bad = 1;
+    return 0;
+  }
+  return 1;
+}
+
+static napi_value str(napi_env env, const char* s) {
+  napi_value v;
+  napi_create_string_utf8(env, s, NAPI_AUTO_LENGTH, &v);
+  return v;
+}
+
+static napi_value StOpen(napi_env env, napi_callback_info info) {
+  args_t a;
+  char path[4096];
+  if (!get_args(env, info, &a, 1) || !str_arg(&a, 0, path, sizeof path)) return NULL;
+  we_safetensors* st = NULL;
+  int rc = we_st_open(path, &st);
+  if (rc != WE_OK) return st_status(env, rc);
+  return big(env, st);
+}
+
+static napi_value StClose(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return st_status(env, we_st_close(st));
+}
+
+static napi_value StCount(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  uint32_t n = 0;
+  int rc = we_st_count(st, &n);
+  if (rc != WE_OK) return st_status(env, rc);
+  return num(env, n);
+}
+
+/* {name, dtype, shape: number[], offset, size} (TensorInfo, src/weights/safetensors.ts:15) */
+static napi_value StInfo(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  uint32_t i = u32_arg(&a, 1);
+  if (a.bad) return NULL;
+  we_tensor_info t;
+  int rc = we_st_info(st, i, &t);
+  if (rc != WE_OK) return st_status(env, rc);
+  napi_value o, shape;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "name", str(env, t.name));
+  napi_set_named_property(env, o, "dtype", str(env, t.dtype));
+  napi_create_array_with_length(env, t.ndim, &shape);
+  for (uint32_t d = 0; d < t.ndim; d++) napi_set_element(env, shape, d, num(env, (double)t.shape[d]));
+  napi_set_named_property(env, o, "shape", shape);
+  napi_set_named_property(env, o, "offset", num(env, (double)t.offset));
+  napi_set_named_property(env, o, "size", num(env, (double)t.size));
+  return o;
+}
+
+static napi_value StFind(napi_env env, napi_callback_info info) {
+  args_t a;
+  char name[4096];
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  if (a.bad || !str_arg(&a, 1, name, sizeof name)) return NULL;
+  uint32_t i = 0;
+  int rc = we_st_find(st, name, &i);
+  if (rc != WE_OK) return st_status(env, rc);
+  return num(env, i);
+}
+
+static napi_value StMetadataCount(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  uint32_t n = 0;
+  int rc = we_st_metadata_count(st, &n);
+  if (rc != WE_OK) return st_status(env, rc);
+  return num(env, n);
+}
+
+static napi_value StMetadataAt(napi_env env, napi_callback_info info) { /* [key, value] */
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  uint32_t i = u32_arg(&a, 1);
+  if (a.bad) return NULL;
+  const char *k = NULL, *v = NULL;
+  int rc = we_st_metadata_at(st, i, &k, &v);
+  if (rc != WE_OK) return st_status(env, rc);
+  napi_value pair;
+  napi_create_array_with_length(env, 2, &pair);
+  napi_set_element(env, pair, 0, str(env, k));
+  napi_set_element(env, pair, 1, str(env, v));
+  return pair;
+}
+
+/* stRead(handle, index, begin, bytes, dst, threads): dst = a BigInt host address (e.g. pinned memory from
+ * hostAlloc) or a TypedArray / Buffer of at least `bytes` bytes */
+static napi_value StRead(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_safetensors* st = ptr_arg(&a, 0);
+  uint32_t idx = u32_arg(&a, 1);
+  double begin = f64_arg(&a, 2), bytes = f64_arg(&a, 3);
+  uint32_t threads = a.argc > 5 && !is_nullish(env, a.argv[5]) ? u32_arg(&a, 5) : 0;
+  if (a.bad) return NULL;
+  if (!(begin >= 0 && bytes >= 0 && begin <= 9007199254740991.0 && bytes <= 9007199254740991.0)) {
+    napi_throw_range_error(env, NULL, "begin and bytes must be non-negative integers");
+    return NULL;
+  }
+  void* dst = NULL;
+  bool is_ta = false;
+  napi_is_typedarray(env, a.argv[4], &is_ta);
+  if (is_ta) {
+    napi_typedarray_type type;
+    size_t length = 0, offset = 0;
+    napi_value ab;
+    void* data = NULL;
+    napi_get_typedarray_info(env, a.argv[4], &type, &length, &data, &ab, &offset);
+    size_t elem = 1;
+    switch (type) {
+      case napi_int16_array: case napi_uint16_array: elem = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+      default: elem = 1;
+    }
+    if ((double)(length * elem) < bytes) {
+      napi_throw_range_error(env, NULL, "destination is smaller than the bytes to read");
+      return NULL;
+    }
+    dst = data;
+  } else {
+    dst = ptr_arg(&a, 4);
+    if (a.bad) return NULL;
+  }
+  return st_status(env, we_st_read(st, idx, (uint64_t)begin, (uint64_t)bytes, dst, threads));
+}
+
 static napi_value LastError(napi_env env, napi_callback_info info) {
   args_t a;
   get_args(env, info, &a, 0);
@@ -647,6 +817,9 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
       {"timerStart", TimerStart}, {"timerStop", TimerStop},
       {"graphBegin", GraphBegin}, {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphDestroy", GraphDestroy},
+      {"stOpen", StOpen},         {"stClose", StClose},       {"stCount", StCount},
+      {"stInfo", StInfo},         {"stFind", StFind},         {"stMetadataCount", StMetadataCount},
+      {"stMetadataAt", StMetadataAt}, {"stRead", StRead},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
     napi_value f;

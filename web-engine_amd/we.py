@@ -31,7 +31,9 @@ DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
 ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
 OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
-ERRORS = {1: "WE_EINVAL", 2: "WE_ENOMEM", 3: "WE_EHIP", 4: "WE_EUNSUPPORTED"}
+ERRORS = {1: "WE_EINVAL", 2: "WE_ENOMEM", 3: "WE_EHIP", 4: "WE_EUNSUPPORTED", 5: "WE_EFORMAT", 6: "WE_EIO",
+          7: "WE_ENOTFOUND"}
+WE_EINVAL = 1
 TILE = 128  # the reference's matmul tile (src/kernels/matmul.ts:33), used by k_split_for
 
 
@@ -89,6 +91,14 @@ SIGNATURES = {
     "we_graph_end": (_I, [_P, _P]),
     "we_graph_launch": (_I, [_P, _P]),
     "we_graph_destroy": (_I, [_P, _P]),
+    "we_st_open": (_I, [ctypes.c_char_p, _P]),
+    "we_st_close": (_I, [_P]),
+    "we_st_count": (_I, [_P, _P]),
+    "we_st_info": (_I, [_P, _U32, _P]),
+    "we_st_find": (_I, [_P, ctypes.c_char_p, _P]),
+    "we_st_metadata_count": (_I, [_P, _P]),
+    "we_st_metadata_at": (_I, [_P, _U32, _P, _P]),
+    "we_st_read": (_I, [_P, _U32, _U64, _U64, _P, _U32]),
 }
 
 _lib = None
