@@ -123,6 +123,15 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
  * two bf16 terms, keeping ~16 mantissa bits). */
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
+/* we_matmul with the gated residual of the reference's gatedAdd (src/kernels/elementwise.ts:52-58, used after the
+ * attention output and MLP down projections, src/model/block.ts:60-64 and :80) fused into the epilogue:
+ *   y = residual + gate[col] * v,  v = the value we_matmul would store (scale, bias, GELU)
+ * gate: f32 [N]; residual: y's dtype and layout (y_offset, y_stride), may be y itself; residual NULL: y = gate * v,
+ * or y += gate * v with WE_EPI_ACCUMULATE. Not with WE_EPI_SPLIT_K. No reference entry point: the reference runs
+ * gatedAdd as its own pass over the GEMM's output. */
+int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                    const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
+                    const float* gate, const void* residual);
 
 /* ---- norms and rotary: rmsnormWgsl (src/kernels/rmsnorm.ts:13-48) / norm() (src/model/ops.ts:78-82),
  * ropeKernel (src/kernels/rope.ts:59-77) / rotate() (src/model/ops.ts:89-93) ---- */

@@ -8,6 +8,7 @@ Tolerances (max|y - ref| / max|ref|, tests/gpu/matmul.test.ts:38-46):
     accumulation rounds);
   * f16 output: 2e-3 (one f16 rounding is 2^-11 of the value);  bf16 output: 1e-2 (2^-8 of the value).
 """
+import ctypes
 import os
 
 import numpy as np
@@ -385,3 +386,101 @@ def test_small_m_split_k_reduction(graph, monkeypatch, m, n, k, x_dt, y_dt, flag
     monkeypatch.setenv("WE_GEMM_SPLITK", "off")
     unsplit = run(graph, p, x_store, x_dt, w, we.FP8, y_dt, flags=flags, bias=bias, y_init=y_init)
     assert O.rel_error(unsplit, want) < tol
+
+
+# ---- gated residual epilogue (we_matmul_gated): gatedAdd (src/kernels/elementwise.ts:52-58) after the GEMM ----
+
+def _store(vals, dt):
+    """f64 values -> (storage of dtype dt, the exact values stored)"""
+    s, exact, _ = encode_act(vals.astype(np.float32), dt)
+    return s, decode(np.ascontiguousarray(s).view(np.uint8), dt)
+
+
+@pytest.mark.parametrize("case", ["fast_full", "fast_ragged", "small_m_split", "generic_f32", "f16_out", "gelu_bias"])
+def test_gated_residual_equals_gemm_then_gated_add(graph, case, monkeypatch):
+    """y = residual + gate * v (v: scale, bias, GELU of the product), against the f64 oracle of the product followed
+    by the reference's gatedAdd, on every epilogue: the fast kernel's whole-tile and per-value paths, the split-K
+    reduce pass (small M), the general kernel (f32 operands) and f16 output."""
+    shapes = {"fast_full": (512, 384, 256, we.BF16, we.FP8, we.BF16), "fast_ragged": (300, 520, 208, we.BF16, we.FP8, we.BF16),
+              "small_m_split": (48, 3072, 3072, we.F16, we.FP8, we.F16), "generic_f32": (70, 90, 128, we.F32, we.F32, we.F32),
+              "f16_out": (256, 256, 192, we.F16, we.F16, we.F16), "gelu_bias": (512, 384, 256, we.BF16, we.FP8, we.BF16)}
+    m, n, k, x_dt, w_dt, y_dt = shapes[case]
+    flags = we.EPI_BIAS | we.EPI_GELU if case == "gelu_bias" else 0
+    rng = np.random.default_rng(len(case))
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    scale = 0.05 if w_dt == we.FP8 else 1.0
+    gate = rng.uniform(-1.5, 1.5, n).astype(np.float32)
+    bias = rng.uniform(-.5, .5, n).astype(np.float32) if flags & we.EPI_BIAS else None
+    res_store, res_vals = _store(rng.standard_normal(m * n), y_dt)
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    mark = graph.mark()
+    xb, wb, gb, rb = graph.buffer(x_store), graph.buffer(w_store), graph.buffer(gate), graph.buffer(res_store)
+    yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
+    bb = graph.buffer(bias) if bias is not None else None
+    if case == "generic_f32":
+        monkeypatch.setenv("WE_GEMM_PATH", "generic")
+    graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=flags, gate=gb, residual=rb)
+    got = decode(graph.read(yb), y_dt)
+    graph.release(mark)
+    v = O.matmul(O.matmul_params(m, n, k, scale), ox, x_oracle, ow, w_oracle).reshape(m, n)
+    if bias is not None:
+        v = v + bias
+    if flags & we.EPI_GELU:
+        v = np.vectorize(O.lib.or_gelu_tanh)(v)
+    want = (res_vals.reshape(m, n) + gate.astype(np.float64) * v).ravel()
+    assert O.rel_error(got, want) < TOL[y_dt], case
+
+
+def test_gated_residual_in_place_and_accumulate(graph):
+    """residual = y (the block's x += gate * proj(...)), and no residual with ACCUMULATE: both equal the gatedAdd
+    of the plain product onto y's old values, bit for bit across the two forms."""
+    m, n, k = 512, 384, 256
+    rng = np.random.default_rng(7)
+    x = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
+    w, _, _ = make_weights(rng, n, k, we.FP8)
+    gate = rng.uniform(-1, 1, n).astype(np.float32)
+    y0, y0_vals = _store(rng.standard_normal(m * n), we.BF16)
+    p = we.matmul_params(m, n, k, 0.05, graph=graph)
+    mark = graph.mark()
+    xb, wb, gb = graph.buffer(x), graph.buffer(w), graph.buffer(gate)
+    y1, y2 = graph.buffer(y0), graph.buffer(y0)
+    graph.matmul(p, we.BF16, xb, we.FP8, wb, we.BF16, y1, gate=gb, residual=y1)
+    graph.matmul(p, we.BF16, xb, we.FP8, wb, we.BF16, y2, flags=we.EPI_ACCUMULATE, gate=gb)
+    a, b = graph.read(y1), graph.read(y2)
+    graph.release(mark)
+    assert np.array_equal(a, b)
+    v = O.matmul(O.matmul_params(m, n, k, 0.05), O.BF16, x, O.FP8, w).reshape(m, n)
+    assert O.rel_error(decode(a, we.BF16), (y0_vals.reshape(m, n) + gate * v).ravel()) < TOL[we.BF16]
+
+
+def test_gated_residual_int4(graph):
+    m, n, k, group = 8, 640, 1024, 64
+    rng = np.random.default_rng(9)
+    words = rng.integers(0, 2 ** 32, n * k // 8, dtype=np.uint64).astype(np.uint32)
+    scales = np.abs(rng.normal(0, 0.01, n * k // group)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(m * k).astype(np.float16)
+    gate = rng.uniform(-1, 1, n).astype(np.float32)
+    res = rng.standard_normal(m * n).astype(np.float32)
+    p = we.matmul_params(m, n, k, 1.0, graph=graph)
+    mark = graph.mark()
+    yb = graph.buffer(m * n * 4)
+    graph.matmul(p, we.F16, graph.buffer(x), we.INT4, graph.buffer(words), we.F32, yb, scales=graph.buffer(scales),
+                 group=group, gate=graph.buffer(gate), residual=graph.buffer(res))
+    got = graph.read(yb).view(np.float32).astype(np.float64)
+    graph.release(mark)
+    v = O.matmul(O.matmul_params(m, n, k, 1.0), O.F16, x.view(np.uint16), O.INT4, words, scales=scales, group=group)
+    want = res.astype(np.float64) + (gate.astype(np.float64) * v.reshape(m, n)).ravel()
+    assert O.rel_error(got, want) < TOL_F32_OUT
+
+
+def test_gated_residual_refusals(graph):
+    p = we.matmul_params(4, 4, 4, 1.0, graph=graph)
+    b = graph.buffer(64)
+    with pytest.raises(we.WeError, match="gate is null"):
+        graph.check(graph.lib.we_matmul_gated(graph.ctx, ctypes.byref(p), we.F32, we._addr(b), we.F32, we._addr(b),
+                                              None, 0, we.F32, we._addr(b), None, 0, None, None))
+    with pytest.raises(we.WeError, match="split-K"):
+        graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, flags=we.EPI_SPLIT_K, gate=b)
+    with pytest.raises(we.WeError, match="residual replaces accumulate"):
+        graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, flags=we.EPI_ACCUMULATE, gate=b, residual=b)

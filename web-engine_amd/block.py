@@ -11,7 +11,8 @@
     q_s, k_s: per-head RMSNorm, then RoPE on the image rows (in place in that buffer)
     o = attention(q, k, v) read straight from the fused rows;  x1_s = x_s + pregate_s * (o_s . proj_s^T)
     out_s = x1_s + postgate_s * down_s(gelu_tanh(up_s(norm2_s(x1_s) * (1 + postscale_s) + postshift_s)))
-  The GELU runs in the up projection's epilogue.
+  The GELU runs in the up projection's epilogue, and both gated residuals in the epilogues of the output
+  projection and the down projection (we_matmul_gated): no elementwise pass touches the residual stream.
 - `BlockStreamer`: src/model/weights.ts:94-131 loads every block before the first step and paces uploads
   with onSubmittedWorkDone; src/gpu/run-ahead.ts:7-21 keeps one block of CPU encoding ahead. Here a block's
   weights live in pinned host memory and are copied on the copy stream into one of two device slots while
@@ -153,13 +154,12 @@ class DoubleBlock:
         self.qkv = graph.buffer(self.tokens * 3 * H * e)
         self.o = graph.buffer(self.tokens * H * e)
         self.h = graph.buffer(big * H * e)
-        self.a = graph.buffer(big * H * e)
         self.u = graph.buffer(big * cfg.mlp * e)
         self.x1 = [graph.buffer(r * H * e) for r in self.rows]
         self.mod = [graph.buffer(6 * H * 4) for _ in self.rows]
 
     def free(self):
-        for b in [self.qkv, self.o, self.h, self.a, self.u] + self.x1 + self.mod:
+        for b in [self.qkv, self.o, self.h, self.u] + self.x1 + self.mod:
             self.graph.free(b)
 
     def forward(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img):
@@ -186,16 +186,17 @@ class DoubleBlock:
                     sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
         for s in range(2):
             w, rows, r0, mod = ws[s], self.rows[s], self.row0[s], self.mod[s]
+            # x1 = x + gate1 * proj(o), the gated residual in the projection's epilogue
             p = we.matmul_params(rows, H, H, w.proj.scale, x_offset=r0 * H, graph=g)
-            g.matmul(p, dt, self.o, we.FP8, w.proj.buffer, dt, self.a)
-            g.elementwise(we.OP_GATED_ADD, rows * H, H, dt, xs[s], self.a, sl(mod, 2 * H * 4, H * 4), self.x1[s])
+            g.matmul(p, dt, self.o, we.FP8, w.proj.buffer, dt, self.x1[s], gate=sl(mod, 2 * H * 4, H * 4),
+                     residual=xs[s])
             g.rmsnorm(rows, H, cfg.eps, 1.0, dt, self.x1[s], w.norm2, sl(mod, 3 * H * 4, H * 4),
                       sl(mod, 4 * H * 4, H * 4), self.h)
             g.matmul(we.matmul_params(rows, cfg.mlp, H, w.up.scale, graph=g), dt, self.h, we.FP8, w.up.buffer, dt,
                      self.u, flags=we.EPI_GELU)
+            # out = x1 + gate2 * down(u), fused likewise
             g.matmul(we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, self.u, we.FP8, w.down.buffer, dt,
-                     self.a)
-            g.elementwise(we.OP_GATED_ADD, rows * H, H, dt, self.x1[s], self.a, sl(mod, 5 * H * 4, H * 4), outs[s])
+                     outs[s], gate=sl(mod, 5 * H * 4, H * 4), residual=self.x1[s])
 
 
 # ------------------------------------------------------------------------------------------ weight streaming

@@ -26,6 +26,8 @@ struct GemmArgs {
   const void* w;
   void* y;
   const float* bias;
+  const float* gate;  // gated residual: y = res + gate[col] * v (res may be y; NULL: none)
+  const void* res;
   uint32_t m, n, k;
   float scale;
   uint32_t x_stride, w_stride, y_stride, x_offset, w_offset, y_offset;
@@ -140,18 +142,15 @@ __device__ __forceinline__ void load_chunk(const void* base, size_t row_off, boo
   }
 }
 
-// One output value: y (= | +=) val in the output dtype.
+// One output value: y = val, y += val (accumulate) or y = res + val (gated residual), in the output dtype.
 __device__ __forceinline__ void store_out(const GemmArgs& a, size_t o, float val) {
-  const bool acc = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
+  const void* add = a.res ? a.res : ((a.flags & WE_EPI_ACCUMULATE_BIT) ? a.y : nullptr);
   if (a.y_dtype == F32) {
-    float* y = (float*)a.y;
-    y[o] = acc ? y[o] + val : val;
+    ((float*)a.y)[o] = add ? ((const float*)add)[o] + val : val;
   } else if (a.y_dtype == BF16) {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_bf16(acc ? bf16_to_f32(y[o]) + val : val);
+    ((uint16_t*)a.y)[o] = f32_to_bf16(add ? bf16_to_f32(((const uint16_t*)add)[o]) + val : val);
   } else {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_f16(acc ? f16_to_f32(y[o]) + val : val);
+    ((uint16_t*)a.y)[o] = f32_to_f16(add ? f16_to_f32(((const uint16_t*)add)[o]) + val : val);
   }
 }
 
@@ -344,12 +343,14 @@ gemm_kernel(GemmArgs a) {
       const uint32_t col = col0 + wn * C::WTN + j * 32 + l32;
       const bool col_ok = col < a.n;
       const float b = (col_ok && (a.flags & WE_EPI_BIAS_BIT)) ? a.bias[col] : 0.0f;
+      const float gt = (col_ok && a.gate) ? a.gate[col] : 1.0f;
       static_for<0, 16>([&](auto V) {
         constexpr int v = decltype(V)::value;
         const uint32_t row = row0 + wm * C::WTM + i * 32 + 8 * (v / 4) + 4 * half + (v % 4);
         if (col_ok && row < a.m) {
           float val = acc[i][j][v] * a.scale + b;
           if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
+          if (a.gate) val *= gt;
           store_out(a, (size_t)a.y_offset + (zrow + row) * (size_t)a.y_stride + col, val);
         }
       });
@@ -427,6 +428,8 @@ hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream) {
   a.w = L.w;
   a.y = L.y;
   a.bias = L.bias;
+  a.gate = L.gate;
+  a.res = L.res;
   a.m = L.m;
   a.n = L.n;
   a.k = L.k;

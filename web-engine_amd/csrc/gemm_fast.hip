@@ -42,6 +42,8 @@ struct FastArgs {
   const void* w;
   void* y;
   const float* bias;
+  const float* gate;  // gated residual: y = res + gate[col] * v (res may be y; NULL: none)
+  const void* res;
   uint32_t x_bytes, w_bytes;  // readable bytes from x / w (their extents)
   uint32_t m, n, k;
   float scale;
@@ -87,18 +89,19 @@ __device__ __forceinline__ u32x2 cvt_fp8x4(uint32_t w) {
   return r;
 }
 
+// y[o .. o + 3] = v, or addend[o ..] + v (addend: the residual, or y itself to accumulate; NULL: none)
 template <int YT>
-__device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float (&v)[4], bool acc) {
+__device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float (&v)[4], const void* addend) {
   if constexpr (YT == F32) {
     f32x4* p = (f32x4*)((float*)a.y + o);
     f32x4 r = {v[0], v[1], v[2], v[3]};
-    if (acc) r += *p;
+    if (addend) r += *(const f32x4*)((const float*)addend + o);
     *p = r;
   } else {
     u32x2* p = (u32x2*)((uint16_t*)a.y + o);
     float t[4] = {v[0], v[1], v[2], v[3]};
-    if (acc) {
-      const u32x2 old = *p;
+    if (addend) {
+      const u32x2 old = *(const u32x2*)((const uint16_t*)addend + o);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const uint32_t h = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
@@ -111,14 +114,15 @@ __device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float 
 }
 
 template <int YT>
-__device__ __forceinline__ void store1(const FastArgs& a, size_t o, float v, bool acc) {
+__device__ __forceinline__ void store1(const FastArgs& a, size_t o, float v, const void* addend) {
   if constexpr (YT == F32) {
-    float* y = (float*)a.y;
-    y[o] = acc ? y[o] + v : v;
+    ((float*)a.y)[o] = addend ? ((const float*)addend)[o] + v : v;
   } else {
-    uint16_t* y = (uint16_t*)a.y;
-    if (acc) v += YT == BF16 ? bf16_to_f32(y[o]) : f16_to_f32(y[o]);
-    y[o] = YT == BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+    if (addend) {
+      const uint16_t h = ((const uint16_t*)addend)[o];
+      v += YT == BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    }
+    ((uint16_t*)a.y)[o] = YT == BF16 ? f32_to_bf16(v) : f32_to_f16(v);
   }
 }
 
@@ -448,17 +452,29 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
   const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;  // the reference's partial rows
+  const void* addend = a.res ? a.res : (accum ? a.y : nullptr);
   // Fast path (uniform branch): the wave's whole sub-tile lies inside y, 4-value stores are allowed, and
-  // there is no bias or accumulate: per row one base pointer, stores at constant offsets from it, GELU
-  // chosen outside the loops (the general path below computes every case per value).
+  // there is no bias; either plain stores or the gated residual (gate and addend both present): per row
+  // one base pointer, stores at constant offsets from it, GELU and gating chosen outside the loops (the
+  // general path below computes every case per value).
   const uint32_t wrow0 = row0 + wm * WTM, wcol0 = col0 + wn * WTN;
-  if (a.vec_store && !accum && !has_bias && wrow0 + WTM <= a.m && wcol0 + WTN <= a.n) {
-    auto fast = [&](auto GELU) {
+  const bool plain = !addend && !a.gate, gated = addend && a.gate;
+  if (a.vec_store && !has_bias && (plain || gated) && wrow0 + WTM <= a.m && wcol0 + WTN <= a.n) {
+    auto fast = [&](auto GELU, auto GATED) {
+      constexpr bool GT = decltype(GATED)::value;
+      f32x4 gv[TN][4];  // the lane's gate values, the same for every row
+      if constexpr (GT) {
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) gv[j][q] = *(const f32x4*)(a.gate + wcol0 + 4 * h + j * 32 + 8 * q);
+      }
 #pragma unroll
       for (int i = 0; i < TM; i++) {
         const size_t yrow = (size_t)a.y_offset + (zrow + wrow0 + i * 32 + l32) * (size_t)a.y_stride + wcol0 + 4 * h;
         if constexpr (YT == F32) {
           float* p = (float*)a.y + yrow;
+          const float* r0 = GT ? (const float*)addend + yrow : nullptr;
 #pragma unroll
           for (int j = 0; j < TN; j++)
 #pragma unroll
@@ -469,28 +485,41 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
                 const float t = acc[i][j][4 * q + e] * a.scale;
                 r[e] = decltype(GELU)::value ? gelu_tanh(t) : t;
               }
+              if constexpr (GT) r = *(const f32x4*)(r0 + j * 32 + 8 * q) + gv[j][q] * r;
               *(f32x4*)(p + j * 32 + 8 * q) = r;
             }
         } else {
           uint16_t* p = (uint16_t*)a.y + yrow;
+          const uint16_t* r0 = GT ? (const uint16_t*)addend + yrow : nullptr;
           const std::integral_constant<bool, YT == F16> tag;
 #pragma unroll
           for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
               float t[4];
+              u32x2 old = {0u, 0u};
+              if constexpr (GT) old = *(const u32x2*)(r0 + j * 32 + 8 * q);
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 t[e] = acc[i][j][4 * q + e] * a.scale;
                 if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
+                if constexpr (GT) {
+                  const uint32_t hb = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
+                  t[e] = (YT == BF16 ? bf16_to_f32((uint16_t)hb) : f16_to_f32((uint16_t)hb)) + gv[j][q][e] * t[e];
+                }
               }
               *(u32x2*)(p + j * 32 + 8 * q) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
             }
         }
       }
     };
-    if (gelu) fast(std::true_type{});
-    else fast(std::false_type{});
+    if (gated) {
+      if (gelu) fast(std::true_type{}, std::true_type{});
+      else fast(std::false_type{}, std::true_type{});
+    } else {
+      if (gelu) fast(std::true_type{}, std::false_type{});
+      else fast(std::false_type{}, std::false_type{});
+    }
     return;
   }
 #pragma unroll
@@ -509,14 +538,15 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
           float t = acc[i][j][4 * q + e] * a.scale;
           if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
           if (gelu) t = gelu_tanh(t);
+          if (a.gate) t *= a.gate[c0 + e < a.n ? c0 + e : 0];
           v[e] = t;
         }
         if (a.vec_store && c0 + 3 < a.n) {
-          store4<YT>(a, yrow + c0, v, accum);
+          store4<YT>(a, yrow + c0, v, addend);
         } else {
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], accum);
+            if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], addend);
         }
       }
     }
@@ -557,20 +587,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
   const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
+  const void* addend = a.res ? a.res : (accum ? a.y : nullptr);
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     float t = v[e] * a.scale;
     if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
     if (gelu) t = gelu_tanh(t);
+    if (a.gate) t *= a.gate[c0 + e < a.n ? c0 + e : 0];
     v[e] = t;
   }
   const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride;
   if (a.vec_store && full) {
-    store4<YT>(a, yrow + c0, v, accum);
+    store4<YT>(a, yrow + c0, v, addend);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; e++)
-      if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], accum);
+      if (c0 + e < a.n) store1<YT>(a, yrow + c0 + e, v[e], addend);
   }
 }
 
@@ -723,6 +755,8 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.w = (const char*)L.w + (uint64_t)L.w_offset * wb;
   a.y = L.y;
   a.bias = L.bias;
+  a.gate = L.gate;
+  a.res = L.res;
   a.x_bytes = L.k ? (uint32_t)(((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2) : 0;
   a.w_bytes = L.k ? (uint32_t)(((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb) : 0;
   a.m = L.m;
@@ -736,7 +770,8 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.kc = kc;
   a.flags = L.flags;
   a.y_dtype = (uint32_t)L.y_dtype;
-  a.vec_store = ((uintptr_t)L.y % (4 * yb) == 0 && ((uint64_t)L.y_offset * yb) % (4 * yb) == 0 &&
+  a.vec_store = ((uintptr_t)L.y % (4 * yb) == 0 && (uintptr_t)L.res % (4 * yb) == 0 &&
+                 (uintptr_t)L.gate % 16 == 0 && ((uint64_t)L.y_offset * yb) % (4 * yb) == 0 &&
                  ((uint64_t)L.y_stride * yb) % (4 * yb) == 0)
                     ? 1u
                     : 0u;

@@ -38,6 +38,8 @@ struct Int4Args {
   const uint16_t* s;
   void* y;
   const float* bias;
+  const float* gate;  // gated residual: y = res + gate[col] * v (res may be y; NULL: none)
+  const void* res;
   uint32_t m, n, k, group;
   float scale;
   uint32_t x_stride, y_stride, x_offset, y_offset;
@@ -134,6 +136,23 @@ __device__ __forceinline__ void load_x(const __amdgpu_buffer_rsrc_t& rx, uint32_
 #pragma unroll
     for (int e = 0; e < 2; e++)
       f.v[e][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, e * 16, 0));
+  }
+}
+
+// the epilogue of one output: scale, bias, GELU, gate, then y = v, y += v or y = res + v
+__device__ __forceinline__ void int4_store(const Int4Args& a, uint32_t row, uint32_t col, float sum) {
+  float val = sum * a.scale;
+  if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
+  if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
+  if (a.gate) val *= a.gate[col];
+  const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
+  const void* add = a.res ? a.res : ((a.flags & WE_EPI_ACCUMULATE_BIT) ? a.y : nullptr);
+  if (a.y_dtype == F32) {
+    ((float*)a.y)[o] = add ? ((const float*)add)[o] + val : val;
+  } else if (a.y_dtype == BF16) {
+    ((uint16_t*)a.y)[o] = f32_to_bf16(add ? bf16_to_f32(((const uint16_t*)add)[o]) + val : val);
+  } else {
+    ((uint16_t*)a.y)[o] = f32_to_f16(add ? f16_to_f32(((const uint16_t*)add)[o]) + val : val);
   }
 }
 
@@ -235,22 +254,7 @@ __global__ void __launch_bounds__(256) int4_gemv_kernel(Int4Args a) {
   const int ln = threadIdx.x & 63, r = threadIdx.x >> 6;
   const float sum = red[ln][r] + red[64 + ln][r] + red[128 + ln][r] + red[192 + ln][r];
   const uint32_t row = m0 + 4 * (ln >> 4) + r, col = n0 + (ln & 15);
-  if (row >= a.m || col >= a.n) return;
-  float val = sum * a.scale;
-  if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
-  if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
-  const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
-  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
-  if (a.y_dtype == F32) {
-    float* y = (float*)a.y;
-    y[o] = accum ? y[o] + val : val;
-  } else if (a.y_dtype == BF16) {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_bf16(accum ? bf16_to_f32(y[o]) + val : val);
-  } else {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_f16(accum ? f16_to_f32(y[o]) + val : val);
-  }
+  if (row < a.m && col < a.n) int4_store(a, row, col, sum);
 }
 
 // ------------------------------------------------------------------------------------------------------
@@ -301,23 +305,6 @@ __device__ __forceinline__ u32x4 interleave8(u32x4 v) {
                __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
 }
 
-__device__ __forceinline__ void int4_store(const Int4Args& a, uint32_t row, uint32_t col, float sum) {
-  float val = sum * a.scale;
-  if (a.flags & WE_EPI_BIAS_BIT) val += a.bias[col];
-  if (a.flags & WE_EPI_GELU_BIT) val = gelu_tanh(val);
-  const size_t o = (size_t)a.y_offset + (size_t)row * a.y_stride + col;
-  const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
-  if (a.y_dtype == F32) {
-    float* y = (float*)a.y;
-    y[o] = accum ? y[o] + val : val;
-  } else if (a.y_dtype == BF16) {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_bf16(accum ? bf16_to_f32(y[o]) + val : val);
-  } else {
-    uint16_t* y = (uint16_t*)a.y;
-    y[o] = f32_to_f16(accum ? f16_to_f32(y[o]) + val : val);
-  }
-}
 
 template <int XT>
 __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
@@ -627,6 +614,8 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   a.s = L.scales;
   a.y = L.y;
   a.bias = L.bias;
+  a.gate = L.gate;
+  a.res = L.res;
   a.m = L.m;
   a.n = L.n;
   a.k = L.k;

@@ -25,6 +25,11 @@ struct GemmLaunch {
   const void* w;
   void* y;
   const float* bias;
+  // gated residual (gatedAdd fused): y = res + gate[col] * v, v the value after scale / bias / GELU; res has
+  // y's type and layout (it may be y itself). gate NULL: off. res NULL with a gate: y = gate * v (or y +=
+  // gate * v under ACCUMULATE).
+  const float* gate;
+  const void* res;
   int x_dtype, w_dtype, y_dtype;
   uint32_t m, n, k;
   float scale;
@@ -57,6 +62,8 @@ struct Int4Launch {
   const uint16_t* scales;
   void* y;
   const float* bias;
+  const float* gate;  // as GemmLaunch
+  const void* res;
   int x_dtype, y_dtype;
   uint32_t m, n, k, group;
   float scale;

@@ -498,8 +498,32 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
   return s < 1 ? 1 : s;
 }
 
+namespace {
+int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
+                const float* gate, const void* res);
+}  // namespace
+
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags) {
+  return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, nullptr, nullptr);
+}
+
+int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                    const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
+                    const float* gate, const void* residual) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!gate) return fail(ctx, WE_EINVAL, "gate is null");
+  if (flags & WE_EPI_SPLIT_K) return fail(ctx, WE_EINVAL, "a gated residual does not combine with split-K partials");
+  if (residual && (flags & WE_EPI_ACCUMULATE))
+    return fail(ctx, WE_EINVAL, "a residual replaces accumulate: pass y as the residual to add to y");
+  return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, gate, residual);
+}
+
+namespace {
+int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
+                const float* gate, const void* res) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
@@ -528,6 +552,8 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
   int rc = check_span(ctx, x, x_need, "x");
   if (!rc) rc = check_span(ctx, y, y_need, "y");
   if (!rc && (flags & WE_EPI_BIAS)) rc = check_span(ctx, bias, (uint64_t)p->n * 4, "bias");
+  if (!rc && gate) rc = check_span(ctx, gate, (uint64_t)p->n * 4, "gate");
+  if (!rc && res) rc = check_span(ctx, res, y_need, "residual");
   if (rc) return rc;
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
 
@@ -551,6 +577,8 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
     L.scales = (const uint16_t*)w_scales;
     L.y = y;
     L.bias = bias;
+    L.gate = gate;
+    L.res = res;
     L.x_dtype = x_dtype;
     L.y_dtype = y_dtype;
     L.m = p->m;
@@ -577,6 +605,8 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
   L.w = w;
   L.y = y;
   L.bias = bias;
+  L.gate = gate;
+  L.res = res;
   L.x_dtype = x_dtype;
   L.w_dtype = w_dtype;
   L.y_dtype = y_dtype;
@@ -617,6 +647,7 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
   return WE_OK;
 }
+}  // namespace
 
 // ------------------------------------------------------------------------------------------ norms, rope, elementwise
 

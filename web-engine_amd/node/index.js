@@ -77,9 +77,16 @@ class Graph {
   }
 
   // ---- the kernels, one call each ----
-  matmul(params, xDtype, x, wDtype, w, yDtype, y, { scales = null, group = 0, bias = null, flags = 0 } = {}) {
-    addon.matmul(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
-                 ptrOf(bias), flags);
+  // gate (f32 [N]) given: y = residual + gate * v, the gatedAdd of src/model/block.ts:60-64 fused (matmulGated)
+  matmul(params, xDtype, x, wDtype, w, yDtype, y,
+         { scales = null, group = 0, bias = null, flags = 0, gate = null, residual = null } = {}) {
+    if (gate === null) {
+      addon.matmul(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
+                   ptrOf(bias), flags);
+    } else {
+      addon.matmulGated(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
+                        ptrOf(bias), flags, ptrOf(gate), ptrOf(residual));
+    }
   }
 
   rmsnorm(rows, d, eps, offset, dtype, x, weight, scale, shift, out) {

@@ -441,6 +441,36 @@ static napi_value Matmul(napi_env env, napi_callback_info info) {
                                     (const float*)bias, flags));
 }
 
+/* matmulGated(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags, gate, residual):
+ * y = residual + gate * v, the reference's gatedAdd after the GEMM fused into its epilogue */
+static napi_value MatmulGated(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 14)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* pdata = NULL;
+  size_t plen = 0;
+  bytes_of(&a, 1, &pdata, &plen);
+  int32_t xdt = i32_arg(&a, 2);
+  void* x = ptr_arg(&a, 3);
+  int32_t wdt = i32_arg(&a, 4);
+  void* w = ptr_arg(&a, 5);
+  void* scales = ptr_arg(&a, 6);
+  uint32_t group = u32_arg(&a, 7);
+  int32_t ydt = i32_arg(&a, 8);
+  void* y = ptr_arg(&a, 9);
+  void* bias = ptr_arg(&a, 10);
+  uint32_t flags = u32_arg(&a, 11);
+  void* gate = ptr_arg(&a, 12);
+  void* res = ptr_arg(&a, 13);
+  if (a.bad) return NULL;
+  if (plen != sizeof(we_matmul_params)) {
+    napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
+    return NULL;
+  }
+  return status(env, ctx, we_matmul_gated(ctx, (const we_matmul_params*)pdata, xdt, x, wdt, w, scales, group, ydt, y,
+                                          (const float*)bias, flags, (const float*)gate, res));
+}
+
 /* ---- norms, rotary, elementwise ---- */
 static napi_value RmsNorm(napi_env env, napi_callback_info info) {
   args_t a;
@@ -811,7 +841,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
-      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul},
+      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulGated", MatmulGated},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},

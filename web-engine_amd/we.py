@@ -79,6 +79,7 @@ SIGNATURES = {
     "we_matmul_params_make": (_I, [_P, _U32, _U32, _U32, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "we_ksplit_for": (_U32, [_U32, _U32, _U32]),
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
+    "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
     "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
     "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
     "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _U32, _P, _U32]),
@@ -302,9 +303,16 @@ class Graph:
         return ms.value
 
     # ---- raw ops (one dispatch each)
-    def matmul(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0):
-        self.check(self.lib.we_matmul(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
-                                      _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags))
+    def matmul(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0, gate=None,
+               residual=None):
+        """we_matmul; with `gate` (f32 [N]) we_matmul_gated: y = residual + gate * v (gatedAdd fused)."""
+        if gate is None:
+            self.check(self.lib.we_matmul(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                          _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags))
+        else:
+            self.check(self.lib.we_matmul_gated(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                                _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags,
+                                                _addr(gate), _addr(residual)))
 
     def rmsnorm(self, rows, d, eps, offset, dtype, x, weight, scale, shift, out):
         self.check(self.lib.we_rmsnorm(self.ctx, rows, d, eps, offset, dtype, _addr(x), _addr(weight), _addr(scale),
