@@ -252,6 +252,42 @@ def file_read_rate(layout, host, scales, pinned, threads=8, reps=3):
             "source": "page cache (file just written)"}
 
 
+def measured_peaks(g, warmup_ms=500, rounds=3, runs=5, read_bytes=2 << 30):
+    """The build's own ceilings, timePeak style (src/bench/peak.ts:69-109: warm up, then the fastest of `rounds`
+    rounds of `runs` dispatches): dense bf16 MFMA, scalar f32 FMA, packed f16 FMA, int8 dot4, and a streaming
+    read of `read_bytes` (beyond the 256 MB Infinity Cache)."""
+    out = g.buffer(max(16384 * 256, we.read_peak_out_words(read_bytes)) * 4)
+    kinds = {"mfma_bf16_tflops": (we.PEAK_MFMA_BF16, 2048, 2048), "f32_fma_tflops": (we.PEAK_F32, 16384, 4096),
+             "f16_fma_tflops": (we.PEAK_F16, 16384, 4096), "i8_dot4_tops": (we.PEAK_I8, 16384, 4096)}
+    res = {}
+    for name, (kind, wg, iters) in kinds.items():
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < warmup_ms:
+            g.peak(kind, wg, iters, out)
+            g.sync()
+        best = float("inf")
+        for _ in range(rounds):
+            g.timer_start()
+            for _ in range(runs):
+                ops = g.peak(kind, wg, iters, out)
+            best = min(best, g.timer_stop() / runs)
+        res[name] = ops / best / 1e9
+    buf = g.buffer(read_bytes)
+    for _ in range(3):
+        g.read_peak(buf, read_bytes, out)
+    best = float("inf")
+    for _ in range(rounds):
+        g.timer_start()
+        for _ in range(runs):
+            g.read_peak(buf, read_bytes, out)
+        best = min(best, g.timer_stop() / runs)
+    res["hbm_read_gbs"] = read_bytes / best / 1e6
+    res["hbm_read_bytes"] = read_bytes
+    g.free(buf)
+    g.free(out)
+    return res
+
+
 def calibration_copy(g, nbytes=256 << 20):
     """A plain streaming kernel of known traffic (out = a + b over f32): reads 2 * nbytes, writes nbytes.
     Its FETCH_SIZE / WRITE_SIZE under rocprofv3 scale the counters of the kernels above."""
@@ -328,6 +364,9 @@ def main():
         extra["c2_bf16_qkv_4096x9216x3072"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
         extra["c1_fp8_64x3072x3072"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16)
     extra["calibration"] = calibration_copy(g)
+    peaks = measured_peaks(g) if args.only == "all" else None
+    if peaks:
+        extra["measured_peaks"] = peaks
     g.destroy()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
@@ -346,6 +385,8 @@ def main():
                             "kernel": "gemm_lds_kernel<256,256,2,4,bf16,fp8, ping-pong> up-projection "
                                       "4096x12288x3072 (+ fused GELU)",
                             "algorithmic": f"{up['flop']:.0f} FLOP per launch / {up['ms'] * 1e3:.1f} us"}
+        if peaks:
+            line["roofline"]["frac_of_measured_peak"] = up["tflops"] / peaks["mfma_bf16_tflops"]
         line["up_proj_tflops"] = up["tflops"]
         line["down_proj_tflops"] = mlp["down"]["tflops"]
     if int4:
@@ -355,6 +396,8 @@ def main():
                                  "frac": m1["gbs"] / PEAK_HBM_GBS, "traffic": measured_traffic("int4_decode_m1"),
                                  "kernel": "int4_gemv_pipe_kernel<f16> M=1 K=3584 N=18944 group 64",
                                  "algorithmic": f"{m1['bytes']} B per launch / {m1['us']:.2f} us"}
+        if peaks:
+            line["roofline_int4"]["frac_of_measured_peak"] = m1["gbs"] / peaks["hbm_read_gbs"]
     line.update(extra)
     if cpu:
         line["cpu_baseline"] = cpu

@@ -171,6 +171,23 @@ int we_unpack_fp8(we_ctx* ctx, const void* packed, size_t n, const float* scale,
 int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, uint32_t rows, uint32_t k,
                     uint32_t group, float* out);
 
+/* ---- peak probes: timePeak (src/bench/peak.ts:69-109) ----
+ * One dispatch of a math-peak kernel on the compute stream (time it with we_timer_start / we_timer_stop).
+ * F32 / F16 / I8 as the reference: workgroups of 64 threads, each thread `iters` iterations of 64 operations
+ * (8 independent chains of fma / packed-f16 fma / int8 dot4); F32 uses scalar FMAs. MFMA_BF16: workgroups of
+ * 256 threads, each wave 8 independent chains of v_mfma_f32_32x32x16_bf16 per iteration (4096 FLOP per thread
+ * per iteration): the ceiling of the matmul's MFMA loop. out: u32 [workgroups x threads] receives each thread's
+ * folded result; *ops (may be NULL) the operation count of the dispatch. */
+#define WE_PEAK_F32 0
+#define WE_PEAK_F16 1
+#define WE_PEAK_I8 2
+#define WE_PEAK_MFMA_BF16 3
+int we_peak(we_ctx* ctx, int kind, uint32_t workgroups, uint32_t iters, uint32_t* out, double* ops);
+/* One streaming read of `bytes` (a multiple of 16, 16-byte aligned) from buf, every load in flight at once; each
+ * wave's sum of the words it read goes to out (u32 [4 * ceil(bytes / 32768)]): the HBM read ceiling the int4 GEMV
+ * is measured against (over more than the 256 MB Infinity Cache). */
+int we_read_peak(we_ctx* ctx, const void* buf, size_t bytes, uint32_t* out);
+
 /* ---- .safetensors files: readHeader / readTensor (src/weights/safetensors.ts:28-70) ----
  * we_st_open reads and validates the header (8-byte LE size, JSON object of {dtype, shape, data_offsets}
  * entries plus optional __metadata__) with the reference's checks and messages: "File is too small to be a

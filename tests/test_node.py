@@ -40,7 +40,7 @@ EXPORTS = {
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
     "we_graph_begin": "graphBegin", "we_graph_end": "graphEnd", "we_graph_launch": "graphLaunch",
-    "we_graph_destroy": "graphDestroy", "we_st_open": "stOpen", "we_st_close": "stClose", "we_st_count": "stCount",
+    "we_graph_destroy": "graphDestroy", "we_peak": "peak", "we_read_peak": "readPeak", "we_st_open": "stOpen", "we_st_close": "stClose", "we_st_count": "stCount",
     "we_st_info": "stInfo", "we_st_find": "stFind", "we_st_metadata_count": "stMetadataCount",
     "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead",
 }

@@ -649,6 +649,33 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
 }
 }  // namespace
 
+// ------------------------------------------------------------------------------------------ peak probes
+
+int we_peak(we_ctx* ctx, int kind, uint32_t workgroups, uint32_t iters, uint32_t* out, double* ops) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (kind < WE_PEAK_F32 || kind > WE_PEAK_MFMA_BF16) return fail(ctx, WE_EINVAL, "unknown peak kind %d", kind);
+  if (workgroups == 0 || workgroups > (1u << 24)) return fail(ctx, WE_EINVAL, "workgroups must be in [1, 2^24], got %u", workgroups);
+  const uint64_t threads = (uint64_t)workgroups * (kind == WE_PEAK_MFMA_BF16 ? 256 : 64);
+  int rc = check_span(ctx, out, threads * 4, "out");
+  if (rc) return rc;
+  if (ops) *ops = (double)threads * iters * (kind == WE_PEAK_MFMA_BF16 ? 4096.0 : 64.0);
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  hipError_t e = we::peak_launch(kind, workgroups, iters, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "peak launch");
+}
+
+int we_read_peak(we_ctx* ctx, const void* buf, size_t bytes, uint32_t* out) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (bytes % 16 || (uintptr_t)buf % 16) return fail(ctx, WE_EINVAL, "the read needs 16-byte aligned whole chunks");
+  int rc = check_span(ctx, buf, bytes, "buf");
+  if (bytes >= (1ull << 44)) return fail(ctx, WE_EINVAL, "the read is limited to 16 TB");
+  if (!rc) rc = check_span(ctx, out, we::read_peak_out_words(bytes) * 4, "out");
+  if (rc) return rc;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  hipError_t e = we::read_peak_launch(buf, bytes, out, ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "read peak launch");
+}
+
 // ------------------------------------------------------------------------------------------ norms, rope, elementwise
 
 int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,

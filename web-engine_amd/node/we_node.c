@@ -650,6 +650,33 @@ static napi_value GraphDestroy(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_graph_destroy(ctx, g));
 }
 
+/* ---- peak probes: timePeak (src/bench/peak.ts:69-109) ---- */
+/* peak(ctx, kind, workgroups, iters, out) -> operation count of the dispatch */
+static napi_value Peak(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  int32_t kind = i32_arg(&a, 1);
+  uint32_t wg = u32_arg(&a, 2), iters = u32_arg(&a, 3);
+  void* out = ptr_arg(&a, 4);
+  if (a.bad) return NULL;
+  double ops = 0;
+  int rc = we_peak(ctx, kind, wg, iters, (uint32_t*)out, &ops);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, ops);
+}
+
+static napi_value ReadPeak(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 4)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* buf = ptr_arg(&a, 1);
+  double bytes = f64_arg(&a, 2);
+  void* out = ptr_arg(&a, 3);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_read_peak(ctx, buf, (size_t)bytes, (uint32_t*)out));
+}
+
 /* ---- .safetensors files: readHeader / readTensor (src/weights/safetensors.ts:28-70) ---- */
 
 /* throws Error(we_last_error(NULL)); a malformed file's error is named SafetensorsError, as the reference's */
@@ -847,6 +874,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
       {"timerStart", TimerStart}, {"timerStop", TimerStop},
       {"graphBegin", GraphBegin}, {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphDestroy", GraphDestroy},
+      {"peak", Peak},             {"readPeak", ReadPeak},
       {"stOpen", StOpen},         {"stClose", StClose},       {"stCount", StCount},
       {"stInfo", StInfo},         {"stFind", StFind},         {"stMetadataCount", StMetadataCount},
       {"stMetadataAt", StMetadataAt}, {"stRead", StRead},

@@ -31,6 +31,12 @@ DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
 ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
 OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
+PEAK_F32, PEAK_F16, PEAK_I8, PEAK_MFMA_BF16 = range(4)
+
+
+def read_peak_out_words(nbytes):
+    """u32 results of we_read_peak over nbytes (one per wave of 64 threads x 8 chunks of 16 bytes)"""
+    return 4 * ((nbytes // 16 + 2047) // 2048)
 ERRORS = {1: "WE_EINVAL", 2: "WE_ENOMEM", 3: "WE_EHIP", 4: "WE_EUNSUPPORTED", 5: "WE_EFORMAT", 6: "WE_EIO",
           7: "WE_ENOTFOUND"}
 WE_EINVAL = 1
@@ -92,6 +98,8 @@ SIGNATURES = {
     "we_graph_end": (_I, [_P, _P]),
     "we_graph_launch": (_I, [_P, _P]),
     "we_graph_destroy": (_I, [_P, _P]),
+    "we_peak": (_I, [_P, _I, _U32, _U32, _P, _P]),
+    "we_read_peak": (_I, [_P, _P, _SZ, _P]),
     "we_st_open": (_I, [ctypes.c_char_p, _P]),
     "we_st_close": (_I, [_P]),
     "we_st_count": (_I, [_P, _P]),
@@ -313,6 +321,15 @@ class Graph:
             self.check(self.lib.we_matmul_gated(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
                                                 _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags,
                                                 _addr(gate), _addr(residual)))
+
+    def peak(self, kind, workgroups, iters, out):
+        """One dispatch of a peak kernel (timePeak, src/bench/peak.ts): returns its operation count."""
+        ops = ctypes.c_double()
+        self.check(self.lib.we_peak(self.ctx, kind, workgroups, iters, _addr(out), ctypes.byref(ops)))
+        return ops.value
+
+    def read_peak(self, buf, nbytes, out):
+        self.check(self.lib.we_read_peak(self.ctx, _addr(buf), nbytes, _addr(out)))
 
     def rmsnorm(self, rows, d, eps, offset, dtype, x, weight, scale, shift, out):
         self.check(self.lib.we_rmsnorm(self.ctx, rows, d, eps, offset, dtype, _addr(x), _addr(weight), _addr(scale),
