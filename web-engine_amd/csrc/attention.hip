@@ -105,8 +105,12 @@ __device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, cons
     static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
     tmax = halves_max(tmax);
     const float mn = fmaxf(m[qb], tmax);
-    const float ms = mn == -__builtin_inff() ? 0.0f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m[qb] - ms);
+    // Lazy rescale: the running max only moves (and O, l are rescaled) when some query of the wave sees its
+    // max rise by more than 8 (log2 units); otherwise the stale max stays the shift, so p <= 2^8. Softmax is
+    // invariant to the shift, and the wave skips 64 multiplies of O on most tiles.
+    const bool rescale = __any(mn > m[qb] + 8.0f);
+    const float mref = rescale ? mn : m[qb];
+    const float ms = mref == -__builtin_inff() ? 0.0f : mref;
     float ps = 0.0f;
     static_for<0, 4>([&](auto S) {
       constexpr int s = S;
@@ -120,9 +124,14 @@ __device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, cons
         pf[qb][s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
       });
     });
-    l[qb] = l[qb] * alpha + ps;
-    m[qb] = mn;
-    static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
+    if (rescale) {
+      const float alpha = __builtin_amdgcn_exp2f(m[qb] - ms);
+      l[qb] = l[qb] * alpha + ps;
+      m[qb] = mn;
+      static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
+    } else {
+      l[qb] += ps;
+    }
   });
   static_for<0, DP / 32>([&](auto D) {
     constexpr int db = D;
@@ -302,7 +311,6 @@ __global__ void __launch_bounds__(256) attn_vt_kernel(const uint16_t* v, uint32_
 // opens each tile, so its latency is hidden behind two tiles of MFMAs, with no staging registers.
 constexpr int DMA_BM = 256;
 constexpr int DMA_NS = 3;
-typedef __attribute__((address_space(3))) void att_lds_t;
 constexpr uint32_t kAttInvalid = 0x80000000u;
 
 template <bool IS_F16, int QB>
@@ -355,14 +363,14 @@ __global__ void __launch_bounds__(512 / QB, 1) attn_dma_kernel(AttnArgs a, const
       const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ (row & 15);
       const uint32_t key = k0 + row;
       const uint32_t off = key < a.tokens ? (key * a.ks + g * DP + logical * 8) * 2 : kAttInvalid;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (att_lds_t*)(base + j * 1024), 16, off, 0, 0, 0);
+      dma16(rk, base + j * 1024, off);
     }
 #pragma unroll
     for (int u = 0; u < IPW; u++) {
       const int j = wave + NW * u;
       const int row = 8 * j + (lane >> 3), phys = lane & 7, logical = phys ^ ((row >> 1) & 7);
       const uint32_t off = ((g * DP + row) * tp + k0 + logical * 8) * 2;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (att_lds_t*)(base + KS_BYTES + j * 1024), 16, off, 0, 0, 0);
+      dma16(rv, base + KS_BYTES + j * 1024, off);
     }
   };
 
@@ -375,6 +383,12 @@ __global__ void __launch_bounds__(512 / QB, 1) attn_dma_kernel(AttnArgs a, const
   });
   if (nt > 0) issue(0, 0);
   if (nt > 1) issue(1, 1);
+  // Q is consumed here, so the compiler waits for its loads once, before the loop, instead of at the first
+  // MFMA of every tile (it cannot tell the first iteration from the others)
+#pragma unroll
+  for (int qq = 0; qq < QB; qq++)
+#pragma unroll
+    for (int ss = 0; ss < DP / 16; ss++) asm volatile("" ::"v"(qf[qq][ss]));
   int st = 0;
   for (int t = 0; t < nt; t++) {
     // own loads of tile t done (tile t + 1's 2 IPW may still be in flight), then everyone's

@@ -159,20 +159,6 @@ __device__ __forceinline__ void int4_store(const Int4Args& a, uint32_t row, uint
 constexpr int INT4_CH = 14;  // 64-k blocks whose weights a wave stages at once (7 KB of LDS per wave)
 constexpr int INT4_XPF = 2;  // blocks of x fragments in flight ahead of the MFMAs
 
-typedef __attribute__((address_space(3))) void lds_ptr_t;
-
-// 16-byte direct-to-LDS buffer load issued as inline asm: lane i writes dst + 16 i. The compiler does not
-// see it, so it adds no waits of its own for the LDS it fills (it otherwise waits for every such load in
-// flight before any LDS read it cannot tell apart); the kernels that use it wait with explicit vmcnt
-// counts. The compiler's waits for its own register loads stay correct: it can only undercount the loads
-// in flight after one, which makes a wait stricter. M0 is set here; nothing else in those kernels reads it.
-__device__ __forceinline__ void dma16(const __amdgpu_buffer_rsrc_t& r, void* dst, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"((uint32_t)(uintptr_t)(lds_ptr_t*)dst), "v"(voff), "s"(r)
-               : "memory");
-}
-
 template <int XT>
 __global__ void __launch_bounds__(256) int4_gemv_kernel(Int4Args a) {
   constexpr bool IS_F16 = XT == F16;
