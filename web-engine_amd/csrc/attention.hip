@@ -5,8 +5,15 @@
 // over all keys or (causal) keys j <= i. Each token's heads may start `stride` elements after the previous
 // token's, so q, k and v can be column slices of one fused QKV projection output.
 //
-// Work split: a workgroup = 4 waves = 128 queries of one head; a wave owns 32 queries. Keys are walked in
-// tiles of 64 that all four waves share through LDS.
+// Work split: a wave owns 32 queries of one head and walks the keys in tiles of 64 shared through LDS with
+// the other waves of its workgroup. Three kernels:
+//   * attn16_kernel / attn32_kernel: any head dim up to 128; 4 waves (128 queries), tiles staged through
+//     registers.
+//   * attn_pp_kernel (head dim 128, 16-bit, the default there): 8 waves (256 queries); K and V^T tiles
+//     reach a 4-stage LDS ring by direct-to-LDS loads; the two waves sharing a SIMD alternate MFMA and
+//     softmax phases between workgroup barriers (ping-pong).
+//   * attn_dma_kernel (WE_ATTN_PATH=ring): the same ring with a 3-stage depth and one phase per tile.
+// All three run the same per-tile arithmetic in the same order, so their outputs agree bit for bit.
 //
 // 16-bit kernel (bf16 or f16 operands, fp32 accumulation, 32x32x16 MFMA):
 //   * S^T = K Q^T: the MFMA's A operand is a K tile row (a key), B is the wave's Q held in registers. In the
@@ -65,37 +72,43 @@ __device__ __forceinline__ void block_coords(const AttnArgs& a, uint32_t& qb, ui
   h = b / a.nqb;
 }
 
-// One 64-key tile for QB blocks of 32 queries of one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
-// Every K and V^T fragment read from LDS feeds QB MFMAs. ks: the K tile (64 rows of DP values, 16-byte chunks
-// XOR-swizzled by (row >> KSH)); vt: the V^T tile (DP rows of 64 keys, keys in bit-2/3-swapped order, chunks
-// swizzled by (row >> 1) & 7). qw[qb]: first query of block qb; qi[qb]: this lane's query in it.
+// One 64-key tile for QB blocks of 32 queries of one wave, in three steps (attn_tile16 runs them in order; the
+// ping-pong kernel runs the scores of tile t with the P V^T of tile t - 1 in one phase and the softmax in
+// the next): S^T = K Q^T, online softmax, O^T += V^T P^T. Every K and V^T fragment read from LDS feeds QB
+// MFMAs. ks: the K tile (64 rows of DP values, 16-byte chunks XOR-swizzled by (row >> KSH)); vt: the V^T
+// tile (DP rows of 64 keys, keys in bit-2/3-swapped order, chunks swizzled by (row >> 1) & 7). qw[qb]: first
+// query of block qb; qi[qb]: this lane's query in it.
 template <int DP, bool IS_F16, int QB>
-__device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, const u32x4 (&qf)[QB][DP / 16],
-                                            f32x16 (&o)[QB][DP / 32], float (&m)[QB], float (&l)[QB], uint32_t k0,
-                                            const uint32_t (&qw)[QB], const uint32_t (&qi)[QB], int c, int hf,
-                                            const AttnArgs& a) {
+__device__ __forceinline__ void attn_scores16(const char* ks, const u32x4 (&qf)[QB][DP / 16], f32x16 (&sacc)[QB][2],
+                                              int c, int hf) {
   constexpr int NCH = DP / 8;
   constexpr int KSH = NCH == 16 ? 0 : NCH == 8 ? 1 : 2;
-  f32x16 sacc[QB][2];
   static_for<0, QB>([&](auto Q) { sacc[Q][0] = f32x16{}; sacc[Q][1] = f32x16{}; });
-  static_for<0, 2>([&](auto B) {
-    constexpr int b = B;
-    const int r = 32 * b + c;
-    static_for<0, DP / 16>([&](auto S) {
-      constexpr int s = S;
+  // the two key halves alternate, so consecutive MFMAs never wait on each other's accumulator
+  static_for<0, DP / 16>([&](auto S) {
+    constexpr int s = S;
+    static_for<0, 2>([&](auto B) {
+      constexpr int b = B;
+      const int r = 32 * b + c;
       const u32x4 af = *(const u32x4*)(ks + r * DP * 2 + (((2 * s + hf) ^ ((r >> KSH) & (NCH - 1))) << 4));
       static_for<0, QB>([&](auto Q) { sacc[Q][b] = mfma_32x32x16<IS_F16>(af, qf[Q][s], sacc[Q][b]); });
     });
   });
-  u32x4 pf[QB][4];
+}
+
+template <int DP, bool IS_F16, int QB>
+__device__ __forceinline__ void attn_softmax16(const f32x16 (&sacc)[QB][2], u32x4 (&pf)[QB][4],
+                                               f32x16 (&o)[QB][DP / 32], float (&m)[QB], float (&l)[QB], uint32_t k0,
+                                               const uint32_t (&qw)[QB], const uint32_t (&qi)[QB], int hf,
+                                               const AttnArgs& a) {
   static_for<0, QB>([&](auto Q) {
     constexpr int qb = Q;
-    // scores in log2 units; keys past the end (or after the query, causal) get -inf
+    // raw scores; keys past the end (or after the query, causal) get -inf
     float x[32];
     const bool mask = (k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw[qb]);
     static_for<0, 32>([&](auto I) {
       constexpr int i = I, b = i / 16, v = i % 16;
-      x[i] = sacc[qb][b][v] * a.scale_log2;
+      x[i] = sacc[qb][b][v];
       if (mask) {
         const uint32_t key = k0 + 32 * b + 8 * (v / 4) + 4 * hf + (v % 4);
         if (key >= a.tokens || (a.causal && key > qi[qb])) x[i] = -__builtin_inff();
@@ -103,7 +116,8 @@ __device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, cons
     });
     float tmax = x[0];
     static_for<1, 32>([&](auto I) { tmax = fmaxf(tmax, x[I]); });
-    tmax = halves_max(tmax);
+    // the row max in log2 units: rounding is monotone, so max(x) * scale is exactly max(x * scale)
+    tmax = halves_max(tmax) * a.scale_log2;
     const float mn = fmaxf(m[qb], tmax);
     // Lazy rescale: the running max only moves (and O, l are rescaled) when some query of the wave sees its
     // max rise by more than 8 (log2 units); otherwise the stale max stays the shift, so p <= 2^8. Softmax is
@@ -116,7 +130,7 @@ __device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, cons
       constexpr int s = S;
       float p[8];
       static_for<0, 8>([&](auto I) {
-        p[I] = __builtin_amdgcn_exp2f(x[16 * (s / 2) + 8 * (s % 2) + I] - ms);
+        p[I] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[16 * (s / 2) + 8 * (s % 2) + I], a.scale_log2, -ms));
         ps += p[I];
       });
       static_for<0, 4>([&](auto J) {
@@ -124,24 +138,39 @@ __device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, cons
         pf[qb][s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
       });
     });
-    if (rescale) {
-      const float alpha = __builtin_amdgcn_exp2f(m[qb] - ms);
-      l[qb] = l[qb] * alpha + ps;
-      m[qb] = mn;
-      static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
-    } else {
-      l[qb] += ps;
-    }
+    // alpha = 1 unless the max moved; multiplying O by it on every tile keeps O in one set of registers
+    // (a branch around the multiply makes the compiler copy all of O on the path that skips it)
+    const float alpha = rescale ? __builtin_amdgcn_exp2f(m[qb] - ms) : 1.0f;
+    l[qb] = __builtin_fmaf(l[qb], alpha, ps);
+    if (rescale) m[qb] = mn;
+    static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
   });
-  static_for<0, DP / 32>([&](auto D) {
-    constexpr int db = D;
-    const int r = 32 * db + c;
-    static_for<0, 4>([&](auto S) {
-      constexpr int s = S;
+}
+
+template <int DP, bool IS_F16, int QB>
+__device__ __forceinline__ void attn_pv16(const char* vt, const u32x4 (&pf)[QB][4], f32x16 (&o)[QB][DP / 32], int c,
+                                          int hf) {
+  static_for<0, 4>([&](auto S) {
+    constexpr int s = S;
+    static_for<0, DP / 32>([&](auto D) {
+      constexpr int db = D;
+      const int r = 32 * db + c;
       const u32x4 vf = *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
       static_for<0, QB>([&](auto Q) { o[Q][db] = mfma_32x32x16<IS_F16>(vf, pf[Q][s], o[Q][db]); });
     });
   });
+}
+
+template <int DP, bool IS_F16, int QB>
+__device__ __forceinline__ void attn_tile16(const char* ks, const char* vt, const u32x4 (&qf)[QB][DP / 16],
+                                            f32x16 (&o)[QB][DP / 32], float (&m)[QB], float (&l)[QB], uint32_t k0,
+                                            const uint32_t (&qw)[QB], const uint32_t (&qi)[QB], int c, int hf,
+                                            const AttnArgs& a) {
+  f32x16 sacc[QB][2];
+  u32x4 pf[QB][4];
+  attn_scores16<DP, IS_F16, QB>(ks, qf, sacc, c, hf);
+  attn_softmax16<DP, IS_F16, QB>(sacc, pf, o, m, l, k0, qw, qi, hf, a);
+  attn_pv16<DP, IS_F16, QB>(vt, pf, o, c, hf);
 }
 
 // O = O^T / l for this lane's query, as 16-bit values, 4 consecutive dims per store.
@@ -407,6 +436,177 @@ __global__ void __launch_bounds__(512 / QB, 1) attn_dma_kernel(AttnArgs a, const
   static_for<0, QB>([&](auto Q) { attn_store16<DP, IS_F16>(o[Q], l[Q], qi[Q], h, hf, a); });
 }
 
+// ------------------------------------------------------------------------------------ 16-bit, ping-pong
+// Same work split, LDS layout and per-tile arithmetic as attn_dma_kernel (QB = 1, 8 waves of 32 queries), with
+// the MFMA and the softmax work of the two waves that share a SIMD (waves w and w + 4: a workgroup's waves go
+// round-robin over the 4 SIMDs) kept out of step. Each wave alternates
+//   M(t): O^T += V^T P^T of tile t - 1, then S^T = K Q^T of tile t   (32 MFMAs, LDS reads)
+//   V(t): the online softmax of tile t                                (VALU: scale, max, exp2, sum, pack)
+// and group 1 (waves 4-7) runs one phase behind group 0, so between two workgroup barriers one wave of every
+// SIMD issues MFMAs while the other one runs its softmax. The order of the operations on O is the one of
+// attn_tile16 (rescale by tile t's softmax, then add tile t's P V^T), so the result is the same bit for bit.
+// Interval j (between barriers): group 0 runs phase j (even: M(j / 2), odd: V((j - 1) / 2)), group 1 phase
+// j - 1; M(nt) is the last P V^T alone. K of tile t is read in intervals 2t and 2t + 1, its V^T in 2t + 2 and
+// 2t + 3, so tile t + PP_NS goes into its stage at the start of interval 2t + 4. Tile t is first read in
+// interval 2t: every wave waits for its own loads of it before the barrier that ends interval 2t - 1.
+constexpr int PP_NS = 4;
+
+// M phase of the ping-pong kernel (head dim 128, 32 queries): O^T += V^T P^T of the previous tile (PV), then
+// S^T = K Q^T of this tile (SC), as one pipeline of 16-byte LDS fragment reads running PP_LA reads ahead of
+// the MFMAs. A scheduling barrier after every step keeps that order: left to itself the compiler issues all
+// 32 reads first, runs out of registers and moves O between register ranges on every tile. Each
+// accumulator sees its MFMAs in the order of attn_pv16 / attn_scores16, so the results are the same.
+constexpr int PP_LA = 3;
+template <bool IS_F16, bool PV, bool SC>
+__device__ __forceinline__ void attn_mphase16(const char* vt, const char* ks, const u32x4 (&qf)[1][8],
+                                              const u32x4 (&pf)[1][4], f32x16 (&o)[1][4], f32x16 (&sacc)[1][2],
+                                              int c, int hf) {
+  constexpr int N = (PV ? 16 : 0) + (SC ? 16 : 0);
+  // step i is P V^T step i / 2 (even i) or scores step i / 2 (odd i) when both run, so the MFMAs of one
+  // accumulator are 4 (P V^T) or 8 (scores) apart and none waits on the previous one's result
+  constexpr auto is_pv = [](int i) { return PV && (!SC || i % 2 == 0); };
+  constexpr auto idx = [](int i) { return PV && SC ? i / 2 : i; };
+  auto frag = [&](auto I) -> u32x4 {
+    constexpr int i = I;
+    if constexpr (is_pv(i)) {
+      constexpr int s = idx(i) / 4, db = idx(i) % 4;  // V^T rows 32 db + c, keys 16 s .. 16 s + 15
+      const int r = 32 * db + c;
+      return *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
+    } else {
+      constexpr int s = idx(i) / 2, b = idx(i) % 2;  // K row 32 b + c, dims 16 s .. 16 s + 15
+      const int r = 32 * b + c;
+      return *(const u32x4*)(ks + r * 256 + (((2 * s + hf) ^ (r & 15)) << 4));
+    }
+  };
+  if constexpr (SC) {
+    sacc[0][0] = f32x16{};
+    sacc[0][1] = f32x16{};
+  }
+  u32x4 f[PP_LA + 1];
+  static_for<0, PP_LA>([&](auto I) {
+    if constexpr (I < N) f[I] = frag(I);
+  });
+  static_for<0, N>([&](auto I) {
+    constexpr int i = I;
+    if constexpr (i + PP_LA < N) f[(i + PP_LA) % (PP_LA + 1)] = frag(std::integral_constant<int, i + PP_LA>{});
+    if constexpr (is_pv(i)) {
+      constexpr int s = idx(i) / 4, db = idx(i) % 4;
+      o[0][db] = mfma_32x32x16<IS_F16>(f[i % (PP_LA + 1)], pf[0][s], o[0][db]);
+    } else {
+      constexpr int s = idx(i) / 2, b = idx(i) % 2;
+      sacc[0][b] = mfma_32x32x16<IS_F16>(f[i % (PP_LA + 1)], qf[0][s], sacc[0][b]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+template <bool IS_F16, bool CAUSAL>
+__global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint16_t* vtg, uint32_t tp,
+                                                         uint32_t kv_heads) {
+  constexpr int DP = 128, NW = 8, IPW = 2;
+  constexpr int KS_BYTES = ATT_BN * DP * 2;  // 16 KB
+  constexpr int STAGE = 2 * KS_BYTES;        // K + V^T
+  __shared__ __attribute__((aligned(1024))) char lds[PP_NS * STAGE];
+
+  uint32_t qblk, h;
+  block_coords(a, qblk, h);
+  const uint32_t g = h / a.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int c = lane & 31, hf = lane >> 5;
+  const uint32_t q0 = qblk * DMA_BM;
+  const uint32_t qw[1] = {q0 + 32 * wave};
+  const uint32_t qi[1] = {qw[0] + c};
+  const uint16_t* Qp = (const uint16_t*)a.q;
+
+  u32x4 qf[1][DP / 16];
+  static_for<0, DP / 16>([&](auto S) {
+    constexpr int s = S;
+    qf[0][s] = u32x4{0, 0, 0, 0};
+    if (qi[0] < a.tokens) qf[0][s] = *(const u32x4*)(Qp + (size_t)qi[0] * a.qs + (size_t)h * DP + 16 * s + 8 * hf);
+  });
+
+  const uint32_t kv_end = CAUSAL ? min(a.tokens, q0 + DMA_BM) : a.tokens;
+  const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
+  const uint32_t k_bytes = ((a.tokens - 1) * a.ks + kv_heads * DP) * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.k, (short)0, (int)k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vtg, (short)0, (int)(kv_heads * DP * tp * 2), 0x00020000);
+  // instruction j (0 .. 15) fills K rows 4j .. 4j + 3, or V^T rows 8j .. 8j + 7; wave w issues j = w + 8u
+  auto issue = [&](int t) {
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    char* base = lds + (t % PP_NS) * STAGE;
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ (row & 15);
+      const uint32_t key = k0 + row;
+      dma16(rk, base + j * 1024, key < a.tokens ? (key * a.ks + g * DP + logical * 8) * 2 : kAttInvalid);
+    }
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 8 * j + (lane >> 3), phys = lane & 7, logical = phys ^ ((row >> 1) & 7);
+      dma16(rv, base + KS_BYTES + j * 1024, ((g * DP + row) * tp + k0 + logical * 8) * 2);
+    }
+  };
+  // own loads of tile t complete; the tiles issued after it (at most PP_NS - 1) may still be in flight
+  auto wait_tile = [&](int t) {
+    const int ahead = min(nt - 1, max(PP_NS - 1, t + 1)) - t;
+    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * IPW) : "memory");
+    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * IPW) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // tile t contributes to this wave's queries (causal: not entirely after them)
+  auto active = [&](int t) { return !CAUSAL || (uint32_t)t * ATT_BN <= qw[0] + 31; };
+  const char* kst = lds;             // K of tile t: kst + (t % PP_NS) * STAGE
+  const char* vst = lds + KS_BYTES;  // V^T of tile t
+
+  f32x16 o[1][DP / 32];
+  static_for<0, DP / 32>([&](auto D) { o[0][D] = f32x16{}; });
+  float m[1] = {-__builtin_inff()}, l[1] = {0.0f};
+  f32x16 sacc[1][2];
+  u32x4 pf[1][4];
+  for (int t = 0; t < PP_NS; t++)
+    if (t < nt) issue(t);
+  // Q is consumed here, so the compiler waits for its loads once, before the loop
+#pragma unroll
+  for (int ss = 0; ss < DP / 16; ss++) asm volatile("" ::"v"(qf[0][ss]));
+  wait_tile(0);
+  barrier();
+  if (grp == 1) barrier();  // group 1 runs one phase behind group 0
+  // tile 0: M(0) is the scores alone
+  if (active(0)) attn_mphase16<IS_F16, false, true>(nullptr, kst, qf, pf, o, sacc, c, hf);
+  if (grp == 1 && nt > 1) wait_tile(1);
+  barrier();
+  if (active(0)) attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, 0u, qw, qi, hf, a);
+  if (grp == 0 && nt > 1) wait_tile(1);
+  barrier();
+  for (int t = 1; t < nt; t++) {
+    if (grp == 0 && t >= 2 && t + 2 < nt) issue(t + 2);
+    const int cs = (t % PP_NS) * STAGE, ps = ((t - 1) % PP_NS) * STAGE;
+    // causal: the scores of a tile no query of this wave sees are computed and left unused
+    if (active(t - 1)) attn_mphase16<IS_F16, true, true>(vst + ps, kst + cs, qf, pf, o, sacc, c, hf);
+    if (grp == 1 && t + 1 < nt) wait_tile(t + 1);
+    barrier();
+    if (grp == 1 && t + 3 < nt) issue(t + 3);
+    if (active(t)) attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, qi, hf, a);
+    if (grp == 0 && t + 1 < nt) wait_tile(t + 1);
+    barrier();
+  }
+  // M(nt): the last P V^T
+  if (active(nt - 1)) attn_mphase16<IS_F16, true, false>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c, hf);
+  if (grp == 0) barrier();  // both groups pass the same number of barriers
+  attn_store16<DP, IS_F16>(o[0], l[0], qi[0], h, hf, a);
+}
+
 // ------------------------------------------------------------------------------------ f32 kernel
 template <int DP>
 __global__ void __launch_bounds__(ATT_NT, 1) attn32_kernel(AttnArgs a) {
@@ -572,8 +772,15 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
     if (e != hipSuccess) return e;
     a.nqb = (L.tokens + DMA_BM - 1) / DMA_BM;
     const dim3 grid(a.nqb * L.heads);
-    if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
-    else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+    const char* path = getenv("WE_ATTN_PATH");
+    if (path && strcmp(path, "ring") == 0) {
+      if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+      else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+    } else {
+      const auto kern = L.dtype == F16 ? (L.causal ? attn_pp_kernel<true, true> : attn_pp_kernel<true, false>)
+                                       : (L.causal ? attn_pp_kernel<false, true> : attn_pp_kernel<false, false>);
+      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+    }
     return hipGetLastError();
   }
   a.nqb = (L.tokens + ATT_BM - 1) / ATT_BM;
