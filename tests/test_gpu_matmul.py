@@ -360,11 +360,14 @@ def test_lora_down_split_over_long_k(graph):  # tests/gpu/lora.test.ts:120-146
     (37, 70, 1024, we.BF16, we.F32, we.EPI_BIAS | we.EPI_GELU),
     (1, 300, 2048, we.BF16, we.BF16, 0),
     (64, 1000, 4096, we.F16, we.F32, we.EPI_ACCUMULATE),
-    (33, 129, 768, we.F16, we.F16, we.EPI_BIAS)])
+    (33, 129, 768, we.F16, we.F16, we.EPI_BIAS),
+    (256, 384, 2048, we.BF16, we.F32, we.EPI_GELU), (256, 384, 2048, we.BF16, we.BF16, 0),
+    (200, 1000, 1024, we.BF16, we.F32, we.EPI_BIAS)])
 def test_small_m_split_k_reduction(graph, monkeypatch, m, n, k, x_dt, y_dt, flags):
-    """Small-M fp8 GEMMs split K across workgroups and the last slice of each tile adds the others. The
-    result matches the oracle, repeats bit for bit (slices are summed in slice order), and matches the
-    unsplit kernel within the same bar."""
+    """fp8 GEMMs whose tiles fill few workgroup slots (small M; or M > 64 with few tiles, like the
+    double-stream block's 512-token text projections) split K across workgroups and a reduce pass adds the
+    slices. The result matches the oracle, repeats bit for bit (slices are summed in slice order), and
+    matches the unsplit kernel within the same bar."""
     rng = np.random.default_rng(m * 7 + n + k)
     x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
     w = rng.integers(0, 254, n * k).astype(np.uint8)

@@ -670,8 +670,8 @@ bool fast_supported(const GemmLaunch& L, uint32_t kc) {
 constexpr uint32_t kCUs = 256;
 
 // Tile shape by predicted occupancy (fp8 weights). A 256 x 256 tile (one per CU) is the fastest per FLOP when
-// its tiles fill whole waves of the 256 CUs; 128 x 128 tiles (two per CU) lose ~4% per tile but quantize 4x finer;
-// 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
+// its tiles fill whole waves of the 256 CUs; 128 x 128 tiles (two per CU) lose ~10% per tile but quantize 4x
+// finer (4096 x 9216 x 3072: 256 x 192 239 us against 128 x 128 at 5 rounds, slower); 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
 // faster layout for the DiT shapes (M = 512 .. 4096, N = 3072 .. 12288, K = 3072 / 12288).
 int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
   if (m <= 32) return GEMM_CFG_32x64;
@@ -690,7 +690,7 @@ int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
     double base;
   };
   const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, 0.85},
-                        {GEMM_CFG_128x128, 128, 128, 2, 0.96}, {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
+                        {GEMM_CFG_128x128, 128, 128, 2, 0.90}, {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
   int best = GEMM_CFG_128x128;
   double best_score = -1.0;
   for (const Cand& c : cands) {
@@ -723,13 +723,22 @@ uint32_t cfg_bn(int cfg) {
 GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits) {
   GemmReducePlan p{1, L.k, 0};
   if (L.generic || (L.splits > 1) || (L.flags & WE_EPI_SPLIT_K_BIT) || L.m == 0 || L.n == 0) return p;
-  if (L.m > 64 || L.k < 512 || !fast_supported(L, L.k)) return p;
+  if (L.k < 512 || !fast_supported(L, L.k)) return p;
   const int cfg = L.cfg >= 0 ? L.cfg : pick_fast_cfg(L.m, L.n, 1, L.w_dtype == FP8);
   const uint64_t tiles = (uint64_t)((L.m + cfg_bm(cfg) - 1) / cfg_bm(cfg)) * ((L.n + cfg_bn(cfg) - 1) / cfg_bn(cfg));
-  if (tiles >= kCUs / 2) return p;
-  uint32_t rs = (uint32_t)((kCUs + tiles - 1) / tiles);  // about one workgroup per CU (measured: 4 .. 12 slices
-                                                          // of M = 64, K = 3072 within 2%)
-  rs = rs < L.k / 256 ? rs : L.k / 256;                        // every slice keeps at least 256 of K
+  uint32_t rs;
+  if (L.m <= 64) {
+    if (tiles >= kCUs / 2) return p;
+    rs = (uint32_t)((kCUs + tiles - 1) / tiles);  // about one workgroup per CU (measured: 4 .. 12 slices of
+                                                   // M = 64, K = 3072 within 2%)
+  } else {
+    // larger M: split when the tiles fill less than half of the workgroup slots (M = 512, N = 3072:
+    // 96 tiles of 128 x 128 for 512 slots), to about one workgroup per slot
+    const uint64_t slots = (uint64_t)kCUs * (cfg == GEMM_CFG_128x128 ? 2 : 1);
+    if (tiles * 2 > slots) return p;
+    rs = (uint32_t)((slots + tiles - 1) / tiles);
+  }
+  rs = rs < L.k / 256 ? rs : L.k / 256;  // every slice keeps at least 256 of K
   if (force_splits) rs = force_splits < L.k / BK ? force_splits : L.k / BK;
   if (rs < 2) return p;
   const uint32_t kc = (L.k + rs * BK - 1) / (rs * BK) * BK;
