@@ -57,6 +57,31 @@ def test_rmsnorm_bf16_storage(graph, rows, d):
     assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 1e-6)
 
 
+@pytest.mark.parametrize("dtype,d", [(we.BF16, 3072), (we.F16, 2048), (we.BF16, 6144)])
+def test_rmsnorm_16bit_modulated_rows(graph, dtype, d):
+    """The double-stream block's modulated norm on 16-bit rows (one wave per row, 16-byte accesses): weight,
+    scale and shift per column, against the f64 oracle at one rounding of the output type."""
+    rows = 37
+    rng = np.random.default_rng(d + dtype)
+    x32 = rng.standard_normal(rows * d).astype(np.float32) * 3
+    w = rng.uniform(-0.2, 0.2, d).astype(np.float32)
+    sc = rng.uniform(-1, 1, d).astype(np.float32)
+    sh = rng.uniform(-1, 1, d).astype(np.float32)
+    if dtype == we.BF16:
+        x = O.bf16_rne(x32)
+        xv = O.bf16_to_f32(x)
+    else:
+        x = x32.astype(np.float16).view(np.uint16)
+        xv = x32.astype(np.float16).astype(np.float32)
+    out = we.norm(graph, graph.buffer(x), graph.buffer(w), rows, d, we.Mod(graph.buffer(sc), graph.buffer(sh)),
+                  eps=1e-6, dtype=dtype)
+    raw = graph.read(out, dtype=np.uint16, count=rows * d)
+    got = (O.bf16_to_f32(raw) if dtype == we.BF16 else raw.view(np.float16).astype(np.float32)).astype(np.float64)
+    want = O.rmsnorm(xv, w, 1e-6, 1.0, sc, sh)
+    ulp = 2 ** -8 if dtype == we.BF16 else 2 ** -11
+    assert np.all(np.abs(got - want) <= ulp * np.abs(want) + 1e-5)
+
+
 def test_rope_interleaved_three_axes(graph):  # tests/gpu/rope.test.ts:5-22
     heads = 3
     pos = O.rope_positions(2, 3, 4, 3)
@@ -109,13 +134,14 @@ def test_fused_qk_norm_rope(graph, half, dtype):
     assert np.all(np.abs(got - want) <= tol * np.maximum(np.abs(want), 1.0))
 
 
-def test_fused_qk_norm_rope_strided_in_place(graph):
+@pytest.mark.parametrize("hd", [64, 128])
+def test_fused_qk_norm_rope_strided_in_place(graph, hd):
     """q/k normalized and rotated in place inside a fused [tokens, 3 * heads * head_dim] QKV row: the k slice
     equals the dense result, the q and v slices are untouched."""
-    text, rows, cols, heads, hd = 4, 3, 5, 2, 64
+    text, rows, cols, heads = 4, 3, 5, 2
     tokens, row = text + rows * cols, heads * hd
     pos = O.rope_positions(0, rows, cols, 2)
-    cos, sin, pairs = O.rope_tables(pos, [32, 32], 10000.0)
+    cos, sin, pairs = O.rope_tables(pos, [hd // 2, hd // 2], 10000.0)
     rng = np.random.default_rng(8)
     qkv = O.bf16_rne(rng.standard_normal(tokens * 3 * row).astype(np.float32))
     w = rng.uniform(-0.3, 0.3, hd).astype(np.float32)

@@ -176,9 +176,81 @@ __global__ void __launch_bounds__(256) rmsnorm_block_kernel(uint32_t rows, uint3
   }
 }
 
+// 16-bit rows with d a multiple of 8 (up to 8 * 64 * NCH): one wave per row, 16-byte loads and stores, the
+// row held in registers between the sum of squares and the scaling (x is read once). Same per-value
+// expression as the kernels above; weight / scale / shift are read as f32x4.
+template <int DT, int NCH>
+__global__ void __launch_bounds__(256) rmsnorm_vec_kernel(uint32_t rows, uint32_t d, float eps, float offset,
+                                                         const u32x4* x, const float* weight, const float* scale,
+                                                         const float* shift, u32x4* out) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint32_t nc = d / 8;
+  const u32x4* xr = x + (size_t)row * nc;
+  u32x4* orow = out + (size_t)row * nc;
+  float v[NCH][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NCH; q++) {
+    const uint32_t c = lane + 64 * q;
+    const u32x4 r = c < nc ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint16_t hbits = (uint16_t)(r[e / 2] >> (16 * (e % 2)));
+      v[q][e] = DT == BF16 ? bf16_to_f32(hbits) : f16_to_f32(hbits);
+      ss += v[q][e] * v[q][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+  const std::integral_constant<bool, DT == F16> tag;
+#pragma unroll
+  for (int q = 0; q < NCH; q++) {
+    const uint32_t c = lane + 64 * q;
+    if (c >= nc) continue;
+    float w[8], sc[8], sh[8];
+    *(f32x4*)&w[0] = *(const f32x4*)(weight + 8 * c);
+    *(f32x4*)&w[4] = *(const f32x4*)(weight + 8 * c + 4);
+#pragma unroll
+    for (int e = 0; e < 8; e++) sc[e] = sh[e] = 0.0f;
+    if (scale) {
+      *(f32x4*)&sc[0] = *(const f32x4*)(scale + 8 * c);
+      *(f32x4*)&sc[4] = *(const f32x4*)(scale + 8 * c + 4);
+    }
+    if (shift) {
+      *(f32x4*)&sh[0] = *(const f32x4*)(shift + 8 * c);
+      *(f32x4*)&sh[4] = *(const f32x4*)(shift + 8 * c + 4);
+    }
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = v[q][e] * inv * (offset + w[e]) * (1.0f + sc[e]) + sh[e];
+    orow[c] = u32x4{pack2(y[0], y[1], tag), pack2(y[2], y[3], tag), pack2(y[4], y[5], tag), pack2(y[6], y[7], tag)};
+  }
+}
+
+template <int DT>
+static bool rmsnorm_vec(uint32_t rows, uint32_t d, float eps, float offset, const void* x, const float* w,
+                        const float* sc, const float* sh, void* out, hipStream_t s) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (d % 8 || d > 8 * 64 * 12 || !a16(x) || !a16(out) || !a16(w) || !a16(sc) || !a16(sh)) return false;
+  const dim3 g((rows + 3) / 4), t(256);
+  const uint32_t nch = (d / 8 + 63) / 64;
+  const u32x4 *xv = (const u32x4*)x;
+  u32x4* ov = (u32x4*)out;
+  if (nch <= 4) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
+  else if (nch <= 6) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 6>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
+  else if (nch <= 8) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
+  else hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 12>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
+  return true;
+}
+
 template <int DT>
 static void rmsnorm_dt(uint32_t rows, uint32_t d, float eps, float offset, const void* x, const float* w,
                        const float* sc, const float* sh, void* out, hipStream_t s) {
+  if constexpr (DT != F32) {
+    if (d > 1024 && rmsnorm_vec<DT>(rows, d, eps, offset, x, w, sc, sh, out, s)) return;
+  }
   if (d <= 1024)
     hipLaunchKernelGGL(rmsnorm_wave_kernel<DT>, dim3((rows + 3) / 4), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh,
                        out);
@@ -287,11 +359,71 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(uint32_t tokens, uint
   }
 }
 
+// Head dim 128, interleaved pairs, 16-bit values, 16-byte aligned rows: 16 lanes per (token, head) row, lane
+// l holding values 8l .. 8l + 7 (pairs 4l .. 4l + 3) in one 16-byte load; four rows per wave. Same per-value
+// expressions as qk_norm_rope_kernel.
+template <int DT>
+__global__ void __launch_bounds__(256) qk_norm_rope_vec_kernel(uint32_t tokens, uint32_t heads, float eps, float offset,
+                                                              const float* weight, uint32_t rope_from, const float* cs,
+                                                              const float* sn, const uint16_t* x, uint32_t xs,
+                                                              uint16_t* out, uint32_t os) {
+  const size_t row = (size_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
+  const bool valid = row < (size_t)tokens * heads;
+  const uint32_t t = valid ? (uint32_t)(row / heads) : 0u, hh = valid ? (uint32_t)(row % heads) : 0u;
+  const size_t base = (size_t)t * xs + (size_t)hh * 128 + 8 * l;
+  const u32x4 r = valid ? *(const u32x4*)(x + base) : u32x4{0u, 0u, 0u, 0u};
+  float v[8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const uint16_t hbits = (uint16_t)(r[e / 2] >> (16 * (e % 2)));
+    v[e] = DT == BF16 ? bf16_to_f32(hbits) : f16_to_f32(hbits);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; p++) ss += v[2 * p] * v[2 * p] + v[2 * p + 1] * v[2 * p + 1];
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);  // the 16 lanes of the row
+  if (!valid) return;
+  const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+  float w[8];
+  *(f32x4*)&w[0] = *(const f32x4*)(weight + 8 * l);
+  *(f32x4*)&w[4] = *(const f32x4*)(weight + 8 * l + 4);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) y[e] = v[e] * inv * (offset + w[e]);
+  if (t >= rope_from) {
+    const size_t ti = (size_t)(t - rope_from) * 64 + 4 * l;
+    const f32x4 c4 = *(const f32x4*)(cs + ti), s4 = *(const f32x4*)(sn + ti);
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const float a = y[2 * p], b = y[2 * p + 1];
+      y[2 * p] = a * c4[p] - b * s4[p];
+      y[2 * p + 1] = b * c4[p] + a * s4[p];
+    }
+  }
+  const std::integral_constant<bool, DT == F16> tag;
+  *(u32x4*)(out + (size_t)t * os + (size_t)hh * 128 + 8 * l) =
+      u32x4{pack2(y[0], y[1], tag), pack2(y[2], y[3], tag), pack2(y[4], y[5], tag), pack2(y[6], y[7], tag)};
+}
+
 hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,
                                const float* weight, uint32_t rope_from, int half, const float* c, const float* sn,
                                int dtype, const void* x, uint32_t xs, void* out, uint32_t os, hipStream_t s) {
   const size_t rows = (size_t)tokens * heads;
   if (rows == 0) return hipSuccess;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if ((dtype == BF16 || dtype == F16) && head_dim == 128 && !half && xs % 8 == 0 && os % 8 == 0 && a16(x) &&
+      a16(out) && a16(weight) && a16(c) && a16(sn)) {
+    const dim3 g((unsigned)((rows + 15) / 16)), t(256);
+    if (dtype == BF16)
+      hipLaunchKernelGGL(qk_norm_rope_vec_kernel<BF16>, g, t, 0, s, tokens, heads, eps, offset, weight, rope_from, c, sn,
+                         (const uint16_t*)x, xs, (uint16_t*)out, os);
+    else
+      hipLaunchKernelGGL(qk_norm_rope_vec_kernel<F16>, g, t, 0, s, tokens, heads, eps, offset, weight, rope_from, c, sn,
+                         (const uint16_t*)x, xs, (uint16_t*)out, os);
+    return hipGetLastError();
+  }
   const dim3 g((unsigned)((rows + 3) / 4)), t(256);
   switch (dtype) {
     case F16:
