@@ -671,7 +671,7 @@ constexpr uint32_t kCUs = 256;
 
 // Tile shape by predicted occupancy (fp8 weights). A 256 x 256 tile (one per CU) is the fastest per FLOP when
 // its tiles fill whole waves of the 256 CUs; 128 x 128 tiles (two per CU) lose ~10% per tile but quantize 4x
-// finer (4096 x 9216 x 3072: 256 x 192 239 us against 128 x 128 at 5 rounds, slower); 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
+// finer (4096 x 9216 x 3072 in one process: 256 x 192 206 us, 128 x 128 225 us); 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
 // faster layout for the DiT shapes (M = 512 .. 4096, N = 3072 .. 12288, K = 3072 / 12288).
 int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
   if (m <= 32) return GEMM_CFG_32x64;
