@@ -82,6 +82,19 @@ int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep);     
 int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes); /* Graph.stats */
 int we_sync(we_ctx* ctx); /* device.queue.onSubmittedWorkDone(), called from src/model/weights.ts:128 */
 
+/* Two compute streams. No counterpart in the reference, whose WebGPU queue is one ordered stream: for
+ * callers that overlap independent work, like the double-stream block's text and image streams.
+ * we_stream_select picks the stream that later calls queue on (0: the main stream, 1: the second one);
+ * each stream has its own kernel scratch. we_stream_fork makes stream 1 wait for the work queued so far on
+ * stream 0; we_stream_join makes stream 0 wait for the work queued so far on stream 1. Work on the two
+ * streams is ordered only through these two calls (we_sync waits for both). Buffers that stream 1 uses, or
+ * that are allocated while it is selected (they are zeroed on it), are ready for stream 0 after a join; do
+ * not free or release them before one. Timers, tickets, downloads and graph capture use the selected
+ * stream; selecting, forking and joining are refused during a capture. */
+int we_stream_select(we_ctx* ctx, int stream);
+int we_stream_fork(we_ctx* ctx);
+int we_stream_join(we_ctx* ctx);
+
 /* ---- pinned host memory and weight streaming: replaces the per-block upload pacing of
  * loadTransformer (src/model/weights.ts:124-129) and runAhead (src/gpu/run-ahead.ts:7-21) ---- */
 int we_host_alloc(we_ctx* ctx, size_t bytes, void** out); /* pinned (hipHostMalloc) */

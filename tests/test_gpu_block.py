@@ -232,6 +232,35 @@ def test_double_block_full_shape_runs_and_zero_gates_are_identity(graph):
     graph.release(mark)
 
 
+def test_double_block_overlapped_streams_equal_serial(graph):
+    """The text stream on the second compute stream beside the image stream (the default) gives the serial
+    block's outputs bit for bit at the full shape (512 + 4096 tokens, hidden 3072, bf16), forward after
+    forward (the text GEMMs' split-K slices use that stream's own scratch)."""
+    cfg, tt, rows, cols = B.DIT_DOUBLE_BLOCK, 512, 64, 64
+    ti, H = rows * cols, cfg.hidden
+    rng = np.random.default_rng(9)
+    tvec = rng.uniform(-.2, .2, 6 * H).astype(np.float32)
+    mark = graph.mark()
+    rope = B.rope_for_image(graph, rows, cols)
+    xt = O.bf16_rne(rng.standard_normal(tt * H).astype(np.float32))
+    xi = O.bf16_rne(rng.standard_normal(ti * H).astype(np.float32))
+    bx_t, bx_i, tv = graph.buffer(xt), graph.buffer(xi), graph.buffer(tvec)
+    layout, host, scales = _layout_weights(graph, cfg, rng)
+    slot = graph.buffer(host)
+    w_t, w_i = layout.weights(slot, scales)
+    outs = {}
+    for overlap in (False, True):
+        blk = B.DoubleBlock(graph, cfg, tt, ti, we.BF16, overlap=overlap)
+        out_t, out_i = graph.buffer(tt * H * 2), graph.buffer(ti * H * 2)
+        for _ in range(2):
+            blk.forward(w_t, w_i, bx_t, bx_i, tv, rope, out_t, out_i)
+        outs[overlap] = (graph.read(out_t).view(np.uint16), graph.read(out_i).view(np.uint16))
+    assert np.array_equal(outs[True][0], outs[False][0])
+    assert np.array_equal(outs[True][1], outs[False][1])
+    assert not np.array_equal(outs[True][1], xi)
+    graph.release(mark)
+
+
 def test_streamed_weights_give_the_resident_result(graph):
     """Three blocks whose weights stream through two device slots from pinned host memory equal the same blocks
     run from resident copies of their weights, bit for bit."""

@@ -42,7 +42,8 @@ EXPORTS = {
     "we_graph_begin": "graphBegin", "we_graph_end": "graphEnd", "we_graph_launch": "graphLaunch",
     "we_graph_destroy": "graphDestroy", "we_peak": "peak", "we_read_peak": "readPeak", "we_st_open": "stOpen", "we_st_close": "stClose", "we_st_count": "stCount",
     "we_st_info": "stInfo", "we_st_find": "stFind", "we_st_metadata_count": "stMetadataCount",
-    "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead",
+    "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead", "we_stream_select": "streamSelect",
+    "we_stream_fork": "streamFork", "we_stream_join": "streamJoin",
 }
 
 

@@ -140,9 +140,12 @@ class StreamWeights:
 
 
 class DoubleBlock:
-    """The double-stream block at fixed token counts, with its workspace allocated once."""
+    """The double-stream block at fixed token counts, with its workspace allocated once. With overlap (the
+    default) the text stream's steps run on the context's second compute stream, beside the image stream's:
+    the two streams meet only in the joint attention, and the text stream's small GEMMs fill workgroup slots
+    the image stream leaves free. The result is the same bit for bit."""
 
-    def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16):
+    def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16, overlap=True):
         if cfg.heads != cfg.kv_heads or cfg.heads * cfg.head_dim != cfg.hidden:
             raise ValueError("the double-stream block needs heads == kvHeads and heads * headDim == hidden")
         self.graph, self.cfg, self.dtype = graph, cfg, dtype
@@ -153,14 +156,36 @@ class DoubleBlock:
         big = max(self.rows)
         self.qkv = graph.buffer(self.tokens * 3 * H * e)
         self.o = graph.buffer(self.tokens * H * e)
-        self.h = graph.buffer(big * H * e)
-        self.u = graph.buffer(big * cfg.mlp * e)
+        self.overlap = overlap
+        if overlap:  # each stream its own norm output and MLP hidden
+            self.h = [graph.buffer(r * H * e) for r in self.rows]
+            self.u = [graph.buffer(r * cfg.mlp * e) for r in self.rows]
+        else:
+            h, u = graph.buffer(big * H * e), graph.buffer(big * cfg.mlp * e)
+            self.h, self.u = [h, h], [u, u]
         self.x1 = [graph.buffer(r * H * e) for r in self.rows]
         self.mod = [graph.buffer(6 * H * 4) for _ in self.rows]
 
     def free(self):
-        for b in [self.qkv, self.o, self.h, self.u] + self.x1 + self.mod:
+        for b in [self.qkv, self.o] + list({id(b): b for b in self.h + self.u}.values()) + self.x1 + self.mod:
             self.graph.free(b)
+
+    def _streams(self, step):
+        """step(s) for the text (s = 0) and image (s = 1) streams: text on the second compute stream when
+        overlapping, then stream 0 waits for it."""
+        g = self.graph
+        if not self.overlap:
+            step(0)
+            step(1)
+            return
+        g.fork()
+        g.stream(1)
+        try:
+            step(0)
+        finally:
+            g.stream(0)
+        step(1)
+        g.join()
 
     def forward(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img):
         """x_s, out_s: [rows_s, hidden] of the block's dtype; tvec f32 [6 hidden]; rope_img: we.Rope over the
@@ -169,34 +194,39 @@ class DoubleBlock:
         H, hd, heads, e = cfg.hidden, cfg.head_dim, cfg.heads, we.ELEM_BYTES[dt]
         sl = we.Graph.slice
         ws, xs, outs = (w_txt, w_img), (x_txt, x_img), (out_txt, out_img)
-        for s in range(2):
-            w, rows, r0 = ws[s], self.rows[s], self.row0[s]
+
+        def qkv_step(s):
+            w, rows, r0, h = ws[s], self.rows[s], self.row0[s], self.h[s]
             g.elementwise(we.OP_ADD, 6 * H, 1, we.F32, tvec, w.table, None, self.mod[s])
             mod = self.mod[s]
-            g.rmsnorm(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1, sl(mod, 0, H * 4), sl(mod, H * 4, H * 4), self.h)
+            g.rmsnorm(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1, sl(mod, 0, H * 4), sl(mod, H * 4, H * 4), h)
             p = we.matmul_params(rows, 3 * H, H, w.qkv.scale, y_offset=r0 * 3 * H, graph=g)
-            g.matmul(p, dt, self.h, we.FP8, w.qkv.buffer, dt, self.qkv)
+            g.matmul(p, dt, h, we.FP8, w.qkv.buffer, dt, self.qkv)
             rotate = s == 1
             for part, norm_w in ((0, w.norm_q), (1, w.norm_k)):
                 base = sl(self.qkv, (r0 * 3 * H + part * H) * e, 0)
                 g.qk_norm_rope(rows, heads, hd, cfg.eps, 1.0, norm_w, 0 if rotate else rows, False,
                                rope_img.cos if rotate else None, rope_img.sin if rotate else None, dt, base, base,
                                x_stride=3 * H, out_stride=3 * H)
-        g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
-                    sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
-        for s in range(2):
-            w, rows, r0, mod = ws[s], self.rows[s], self.row0[s], self.mod[s]
+
+        def out_step(s):
+            w, rows, r0, mod, h, u = ws[s], self.rows[s], self.row0[s], self.mod[s], self.h[s], self.u[s]
             # x1 = x + gate1 * proj(o), the gated residual in the projection's epilogue
             p = we.matmul_params(rows, H, H, w.proj.scale, x_offset=r0 * H, graph=g)
             g.matmul(p, dt, self.o, we.FP8, w.proj.buffer, dt, self.x1[s], gate=sl(mod, 2 * H * 4, H * 4),
                      residual=xs[s])
             g.rmsnorm(rows, H, cfg.eps, 1.0, dt, self.x1[s], w.norm2, sl(mod, 3 * H * 4, H * 4),
-                      sl(mod, 4 * H * 4, H * 4), self.h)
-            g.matmul(we.matmul_params(rows, cfg.mlp, H, w.up.scale, graph=g), dt, self.h, we.FP8, w.up.buffer, dt,
-                     self.u, flags=we.EPI_GELU)
+                      sl(mod, 4 * H * 4, H * 4), h)
+            g.matmul(we.matmul_params(rows, cfg.mlp, H, w.up.scale, graph=g), dt, h, we.FP8, w.up.buffer, dt,
+                     u, flags=we.EPI_GELU)
             # out = x1 + gate2 * down(u), fused likewise
-            g.matmul(we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, self.u, we.FP8, w.down.buffer, dt,
+            g.matmul(we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, u, we.FP8, w.down.buffer, dt,
                      outs[s], gate=sl(mod, 5 * H * 4, H * 4), residual=self.x1[s])
+
+        self._streams(qkv_step)
+        g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
+                    sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
+        self._streams(out_step)
 
 
 # ------------------------------------------------------------------------------------------ weight streaming

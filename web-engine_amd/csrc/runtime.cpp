@@ -39,9 +39,16 @@ struct we_ctx {
   uint64_t created = 0, reused = 0, created_bytes = 0;
   std::vector<hipEvent_t> tickets;
   uint64_t next_ticket = 1;
-  void* scratch = nullptr;  // kernel scratch (split-K partial sums, attention V^T), grown on demand
-  bool capturing = false;   // between we_graph_begin and we_graph_end
+  void* scratch = nullptr;  // kernel scratch (split-K partial sums, attention V^T) of the selected compute
+  bool capturing = false;   // stream, grown on demand; between we_graph_begin and we_graph_end
   size_t scratch_bytes = 0;
+  // two compute streams (default priority): `compute`, `scratch` and `scratch_bytes` are those of lanes[lane];
+  // the other lane's scratch waits in lane_scratch until it is selected again
+  hipStream_t lanes[2] = {nullptr, nullptr};
+  int lane = 0;
+  void* lane_scratch[2] = {nullptr, nullptr};
+  size_t lane_scratch_bytes[2] = {0, 0};
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   hipDeviceProp_t prop{};
 };
 
@@ -166,8 +173,13 @@ int we_ctx_create(int device, we_ctx** out) {
   };
   if (hipSetDevice(device) != hipSuccess) return cleanup(WE_EHIP);
   if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return cleanup(WE_EHIP);
-  if (hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
+  for (auto& st : ctx->lanes)
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
+  ctx->compute = ctx->lanes[0];
   if (hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
+  if (hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess)
+    return cleanup(WE_EHIP);
   if (hipEventCreate(&ctx->t0) != hipSuccess || hipEventCreate(&ctx->t1) != hipSuccess) return cleanup(WE_EHIP);
   ctx->tickets.resize(kTicketRing, nullptr);
   for (auto& e : ctx->tickets)
@@ -184,16 +196,21 @@ int we_ctx_destroy(we_ctx* ctx) {
     if (hipStreamEndCapture(ctx->compute, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
     ctx->capturing = false;
   }
-  if (ctx->compute) (void)hipStreamSynchronize(ctx->compute);
+  for (auto st : ctx->lanes)
+    if (st) (void)hipStreamSynchronize(st);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
   for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->lane_scratch[1 - ctx->lane]) (void)hipFree(ctx->lane_scratch[1 - ctx->lane]);
   for (auto& kv : ctx->pinned) (void)hipHostFree((void*)kv.first);
   for (auto& e : ctx->tickets)
     if (e) (void)hipEventDestroy(e);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
-  if (ctx->compute) (void)hipStreamDestroy(ctx->compute);
+  if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+  if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
+  for (auto st : ctx->lanes)
+    if (st) (void)hipStreamDestroy(st);
   if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
   delete ctx;
   return WE_OK;
@@ -328,7 +345,44 @@ int we_sync(we_ctx* ctx) {
   if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   HIP_OK(ctx, hipStreamSynchronize(ctx->copy), "copy stream");
-  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "compute stream");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->lanes[0]), "compute stream");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->lanes[1]), "second compute stream");
+  return WE_OK;
+}
+
+// ------------------------------------------------------------------------------------------ two compute streams
+
+int we_stream_select(we_ctx* ctx, int stream) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (stream != 0 && stream != 1) return fail(ctx, WE_EINVAL, "stream must be 0 or 1, got %d", stream);
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  if (stream == ctx->lane) return WE_OK;
+  ctx->lane_scratch[ctx->lane] = ctx->scratch;
+  ctx->lane_scratch_bytes[ctx->lane] = ctx->scratch_bytes;
+  ctx->scratch = ctx->lane_scratch[stream];
+  ctx->scratch_bytes = ctx->lane_scratch_bytes[stream];
+  ctx->lane_scratch[stream] = nullptr;
+  ctx->lane_scratch_bytes[stream] = 0;
+  ctx->compute = ctx->lanes[stream];
+  ctx->lane = stream;
+  return WE_OK;
+}
+
+int we_stream_fork(we_ctx* ctx) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipEventRecord(ctx->fork_ev, ctx->lanes[0]), "hipEventRecord");
+  HIP_OK(ctx, hipStreamWaitEvent(ctx->lanes[1], ctx->fork_ev, 0), "hipStreamWaitEvent");
+  return WE_OK;
+}
+
+int we_stream_join(we_ctx* ctx) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  HIP_OK(ctx, hipEventRecord(ctx->join_ev, ctx->lanes[1]), "hipEventRecord");
+  HIP_OK(ctx, hipStreamWaitEvent(ctx->lanes[0], ctx->join_ev, 0), "hipStreamWaitEvent");
   return WE_OK;
 }
 

@@ -72,6 +72,21 @@ class Graph {
     addon.sync(this.ctx);
   }
 
+  /** Two compute streams: later calls queue on stream `which` (0: main, 1: second). */
+  stream(which) {
+    addon.streamSelect(this.ctx, which);
+  }
+
+  /** Stream 1 waits for the work queued so far on stream 0. */
+  fork() {
+    addon.streamFork(this.ctx);
+  }
+
+  /** Stream 0 waits for the work queued so far on stream 1. */
+  join() {
+    addon.streamJoin(this.ctx);
+  }
+
   deviceInfo() {
     return addon.deviceInfo(this.ctx);
   }

@@ -161,6 +161,31 @@ static napi_value Sync(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_sync(ctx));
 }
 
+static napi_value StreamSelect(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  int which = (int)f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_stream_select(ctx, which));
+}
+
+static napi_value StreamFork(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_stream_fork(ctx));
+}
+
+static napi_value StreamJoin(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_stream_join(ctx));
+}
+
 /* ---- buffers ---- */
 static napi_value BufAlloc(napi_env env, napi_callback_info info) {
   args_t a;
@@ -863,7 +888,7 @@ static napi_value Init(napi_env env, napi_value exports) {
     napi_callback fn;
   } fns[] = {
       {"create", Create},         {"destroy", Destroy},       {"deviceInfo", DeviceInfo},
-      {"sync", Sync},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
+      {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite},

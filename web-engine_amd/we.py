@@ -74,6 +74,9 @@ SIGNATURES = {
     "we_release": (_I, [_P, _SZ, _P, _SZ]),
     "we_stats": (_I, [_P, _P, _P, _P]),
     "we_sync": (_I, [_P]),
+    "we_stream_select": (_I, [_P, ctypes.c_int]),
+    "we_stream_fork": (_I, [_P]),
+    "we_stream_join": (_I, [_P]),
     "we_host_alloc": (_I, [_P, _SZ, _P]),
     "we_host_free": (_I, [_P, _P]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
@@ -233,6 +236,19 @@ class Graph:
 
     def sync(self):
         self.check(self.lib.we_sync(self.ctx))
+
+    # ---- two compute streams (we_stream_select / fork / join)
+    def stream(self, which):
+        """Queue later calls on compute stream `which` (0: main, 1: second)."""
+        self.check(self.lib.we_stream_select(self.ctx, which))
+
+    def fork(self):
+        """Stream 1 waits for the work queued so far on stream 0."""
+        self.check(self.lib.we_stream_fork(self.ctx))
+
+    def join(self):
+        """Stream 0 waits for the work queued so far on stream 1."""
+        self.check(self.lib.we_stream_join(self.ctx))
 
     on_submitted_work_done = sync
 
