@@ -96,11 +96,15 @@ __device__ __forceinline__ void attn_scores16(const char* ks, const u32x4 (&qf)[
   });
 }
 
-template <int DP, bool IS_F16, int QB>
-__device__ __forceinline__ void attn_softmax16(const f32x16 (&sacc)[QB][2], u32x4 (&pf)[QB][4],
+// FAST (QB = 1): the caller's running max must not move; if it would, the call returns false and changes
+// nothing (the caller redoes the tile with the general version). O is then never multiplied.
+template <int DP, bool IS_F16, int QB, bool FAST = false>
+__device__ __forceinline__ bool attn_softmax16(const f32x16 (&sacc)[QB][2], u32x4 (&pf)[QB][4],
                                                f32x16 (&o)[QB][DP / 32], float (&m)[QB], float (&l)[QB], uint32_t k0,
                                                const uint32_t (&qw)[QB], const uint32_t (&qi)[QB], int hf,
                                                const AttnArgs& a) {
+  static_assert(!FAST || QB == 1, "the fast softmax handles one query block");
+  bool ok = true;
   static_for<0, QB>([&](auto Q) {
     constexpr int qb = Q;
     // raw scores; keys past the end (or after the query, causal) get -inf
@@ -123,6 +127,12 @@ __device__ __forceinline__ void attn_softmax16(const f32x16 (&sacc)[QB][2], u32x
     // max rise by more than 8 (log2 units); otherwise the stale max stays the shift, so p <= 2^8. Softmax is
     // invariant to the shift, and the wave skips 64 multiplies of O on most tiles.
     const bool rescale = __any(mn > m[qb] + 8.0f);
+    if constexpr (FAST) {
+      if (rescale) {
+        ok = false;
+        return;
+      }
+    }
     const float mref = rescale ? mn : m[qb];
     const float ms = mref == -__builtin_inff() ? 0.0f : mref;
     float ps = 0.0f;
@@ -138,13 +148,18 @@ __device__ __forceinline__ void attn_softmax16(const f32x16 (&sacc)[QB][2], u32x
         pf[qb][s][j] = pack2(p[2 * j], p[2 * j + 1], std::integral_constant<bool, IS_F16>{});
       });
     });
-    // alpha = 1 unless the max moved; multiplying O by it on every tile keeps O in one set of registers
-    // (a branch around the multiply makes the compiler copy all of O on the path that skips it)
-    const float alpha = rescale ? __builtin_amdgcn_exp2f(m[qb] - ms) : 1.0f;
-    l[qb] = __builtin_fmaf(l[qb], alpha, ps);
-    if (rescale) m[qb] = mn;
-    static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
+    if constexpr (FAST) {
+      l[qb] = __builtin_fmaf(l[qb], 1.0f, ps);
+    } else {
+      // alpha = 1 unless the max moved; multiplying O by it on every tile keeps O in one set of registers
+      // (a branch around the multiply makes the compiler copy all of O on the path that skips it)
+      const float alpha = rescale ? __builtin_amdgcn_exp2f(m[qb] - ms) : 1.0f;
+      l[qb] = __builtin_fmaf(l[qb], alpha, ps);
+      if (rescale) m[qb] = mn;
+      static_for<0, DP / 32>([&](auto D) { o[qb][D] *= alpha; });
+    }
   });
+  return ok;
 }
 
 template <int DP, bool IS_F16, int QB>
@@ -589,7 +604,7 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
   if (active(0)) attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, 0u, qw, qi, hf, a);
   if (grp == 0 && nt > 1) wait_tile(1);
   barrier();
-  for (int t = 1; t < nt; t++) {
+  auto m_half = [&](int t) {
     if (grp == 0 && t >= 2 && t + 2 < nt) issue(t + 2);
     const int cs = (t % PP_NS) * STAGE, ps = ((t - 1) % PP_NS) * STAGE;
     // causal: the scores of a tile no query of this wave sees are computed and left unused
@@ -597,9 +612,28 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
     if (grp == 1 && t + 1 < nt) wait_tile(t + 1);
     barrier();
     if (grp == 1 && t + 3 < nt) issue(t + 3);
-    if (active(t)) attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, qi, hf, a);
+  };
+  auto v_end = [&](int t) {
     if (grp == 0 && t + 1 < nt) wait_tile(t + 1);
     barrier();
+  };
+  // While no query's max moves (most tiles once the first has set it), the softmax never touches O. The
+  // first tile that would move it, and every tile after, takes the general step (O multiplied by alpha).
+  int t = 1;
+  for (; t < nt; t++) {
+    m_half(t);
+    if (active(t) && !attn_softmax16<DP, IS_F16, 1, true>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, qi, hf, a))
+      break;
+    v_end(t);
+  }
+  if (t < nt) {
+    attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, qi, hf, a);
+    v_end(t);
+    for (t++; t < nt; t++) {
+      m_half(t);
+      if (active(t)) attn_softmax16<DP, IS_F16, 1>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, qi, hf, a);
+      v_end(t);
+    }
   }
   // M(nt): the last P V^T
   if (active(nt - 1)) attn_mphase16<IS_F16, true, false>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c, hf);
