@@ -344,7 +344,7 @@ def main():
     ap.add_argument("--only", choices=["mlp", "int4", "block", "all"], default="all")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build has no multi-GPU "
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the library has no multi-GPU "
               f"path (sharding across GPUs is designed, not built)", file=sys.stderr)
         sys.exit(2)
 

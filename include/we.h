@@ -24,7 +24,7 @@ extern "C" {
 #define WE_EINVAL 1       /* bad shape / stride / alignment / argument; message = the reference's text */
 #define WE_ENOMEM 2       /* device or pinned-host allocation failed */
 #define WE_EHIP 3         /* a HIP runtime call failed; message carries hipGetErrorString */
-#define WE_EUNSUPPORTED 4 /* a dtype combination or mode this build does not implement */
+#define WE_EUNSUPPORTED 4 /* a dtype combination or mode the library does not implement */
 #define WE_EFORMAT 5      /* not a valid .safetensors file; message = the reference's SafetensorsError text */
 #define WE_EIO 6          /* a file could not be opened or read */
 #define WE_ENOTFOUND 7    /* no tensor of that name */

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the quantized-weight matmul path (fp8 / bf16 / f32 / int4 weights, RMSNorm, RoPE,
  * elementwise epilogues, split-K). TEST INFRASTRUCTURE ONLY: the tests, the smoke check and the
- * bench's cpu_baseline leg load it as the checker; the product library never links or calls it.
+ * bench's cpu_baseline leg load it to check results; the product library never links or calls it.
  *
  * Every function restates the reference's algorithm in plain C and cites the reference file:line it
  * follows (paths relative to the dotstories/web-engine tree). Accumulation that the reference's

@@ -1,4 +1,4 @@
-"""ctypes binding of the CPU oracle (oracle/liboracle.so). Test infrastructure: the checker only."""
+"""ctypes binding of the CPU oracle (oracle/liboracle.so). Test infrastructure only: results are checked against it."""
 import ctypes
 import pathlib
 import subprocess

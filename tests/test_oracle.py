@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker of the HIP path.
+"""Pins the CPU oracle before the GPU tests compare the HIP path against it.
 
 Sources of truth, none of them the oracle itself:
   * known-answer values from the reference's own tests (tests/fp8.test.ts, tests/noise.test.ts,

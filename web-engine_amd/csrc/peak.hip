@@ -3,7 +3,7 @@
 //
 // Math kinds follow the reference: every thread runs PEAK_CHAINS = 8 independent chains for `iters`
 // iterations, 64 operations per thread per iteration:
-//   F32: 8 chains x 4 fma (2 ops each) in f32 (scalar v_fma_f32: this build compiles without packed f32
+//   F32: 8 chains x 4 fma (2 ops each) in f32 (scalar v_fma_f32: the library compiles without packed f32
 //        math, so the probe reports the scalar-FMA ceiling, half the packed-FMA figure MI355X publishes);
 //   F16: 8 chains x 2 packed fma (v_pk_fma_f16, 4 ops each);
 //   I8:  8 chains x dot4 of int8 (v_dot4_i32_i8, 4 multiply-adds = 8 ops);
