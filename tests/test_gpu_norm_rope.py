@@ -107,7 +107,7 @@ def test_rope_half_pairs(graph):  # tests/gpu/rope.test.ts:24-42
 
 
 @pytest.mark.parametrize("half", [False, True])
-@pytest.mark.parametrize("dtype", [we.F32, we.BF16])
+@pytest.mark.parametrize("dtype", [we.F32, we.BF16, we.F16])
 def test_fused_qk_norm_rope(graph, half, dtype):
     """RMSNorm per head (offset 1, eps 1e-6) then 2D-axial RoPE (theta 10000) on the image tokens only,
     as the q/k path of attend() (src/model/block.ts:53-56) composes it."""
@@ -118,19 +118,29 @@ def test_fused_qk_norm_rope(graph, half, dtype):
     rng = np.random.default_rng(3)
     x32 = rng.standard_normal(tokens * heads * hd).astype(np.float32) * 2
     w = rng.uniform(-0.3, 0.3, hd).astype(np.float32)
-    x = x32 if dtype == we.F32 else O.bf16_rne(x32)
-    xs = x32 if dtype == we.F32 else O.bf16_to_f32(x)
+    if dtype == we.F32:
+        x, xs = x32, x32
+    elif dtype == we.BF16:
+        x = O.bf16_rne(x32)
+        xs = O.bf16_to_f32(x)
+    else:
+        x = x32.astype(np.float16).view(np.uint16)
+        xs = x32.astype(np.float16).astype(np.float32)
     out = graph.buffer(x.nbytes)
     graph.qk_norm_rope(tokens, heads, hd, 1e-6, 1.0, graph.buffer(w), text, half, graph.buffer(cos),
                        graph.buffer(sin), dtype, graph.buffer(x), out)
     raw = graph.read(out)
-    got = raw.view(np.float32).astype(np.float64) if dtype == we.F32 else O.bf16_to_f32(raw.view(np.uint16)).astype(
-        np.float64)
+    if dtype == we.F32:
+        got = raw.view(np.float32).astype(np.float64)
+    elif dtype == we.BF16:
+        got = O.bf16_to_f32(raw.view(np.uint16)).astype(np.float64)
+    else:
+        got = raw.view(np.float16).astype(np.float64)
     normed = O.rmsnorm(xs, w, 1e-6, 1.0).astype(np.float32)  # [tokens * heads, hd]
     img = normed.reshape(tokens, heads * hd)[text:].ravel()
     rot = O.rope_rotate(img, rows * cols, heads, pairs, cos, sin, half=half)
     want = np.concatenate([normed.reshape(tokens, heads * hd)[:text].ravel().astype(np.float64), rot])
-    tol = 2e-5 if dtype == we.F32 else 2 ** -8
+    tol = {we.F32: 2e-5, we.BF16: 2 ** -8, we.F16: 2 ** -10}[dtype]
     assert np.all(np.abs(got - want) <= tol * np.maximum(np.abs(want), 1.0))
 
 
