@@ -13,7 +13,8 @@
 //     reach a 4-stage LDS ring by direct-to-LDS loads; the two waves sharing a SIMD alternate MFMA and
 //     softmax phases between workgroup barriers (ping-pong).
 //   * attn_dma_kernel (WE_ATTN_PATH=ring): the same ring with a 3-stage depth and one phase per tile.
-// All three run the same per-tile arithmetic in the same order, so their outputs agree bit for bit.
+// For 16-bit operands at head dim 128 the three run the same per-tile arithmetic in the same order, so their
+// outputs agree bit for bit.
 //
 // 16-bit kernel (bf16 or f16 operands, fp32 accumulation, 32x32x16 MFMA):
 //   * S^T = K Q^T: the MFMA's A operand is a K tile row (a key), B is the wave's Q held in registers. In the
