@@ -99,6 +99,10 @@ int we_stream_join(we_ctx* ctx);
  * loadTransformer (src/model/weights.ts:124-129) and runAhead (src/gpu/run-ahead.ts:7-21) ---- */
 int we_host_alloc(we_ctx* ctx, size_t bytes, void** out); /* pinned (hipHostMalloc) */
 int we_host_free(we_ctx* ctx, void* ptr);
+/* WE_OK when [p, p + bytes) lies inside one live we_host_alloc block of this context, else WE_EINVAL. No
+ * counterpart in the reference (WebGPU owns its staging memory): bindings call it before they write into
+ * pinned memory on a script's behalf, so a wrong offset or length, or a write after we_host_free, is refused. */
+int we_host_span(we_ctx* ctx, const void* p, size_t bytes);
 /* enqueue dst <- pinned src on the copy stream after the compute work recorded by `after` (0 = none);
  * returns a ticket that compute can wait on */
 int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket);
@@ -115,7 +119,11 @@ int we_timer_stop(we_ctx* ctx, float* ms);
  * we_graph_begin starts capturing the kernels later calls queue on the compute stream; we_graph_end
  * instantiates them; we_graph_launch replays them in stream order. Between begin and end only kernel-
  * queuing calls and we_buf_copy are allowed: allocation, host transfers, syncs, tickets and timers fail.
- * A replay reads and writes the buffers the captured calls named, with their contents at replay time. */
+ * A replay reads and writes the buffers the captured calls named, with their contents at replay time.
+ * Kernels that need scratch (split-K partial sums, attention's V^T) replay into the scratch block of the stream
+ * they were captured on: a graph keeps that block alive until we_graph_destroy, also when a later eager call
+ * outgrows it, and we_graph_launch refuses to run a graph while the other compute stream is selected. Replays
+ * of graphs captured on one stream share that stream's scratch, so they run one after another in its order. */
 typedef struct we_graph we_graph;
 int we_graph_begin(we_ctx* ctx);
 int we_graph_end(we_ctx* ctx, we_graph** graph);
@@ -132,8 +140,8 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
 /* y = x . W^T * scale with W [N, K] as stored (fp8 / bf16 / f16 / f32 / int4). Replaces matmulWgsl
  * (src/kernels/matmul.ts:118-178) dispatched by linear() (src/model/ops.ts:61-73).
  * x: x_dtype in {F32, F16, BF16}; y: y_dtype in {F32, F16, BF16}; w_scales: int4 only, f16 [N, K/group];
- * bias: f32 [N] with WE_EPI_BIAS. Accumulation is fp32 on bf16/f16 MFMA (f32 inputs are split into
- * two bf16 terms, keeping ~16 mantissa bits). */
+ * bias: f32 [N] with WE_EPI_BIAS. Accumulation is fp32 on bf16/f16 MFMA (f32 operands are split into
+ * three bf16 planes whose sum is the f32 value exactly, so every product keeps all 24 mantissa bits). */
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
 /* we_matmul with the gated residual of the reference's gatedAdd (src/kernels/elementwise.ts:52-58, used after the

@@ -5,6 +5,8 @@ against an independent implementation:
   - e4m3fn.json : torch.float8_e4m3fn decode of all 256 bytes, and torch's float32 -> e4m3fn rounding
   - convert.json : torch's float32 -> bfloat16 / float16 rounding of edge values
   - gelu.json    : torch.nn.functional.gelu(approximate="tanh") in float64 on edge and random inputs
+  - rmsnorm.json : torch.nn.functional.rms_norm in float64 with weight (offset + w) * (1 + scale), plus shift:
+                   the RMSNorm of src/kernels/rmsnorm.ts:42-45, with and without the Krea modulation
 torch-randn.json is the reference's own fixture (tests/fixtures/torch-randn.json), copied as data.
 
 Run: python tests/golden/make_golden.py   (needs torch; the tests only read the JSON files)
@@ -48,6 +50,21 @@ def main():
     xs = [-60.0, 60.0, 0.0, -1e-3, 1e-3, -3.0, 3.0, -8.0, 8.0, 15.0, -15.0] + (rng.uniform(-8, 8, 100)).tolist()
     g = torch.nn.functional.gelu(torch.tensor(xs, dtype=torch.float64), approximate="tanh").tolist()
     (HERE / "gelu.json").write_text(json.dumps({"source": f"torch {torch.__version__}", "x": xs, "gelu": g}, indent=1))
+
+    cases = []
+    for rows, d, eps, offset, mod in ((3, 16, 1e-5, 1.0, False), (3, 16, 1e-5, 0.0, True), (2, 128, 1e-6, 1.0, True),
+                                      (1, 512, 1e-6, 1.0, True), (2, 7, 1e-5, 0.0, False)):
+        x = rng.uniform(-3, 3, rows * d).astype(np.float32)
+        w = rng.uniform(-0.5, 0.5, d).astype(np.float32)
+        sc = rng.uniform(-0.3, 0.3, d).astype(np.float32) if mod else np.zeros(d, np.float32)
+        sh = rng.uniform(-0.3, 0.3, d).astype(np.float32) if mod else np.zeros(d, np.float32)
+        t = torch.tensor(x.astype(np.float64)).reshape(rows, d)
+        weight = (offset + torch.tensor(w.astype(np.float64))) * (1 + torch.tensor(sc.astype(np.float64)))
+        out = torch.nn.functional.rms_norm(t, (d,), weight=weight, eps=eps) + torch.tensor(sh.astype(np.float64))
+        cases.append({"rows": rows, "d": d, "eps": eps, "offset": offset, "modulated": mod, "x": x.tolist(),
+                      "weight": w.tolist(), "scale": sc.tolist(), "shift": sh.tolist(),
+                      "out": out.reshape(-1).tolist()})
+    (HERE / "rmsnorm.json").write_text(json.dumps({"source": f"torch {torch.__version__}", "cases": cases}))
 
 
 if __name__ == "__main__":

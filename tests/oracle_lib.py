@@ -279,6 +279,71 @@ def double_block(cfg, txt_tokens, img_tokens, x_txt, x_img, w_txt, w_img, tvec, 
     return out_t, out_i
 
 
+def double_block_rows(cfg, txt_tokens, img_tokens, x_txt, x_img, w_txt, w_img, tvec, cos_img, sin_img, rows_txt,
+                      rows_img):
+    """Outputs of the double-stream block for selected rows only (text rows `rows_txt`, image rows `rows_img`),
+    composed in float64 numpy from the steps of or_double_block_f64: K and V of every token (attention needs all
+    of them), everything else only for the selected rows. It makes the full 512 + 4096-token shape checkable on
+    the CPU in seconds. Pinned to or_double_block_f64 row for row (test_oracle)."""
+    H, hd, heads, eps = cfg.hidden, cfg.head_dim, cfg.heads, cfg.eps
+    table = e4m3_table()
+    T = txt_tokens + img_tokens
+
+    def mm(x, lin, rows=None):
+        b, scale, n, k = lin
+        w = np.asarray(b, np.uint8).reshape(n, k)
+        if rows is not None:
+            w = w[rows]
+        return (x @ table[w].T) * float(scale)
+
+    def rms(x, w, scale=None, shift=None):
+        x = np.asarray(x, np.float64)
+        inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+        y = x * inv * (1.0 + np.asarray(w, np.float64))
+        if scale is not None:
+            y = y * (1.0 + scale) + shift
+        return y
+
+    def rope(x, c, s):  # x [rows, heads, hd], interleaved pairs; c, s [rows, hd / 2]
+        a, b = x[..., 0::2], x[..., 1::2]
+        c, s = c[:, None, :].astype(np.float64), s[:, None, :].astype(np.float64)
+        out = np.empty_like(x)
+        out[..., 0::2] = a * c - b * s
+        out[..., 1::2] = b * c + a * s
+        return out
+
+    ws, xs = (w_txt, w_img), (np.asarray(x_txt, np.float64).reshape(-1, H), np.asarray(x_img, np.float64).reshape(-1, H))
+    picks, row0 = (np.asarray(rows_txt, np.int64), np.asarray(rows_img, np.int64)), (0, txt_tokens)
+    k_all, v_all = np.empty((T, heads, hd)), np.empty((T, heads, hd))
+    q_sel, mods = [], []
+    cos_img = np.asarray(cos_img, np.float32).reshape(img_tokens, hd // 2)
+    sin_img = np.asarray(sin_img, np.float32).reshape(img_tokens, hd // 2)
+    for s in range(2):
+        w, x = ws[s], xs[s]
+        mod = (np.asarray(tvec, np.float64) + np.asarray(w["table"], np.float64)).reshape(6, H)
+        mods.append(mod)
+        h = rms(x, w["norm1"], mod[0], mod[1])
+        kv = mm(h, w["qkv"], np.arange(H, 3 * H))
+        k = rms(kv[:, :H].reshape(-1, heads, hd), w["norm_k"])
+        v = kv[:, H:].reshape(-1, heads, hd)
+        q = rms(mm(h[picks[s]], w["qkv"], np.arange(0, H)).reshape(-1, heads, hd), w["norm_q"])
+        if s == 1:
+            k = rope(k, cos_img, sin_img)
+            q = rope(q, cos_img[picks[s]], sin_img[picks[s]])
+        k_all[row0[s]:row0[s] + x.shape[0]], v_all[row0[s]:row0[s] + x.shape[0]] = k, v
+        q_sel.append(q)
+    outs = []
+    for s in range(2):
+        w, mod, q = ws[s], mods[s], q_sel[s]
+        sc = np.einsum("rhd,thd->rht", q, k_all) / np.sqrt(hd)
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        o = np.einsum("rht,thd->rhd", p / p.sum(-1, keepdims=True), v_all).reshape(-1, H)
+        x1 = xs[s][picks[s]] + mod[2] * mm(o, w["proj"])
+        u = gelu_tanh(mm(rms(x1, w["norm2"], mod[3], mod[4]), w["up"]))
+        outs.append(x1 + mod[5] * mm(u, w["down"]))
+    return outs[0], outs[1]
+
+
 def elementwise(op, a, b=None, c=None, d=1):
     a = c_contig(a, np.float32)
     bb = None if b is None else c_contig(b, np.float32)
@@ -294,6 +359,14 @@ def dequant_int4(words, scales, rows, k, group):
     out = np.empty(rows * k, np.float32)
     lib.or_dequant_int4(ptr(words), ptr(scales), rows, k, group, ptr(out))
     return out
+
+
+def gelu_tanh(v):
+    """Vectorized float64 tanh GELU, the formula of or_gelu_tanh (PyTorch gelu(approximate="tanh"),
+    src/kernels/elementwise.ts:25-29), for checks over millions of outputs; pinned to or_gelu_tanh and the torch
+    golden in test_oracle."""
+    v = np.asarray(v, np.float64)
+    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v * v * v)))
 
 
 def rel_error(got, ref):

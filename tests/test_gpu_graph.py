@@ -97,3 +97,55 @@ def test_capture_refuses_allocation_and_host_traffic(graph):
     graph.graph_destroy(g)
     assert np.allclose(got, 2.0)  # x / rms(x) * (1 + w) = 2
     graph.release(mark)
+
+
+def test_graph_keeps_its_scratch_when_an_eager_call_outgrows_it():
+    """A graph captured with a split-K GEMM (partial sums in the context scratch) still replays correctly after an
+    eager 4608-token attention grew the scratch past the 16 MiB first allocation: the graph holds its scratch
+    block until it is destroyed. A graph captured on compute stream 1 is refused on stream 0."""
+    g = we.Graph(0)  # a fresh context: its scratch starts at the minimum size
+    try:
+        rng = np.random.default_rng(3)
+        m, n, k = 64, 3072, 3072
+        x = g.buffer(rng.standard_normal(m * k).astype(np.float16))
+        w = rng.integers(0, 254, n * k).astype(np.uint8)
+        w = g.buffer((w + (w >= 0x7F)).astype(np.uint8))
+        y_eager, y_graph = g.buffer(m * n * 2), g.buffer(m * n * 2)
+        p = we.matmul_params(m, n, k, 0.02, graph=g)
+        g.matmul(p, we.F16, x, we.FP8, w, we.F16, y_eager)  # eager first: the scratch exists before capture
+        g.sync()
+        g.graph_begin()
+        g.matmul(p, we.F16, x, we.FP8, w, we.F16, y_graph)
+        gr = g.graph_end()
+        t, heads, hd = 4608, 24, 128  # V^T of 4608 x 24 x 128 bf16 is 28 MB of scratch
+        qkv = g.buffer(O.bf16_rne(rng.standard_normal(t * 3 * heads * hd).astype(np.float32)))
+        o = g.buffer(t * heads * hd * 2)
+        H = heads * hd
+        g.attention(t, heads, heads, hd, False, we.BF16, qkv, we.Graph.slice(qkv, H * 2, 0),
+                    we.Graph.slice(qkv, 2 * H * 2, 0), o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
+        g.sync()
+        want = g.read(y_eager).copy()
+        for _ in range(2):
+            g.write(y_graph, np.zeros(m * n * 2, np.uint8))
+            g.sync()
+            g.graph_launch(gr)
+            assert np.array_equal(g.read(y_graph), want)
+        g.graph_destroy(gr)
+        # captured on stream 1: refused on stream 0, runs on stream 1
+        g.stream(1)
+        g.matmul(p, we.F16, x, we.FP8, w, we.F16, y_graph)
+        g.graph_begin()
+        g.matmul(p, we.F16, x, we.FP8, w, we.F16, y_graph)
+        gr1 = g.graph_end()
+        g.stream(0)
+        with pytest.raises(we.WeError, match="captured on compute stream 1"):
+            g.graph_launch(gr1)
+        g.stream(1)
+        g.write(y_graph, np.zeros(m * n * 2, np.uint8))
+        g.graph_launch(gr1)
+        g.sync()
+        assert np.array_equal(g.read(y_graph), want)
+        g.graph_destroy(gr1)
+        g.stream(0)
+    finally:
+        g.destroy()

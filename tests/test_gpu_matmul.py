@@ -241,11 +241,46 @@ def test_nan_codes_decode_like_the_shader(graph):
     assert got[0, 0] == 63 + 480 and got[0, 1] == 63 - 480 and got[0, 2] == 64
 
 
-@pytest.mark.parametrize("name,m,n,k,w_dt", [("C3 up", 4096, 12288, 3072, we.FP8), ("C3 down", 4096, 3072, 12288, we.FP8),
-                                             ("C2 qkv", 4096, 9216, 3072, we.BF16)])
-def test_full_size_sampled_rows(graph, name, m, n, k, w_dt):
+@pytest.mark.parametrize("y_dt", [we.BF16, we.F32, we.F16])
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("cfg", [None, 0])
+def test_fast_epilogue_gelu_without_bias(graph, monkeypatch, y_dt, gated, cfg):
+    """The fast kernel's whole-sub-tile epilogue with GELU and no bias: the up-projection as benchmarked (256 x 256
+    ping-pong tiles, bf16 out) and the gated form, against the oracle product followed by or_gelu_tanh (and the
+    reference's gatedAdd). 512 x 768 outputs are 2 x 3 whole 256 x 256 tiles; cfg None takes the default pick."""
+    m, n, k = 512, 768, 512
+    rng = np.random.default_rng(31 + y_dt + 3 * gated)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), we.BF16)
+    w = rng.integers(0, 254, n * k).astype(np.uint8)
+    w = (w + (w >= 0x7F)).astype(np.uint8)
+    gate = rng.uniform(-1.5, 1.5, n).astype(np.float32) if gated else None
+    res_store, res_vals = _store(rng.standard_normal(m * n), y_dt) if gated else (None, None)
+    if cfg is not None:
+        monkeypatch.setenv("WE_GEMM_CFG", str(cfg))
+    p = we.matmul_params(m, n, k, 0.02, graph=graph)
+    mark = graph.mark()
+    yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
+    graph.matmul(p, we.BF16, graph.buffer(x_store), we.FP8, graph.buffer(w), y_dt, yb, flags=we.EPI_GELU,
+                 gate=graph.buffer(gate) if gated else None, residual=graph.buffer(res_store) if gated else None)
+    got = decode(graph.read(yb), y_dt)
+    graph.release(mark)
+    v = O.gelu_tanh(O.matmul(O.matmul_params(m, n, k, 0.02), ox, x_oracle, O.FP8, w))
+    want = (res_vals + np.tile(gate.astype(np.float64), m) * v) if gated else v
+    tol = 1e-4 if y_dt == we.F32 else TOL[y_dt]
+    assert O.rel_error(got, want) < tol
+
+
+@pytest.mark.parametrize("name,m,n,k,w_dt,flags", [("C3 up", 4096, 12288, 3072, we.FP8, we.EPI_GELU),
+                                                   ("C3 down", 4096, 3072, 12288, we.FP8, 0),
+                                                   ("C2 qkv", 4096, 9216, 3072, we.BF16, 0)])
+def test_full_size_sampled_rows(graph, name, m, n, k, w_dt, flags):
     """Full-size GEMMs: every output is computed, 6 whole rows (incl. the first and last) are checked
-    against the f64 oracle, and the row sums of y equal x @ rowsum(W) (a checksum over all outputs)."""
+    against the f64 oracle, and the row sums of y equal x @ rowsum(W) (a checksum over all outputs).
+    Then the GEMM exactly as bench.py runs it (bf16 output, default tile pick; the up-projection with GELU
+    fused and no bias): its sampled rows against the oracle (+ GELU) at the bf16 bar, and every one of its
+    outputs against the f32-output run above passed through GELU in float64 and rounded to bf16. Both runs take
+    the same tile pick and the same accumulation order, so they agree to the rounding of the output: exactly
+    without GELU, within one bf16 step with it."""
     rng = np.random.default_rng(m + n + k)
     x = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
     if w_dt == we.FP8:
@@ -268,6 +303,21 @@ def test_full_size_sampled_rows(graph, name, m, n, k, w_dt):
     xs = O.bf16_to_f32(x).astype(np.float64).reshape(m, k)
     want_sum = xs @ wdec.sum(0) * scale
     assert np.abs(got.sum(1) - want_sum).max() < 1e-4 * np.abs(want_sum).max() + 1e-3
+    # ---- the benchmarked variant: bf16 out (+ fused GELU for the up-projection)
+    bench = run(graph, p, x, we.BF16, w, w_dt, we.BF16, flags=flags).reshape(m, n)
+    gelu = (lambda v: O.gelu_tanh(v)) if flags & we.EPI_GELU else (lambda v: v)  # noqa: E731
+    for r in rows:
+        want = gelu(O.matmul_rows(op, O.BF16, x, ow, w, r, r + 1).reshape(m, n)[r])
+        assert O.rel_error(bench[r], want) < TOL[we.BF16], (name, r)
+    expect = O.bf16_to_f32(O.bf16_rne(gelu(got).astype(np.float32))).astype(np.float64)
+    if flags & we.EPI_GELU:
+        diff = np.abs(bench - expect)
+        assert (diff <= 2.0 ** -7 * np.abs(expect) + 1e-30).all(), (name, float(diff.max()))
+        # a one-step difference only where GELU's last f32 bits meet a rounding tie (outputs that underflow
+        # f32 aside)
+        assert ((diff == 0) | (np.abs(expect) < 1e-30)).mean() > 0.99, name
+    else:
+        assert np.array_equal(bench, expect), name
 
 
 # ------------------------------------------------------------------ LoRA through linear() (tests/gpu/lora.test.ts)
@@ -327,6 +377,28 @@ def test_lora_on_fp8_linear_bf16_and_f32_weights(graph):  # tests/gpu/lora.test.
     plain = graph.read(we.linear(graph, graph.buffer(x), base, m), dtype=np.float32, count=m * n)
     assert rms_rel(plain, want) > 1e-3  # the update is really there
     graph.release(mark)
+
+
+@pytest.mark.parametrize("y_dt", [we.F32, we.BF16])
+def test_lora_with_gelu_applies_gelu_to_the_sum(graph, y_dt):
+    """linear(..., gelu_tanh=True) with LoRA returns gelu(x W^T s + bias + lora), as a caller of the reference
+    applies GELU to what linear returns (src/model/ops.ts:61-73); the fused GELU stays off the base GEMM."""
+    m, n, k, r, s = 6, 40, 64, 4, 0.6
+    d = LcgDraws(13, m * k + n * k + r * k + n * r + n)
+    x, w = d.floats(m * k), d.fp8(n * k)
+    (down_b, down_v), (up_b, up_v) = d.bf16(r * k), d.bf16(n * r)
+    bias = d.floats(n)
+    mark = graph.mark()
+    lora = (we.Linear(graph.buffer(down_b), "bf16", 1.0, r, k), we.Linear(graph.buffer(up_b), "bf16", s, n, r))
+    lin = we.Linear(graph.buffer(w), "fp8", 0.25, n, k, bias=graph.buffer(bias), lora=lora)
+    got = decode(graph.read(we.linear(graph, graph.buffer(x), lin, m, y_dtype=y_dt, gelu_tanh=True)), y_dt)
+    graph.release(mark)
+    lin_sum = lora_reference(x, O.e4m3_table()[w], 0.25, down_v, up_v, s, m, n, k, r) + np.tile(bias, m)
+    want = O.gelu_tanh(lin_sum)
+    assert rms_rel(got, want) < (1e-6 if y_dt == we.F32 else 1e-2)
+    wrong = O.gelu_tanh(lin_sum - lora_reference(x, O.e4m3_table()[w] * 0, 0.0, down_v, up_v, s, m, n, k, r)) + \
+        lora_reference(x, O.e4m3_table()[w] * 0, 0.0, down_v, up_v, s, m, n, k, r)
+    assert rms_rel(wrong, want) > 1e-3  # the order matters for these inputs
 
 
 def test_lora_rank_not_multiple_of_4_is_rejected(graph):  # tests/gpu/lora.test.ts:80-89

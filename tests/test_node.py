@@ -32,7 +32,7 @@ EXPORTS = {
     "we_ctx_create": "create", "we_ctx_destroy": "destroy", "we_device_info": "deviceInfo", "we_sync": "sync",
     "we_buf_alloc": "bufAlloc", "we_buf_free": "bufFree", "we_buf_upload": "upload", "we_buf_download": "download",
     "we_buf_copy": "copy", "we_mark": "mark", "we_release": "release", "we_stats": "stats",
-    "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_stream_copy": "streamCopy",
+    "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_host_span": "hostSpan", "we_stream_copy": "streamCopy",
     "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
     "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
     "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_matmul_gated": "matmulGated", "we_rmsnorm": "rmsnorm",

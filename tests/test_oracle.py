@@ -349,6 +349,11 @@ def test_gelu_matches_torch_and_shader_form():  # tests/gpu/text.test.ts:56-60, 
     assert np.abs(ours - np.array(g["gelu"])).max() < 1e-12
     shader = np.array([O.lib.or_gelu_tanh_shader(v) for v in g["x"]], np.float64)
     assert np.abs(shader - np.array(g["gelu"])).max() < 1e-5
+    # the vectorized form used over whole GEMM outputs equals the C oracle, and the torch golden
+    v = np.concatenate([np.array(g["x"]), np.random.default_rng(3).normal(0, 4, 5000)])
+    assert np.abs(O.gelu_tanh(v) - np.array([O.lib.or_gelu_tanh(t) for t in v])).max() < 1e-12
+    assert np.abs(O.gelu_tanh(g["x"]) - np.array(g["gelu"])).max() < 1e-12
+    assert np.abs(O.gelu_tanh(v) - v).max() > 0.1  # not the identity
 
 
 def test_elementwise_ops_match_scipy():  # src/kernels/elementwise.ts:38-84, tests/gpu/elementwise.test.ts:15-40
@@ -547,3 +552,39 @@ def test_double_block_oracle_matches_numpy_composition():
     wi2 = dict(wi, up=_draw_linear(rng, cfg.mlp, H))
     got_t2, got_i2 = O.double_block(cfg, tt, ti, xt, xi, wt, wi2, tvec, cos, sin)
     assert np.array_equal(got_t2, got_t) and not np.array_equal(got_i2, got_i)
+
+
+def test_double_block_rows_equal_the_oracle_rows():
+    """The sampled-row composition (used to check the full 512 + 4096-token block on the GPU) equals
+    or_double_block_f64 on every row it is asked for, text and image, including first and last rows."""
+    cfg = _Cfg(hidden=64, mlp=128, heads=2, kv_heads=2, head_dim=32, eps=1e-6)
+    H, tt, rows, cols = 64, 5, 3, 4
+    ti = rows * cols
+    rng = np.random.default_rng(4)
+    wt, wi = _double_inputs(rng, cfg)
+    tvec = rng.uniform(-.3, .3, 6 * H).astype(np.float32)
+    cos, sin, _ = O.rope_tables(O.rope_positions(0, rows, cols, 2), [16, 16], 10000.0)
+    xt, xi = rng.uniform(-2, 2, tt * H), rng.uniform(-2, 2, ti * H)
+    full_t, full_i = O.double_block(cfg, tt, ti, xt, xi, wt, wi, tvec, cos, sin)
+    rt, ri = [0, 3, 4], [0, 5, 7, 11]
+    got_t, got_i = O.double_block_rows(cfg, tt, ti, xt, xi, wt, wi, tvec, cos, sin, rt, ri)
+    want_t, want_i = full_t.reshape(tt, H)[rt], full_i.reshape(ti, H)[ri]
+    assert np.abs(got_t - want_t).max() < 1e-10 * np.abs(want_t).max()
+    assert np.abs(got_i - want_i).max() < 1e-10 * np.abs(want_i).max()
+    # a rotation left out of the image keys cannot pass
+    no_rope = O.double_block_rows(cfg, tt, ti, xt, xi, wt, wi, tvec, np.ones_like(cos), np.zeros_like(sin), rt, ri)
+    assert np.abs(no_rope[1] - want_i).max() > 1e-3 * np.abs(want_i).max()
+
+
+def test_rmsnorm_oracle_matches_torch_golden():
+    """or_rmsnorm_f64 against torch.nn.functional.rms_norm (tests/golden/rmsnorm.json, written by make_golden.py
+    without the oracle): plain (offset 0 and 1) and Krea-modulated rows, d from 7 to 512, eps 1e-5 and 1e-6."""
+    for c in load("rmsnorm.json")["cases"]:
+        x, w = np.array(c["x"], np.float32), np.array(c["weight"], np.float32)
+        sc, sh = np.array(c["scale"], np.float32), np.array(c["shift"], np.float32)
+        got = O.rmsnorm(x, w, c["eps"], c["offset"], sc if c["modulated"] else None, sh if c["modulated"] else None)
+        want = np.array(c["out"])
+        assert np.abs(got - want).max() < 1e-12 * np.abs(want).max(), (c["rows"], c["d"])
+        # a dropped offset or eps cannot pass
+        assert np.abs(O.rmsnorm(x, w, c["eps"], 1.0 - c["offset"], sc if c["modulated"] else None,
+                                sh if c["modulated"] else None) - want).max() > 1e-3

@@ -208,6 +208,21 @@ def test_parallel_read_of_a_large_tensor(path):
     assert np.array_equal(part, big[-1000:])
 
 
+def test_parallel_read_covers_every_byte_when_pieces_round_down(path):
+    """64 MiB + 3 bytes over 8 threads: floor(bytes / 8) is already page-aligned, so pieces of that size would
+    leave the last 3 bytes unread. Every byte arrives, for the whole tensor and for a sub-range with the same
+    property."""
+    rng = np.random.default_rng(1)
+    big = rng.integers(1, 256, 64 * 1024 * 1024 + 3, dtype=np.uint8)  # no zero bytes: a skipped byte shows
+    W.save(path, {"big": ("U8", [big.size], big)})
+    st = W.read_header(path)
+    for threads in (8, 7, 16):
+        assert np.array_equal(st.read("big", threads=threads), big), threads
+    sub = np.zeros(32 * 1024 * 1024 + 5, np.uint8)
+    st.read_into("big", sub.ctypes.data, begin=17, nbytes=sub.size, threads=4)
+    assert np.array_equal(sub, big[17:17 + sub.size])
+
+
 # ---- tests/inspect.test.ts ----------------------------------------------------------------------------------
 
 def _t(dtype, shape):

@@ -50,6 +50,11 @@ struct we_ctx {
   size_t lane_scratch_bytes[2] = {0, 0};
   hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   hipDeviceProp_t prop{};
+  // scratch blocks that captured graphs hold (graph count per block): a replay writes the scratch its capture
+  // named, so a block outgrown while a graph holds it is retired instead of freed, and freed when its last
+  // graph is destroyed
+  std::map<void*, int> scratch_refs;
+  std::vector<void*> retired;
 };
 
 namespace {
@@ -94,8 +99,13 @@ int ensure_scratch(we_ctx* ctx, size_t bytes) {
     return fail(ctx, WE_EINVAL, "scratch must grow to %zu bytes: run the call once before capturing it", bytes);
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   if (ctx->scratch) {
-    HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
-    HIP_OK(ctx, hipFree(ctx->scratch), "hipFree scratch");
+    auto held = ctx->scratch_refs.find(ctx->scratch);
+    if (held != ctx->scratch_refs.end() && held->second > 0) {
+      ctx->retired.push_back(ctx->scratch);  // a live graph replays into it: keep it until that graph goes
+    } else {
+      HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+      HIP_OK(ctx, hipFree(ctx->scratch), "hipFree scratch");
+    }
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;
   }
@@ -202,6 +212,7 @@ int we_ctx_destroy(we_ctx* ctx) {
   for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->lane_scratch[1 - ctx->lane]) (void)hipFree(ctx->lane_scratch[1 - ctx->lane]);
+  for (void* p : ctx->retired) (void)hipFree(p);
   for (auto& kv : ctx->pinned) (void)hipHostFree((void*)kv.first);
   for (auto& e : ctx->tickets)
     if (e) (void)hipEventDestroy(e);
@@ -411,6 +422,21 @@ int we_host_free(we_ctx* ctx, void* ptr) {
   return WE_OK;
 }
 
+int we_host_span(we_ctx* ctx, const void* p, size_t bytes) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!p) return fail(ctx, WE_EINVAL, "pinned address is null");
+  auto it = ctx->pinned.upper_bound((uintptr_t)p);
+  if (it == ctx->pinned.begin()) return fail(ctx, WE_EINVAL, "address is not pinned memory of this context");
+  --it;
+  const uintptr_t a = (uintptr_t)p, end = it->first + it->second;
+  if (a >= end && !(a == it->first && bytes == 0))
+    return fail(ctx, WE_EINVAL, "address is not pinned memory of this context");
+  if (bytes > end - a)
+    return fail(ctx, WE_EINVAL, "%zu bytes at offset %zu run past the %zu-byte pinned buffer", bytes,
+                (size_t)(a - it->first), it->second);
+  return WE_OK;
+}
+
 int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes, uint64_t after, uint64_t* ticket) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
@@ -464,6 +490,8 @@ int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done) {
 struct we_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  void* scratch = nullptr;  // the scratch block the captured kernels name (held until destroy)
+  int lane = 0;             // the compute stream it was captured on, and the only one it replays on
 };
 
 int we_graph_begin(we_ctx* ctx) {
@@ -488,7 +516,8 @@ int we_graph_end(we_ctx* ctx, we_graph** graph) {
     (void)hipGraphDestroy(g);
     return hip_fail(ctx, e, "hipGraphInstantiate");
   }
-  *graph = new we_graph{g, exec};
+  *graph = new we_graph{g, exec, ctx->scratch, ctx->lane};
+  if (ctx->scratch) ctx->scratch_refs[ctx->scratch]++;
   return WE_OK;
 }
 
@@ -496,6 +525,9 @@ int we_graph_launch(we_ctx* ctx, we_graph* graph) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!graph) return fail(ctx, WE_EINVAL, "graph is null");
   if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  // its kernels use the scratch of the stream it was captured on, ordered only against that stream's work
+  if (graph->lane != ctx->lane)
+    return fail(ctx, WE_EINVAL, "graph was captured on compute stream %d; select that stream to launch it", graph->lane);
   HIP_OK(ctx, hipGraphLaunch(graph->exec, ctx->compute), "hipGraphLaunch");
   return WE_OK;
 }
@@ -504,9 +536,21 @@ int we_graph_destroy(we_ctx* ctx, we_graph* graph) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!graph) return WE_OK;
   if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
-  HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  HIP_OK(ctx, hipStreamSynchronize(ctx->lanes[graph->lane]), "hipStreamSynchronize");
   (void)hipGraphExecDestroy(graph->exec);
   (void)hipGraphDestroy(graph->graph);
+  if (graph->scratch) {
+    auto held = ctx->scratch_refs.find(graph->scratch);
+    if (held != ctx->scratch_refs.end() && --held->second <= 0) {
+      ctx->scratch_refs.erase(held);
+      for (size_t i = 0; i < ctx->retired.size(); i++)
+        if (ctx->retired[i] == graph->scratch) {  // outgrown meanwhile and no graph left on it
+          (void)hipFree(graph->scratch);
+          ctx->retired.erase(ctx->retired.begin() + (long)i);
+          break;
+        }
+    }
+  }
   delete graph;
   return WE_OK;
 }

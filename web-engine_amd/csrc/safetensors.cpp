@@ -547,11 +547,13 @@ int we_st_read(const we_safetensors* st, uint32_t index, uint64_t begin, uint64_
     if (int e = read_all(st->fd, off0, bytes, d)) return st_fail(WE_EIO, "%s: read failed: %s", t.name.c_str(), strerror(e));
     return WE_OK;
   }
-  const uint64_t per = (bytes / n + 4095) & ~4095ull;  // page-aligned pieces
+  // page-aligned pieces of ceil(bytes / n), so n pieces always cover the range; the last piece also runs to the
+  // end of the range, whatever the rounding
+  const uint64_t per = ((bytes + n - 1) / n + 4095) & ~4095ull;
   std::vector<int> errs(n, 0);
   std::vector<std::thread> pool;
   for (uint64_t i = 0; i < n; i++) {
-    const uint64_t b = std::min(bytes, i * per), e = std::min(bytes, b + per);
+    const uint64_t b = std::min(bytes, i * per), e = i + 1 == n ? bytes : std::min(bytes, b + per);
     if (b >= e) break;
     pool.emplace_back([&, i, b, e] { errs[i] = read_all(st->fd, off0 + b, e - b, d + b); });
   }

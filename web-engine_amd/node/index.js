@@ -134,16 +134,21 @@ class Graph {
   }
 
   // ---- pinned host memory and the copy stream (src/model/weights.ts:124-129, src/gpu/run-ahead.ts:7-21) ----
+  /** Pinned host memory: { ptr, size, ctx }; hostWrite and readTensor check every write against it. */
   hostAlloc(bytes) {
-    return { ptr: addon.hostAlloc(this.ctx, bytes), size: bytes };
+    return { ptr: addon.hostAlloc(this.ctx, bytes), size: bytes, ctx: this.ctx };
   }
 
   hostWrite(pinned, offset, data) {
-    addon.hostWrite(this.ctx, pinned.ptr, offset, data);
+    if (pinned.freed) throw new Error("pinned buffer was freed");
+    if (!(Number.isInteger(offset) && offset >= 0 && offset + data.byteLength <= pinned.size))
+      throw new RangeError(`write of ${data.byteLength} bytes at ${offset} runs past the ${pinned.size}-byte pinned buffer`);
+    addon.hostWrite(this.ctx, pinned.ptr, offset, data);  // checked again natively against the live block
   }
 
   hostFree(pinned) {
     addon.hostFree(this.ctx, pinned.ptr);
+    pinned.freed = true;
   }
 
   streamCopy(dst, pinnedSrc, bytes, after = 0) {
@@ -213,7 +218,9 @@ function narrowLinear(graph, x, w, m, xDtype = F32) {
 function linear(graph, x, w, m, { xDtype = F32, yDtype = F32, geluTanh = false } = {}) {
   const shape = { m, n: w.n, k: w.k };
   const y = graph.buffer(m * w.n * ELEM_BYTES[yDtype]);
-  const flags = (w.bias ? EPI.BIAS : 0) | (geluTanh ? EPI.GELU_TANH : 0);
+  // GELU applies to the whole sum (a caller of the reference applies it to what linear returns): with LoRA it
+  // runs in place after the update is added, not in the base GEMM's epilogue
+  const flags = (w.bias ? EPI.BIAS : 0) | (geluTanh && !w.lora ? EPI.GELU_TANH : 0);
   const int4 = wdt(w.dtype) === INT4;
   graph.matmul(matmulParams(shape, w.scale, {}, graph), xDtype, x, wdt(w.dtype), w.buffer, yDtype, y,
                { scales: w.scales, group: int4 ? (w.group == null ? 64 : w.group) : 0, bias: w.bias, flags });
@@ -223,6 +230,7 @@ function linear(graph, x, w, m, { xDtype = F32, yDtype = F32, geluTanh = false }
   const t = narrowLinear(graph, x, down, m, xDtype);
   graph.matmul(matmulParams({ m, n: up.n, k: up.k }, up.scale, {}, graph), F32, t, wdt(up.dtype), up.buffer, yDtype, y,
                { flags: EPI.ACCUMULATE });
+  if (geluTanh) graph.elementwise(OP.GELU_TANH, m * w.n, 1, yDtype, y, null, null, y);
   return y;
 }
 
@@ -301,13 +309,20 @@ function readHeader(path) {
   return { tensors, metadata, handle, close: () => addon.stClose(handle) };
 }
 
-/** The raw bytes of one tensor, or only its first `limit` bytes; `dst` (a Uint8Array, or a BigInt pinned host
- * address) receives them when given. */
-function readTensor(st, tensor, limit, dst, threads) {
+/** The raw bytes of one tensor, or only its first `limit` bytes; `dst` (a Uint8Array, or pinned memory from
+ * Graph.hostAlloc, optionally with a byte `offset` into it) receives them when given. */
+function readTensor(st, tensor, limit, dst, threads, offset = 0) {
   const n = Math.min(limit === undefined ? tensor.size : limit, tensor.size);
-  const out = dst === undefined ? new Uint8Array(n) : dst;
-  addon.stRead(st.handle, tensor.index, 0, n, out, threads || 0);
-  return out;
+  if (dst === undefined) dst = new Uint8Array(n);
+  if (ArrayBuffer.isView(dst)) {
+    addon.stRead(st.handle, tensor.index, 0, n, dst, threads || 0);
+    return dst;
+  }
+  if (typeof dst !== "object" || dst.ctx == null) throw new TypeError("readTensor: dst must be a TypedArray or pinned memory from Graph.hostAlloc");
+  if (dst.freed) throw new Error("pinned buffer was freed");
+  if (offset + n > dst.size) throw new RangeError(`${n} bytes at ${offset} run past the ${dst.size}-byte pinned buffer`);
+  addon.stRead(st.handle, tensor.index, 0, n, dst.ptr + BigInt(offset), threads || 0, dst.ctx);
+  return dst;
 }
 
 module.exports = {

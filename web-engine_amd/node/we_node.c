@@ -361,6 +361,7 @@ static napi_value HostFree(napi_env env, napi_callback_info info) {
 static napi_value HostWrite(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 4)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
   void* p = ptr_arg(&a, 1);
   double off = f64_arg(&a, 2);
   void* data = NULL;
@@ -371,8 +372,26 @@ static napi_value HostWrite(napi_env env, napi_callback_info info) {
     napi_throw_error(env, NULL, "pinned buffer is null");
     return NULL;
   }
+  if (!(off >= 0 && off <= 9007199254740991.0 && off == (double)(uint64_t)off)) {
+    napi_throw_range_error(env, NULL, "offset must be a non-negative integer");
+    return NULL;
+  }
+  /* the whole destination must lie in one live pinned block of this context */
+  int rc = we_host_span(ctx, (char*)p + (size_t)off, len);
+  if (rc != WE_OK) return status(env, ctx, rc);
   memcpy((char*)p + (size_t)off, data, len);
   return undefined(env);
+}
+
+/* hostSpan(ctx, ptr, bytes): throws unless [ptr, ptr + bytes) is inside live pinned memory of ctx */
+static napi_value HostSpan(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 3)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* p = ptr_arg(&a, 1);
+  double bytes = f64_arg(&a, 2);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_host_span(ctx, p, (size_t)bytes));
 }
 
 static napi_value StreamCopy(napi_env env, napi_callback_info info) {
@@ -830,8 +849,8 @@ static napi_value StMetadataAt(napi_env env, napi_callback_info info) { /* [key,
   return pair;
 }
 
-/* stRead(handle, index, begin, bytes, dst, threads): dst = a BigInt host address (e.g. pinned memory from
- * hostAlloc) or a TypedArray / Buffer of at least `bytes` bytes */
+/* stRead(handle, index, begin, bytes, dst, threads, ctx): dst = a TypedArray / Buffer of at least `bytes` bytes,
+ * or a BigInt address of pinned memory from hostAlloc of the context ctx, which must then hold all `bytes` */
 static napi_value StRead(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 5)) return NULL;
@@ -867,7 +886,14 @@ static napi_value StRead(napi_env env, napi_callback_info info) {
     dst = data;
   } else {
     dst = ptr_arg(&a, 4);
+    we_ctx* ctx = a.argc > 6 && !is_nullish(env, a.argv[6]) ? ptr_arg(&a, 6) : NULL;
     if (a.bad) return NULL;
+    if (!ctx) {
+      napi_throw_type_error(env, NULL, "a raw destination address needs the context that owns its pinned memory");
+      return NULL;
+    }
+    int rc = we_host_span(ctx, dst, (size_t)bytes);
+    if (rc != WE_OK) return status(env, ctx, rc);
   }
   return st_status(env, we_st_read(st, idx, (uint64_t)begin, (uint64_t)bytes, dst, threads));
 }
@@ -891,7 +917,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
-      {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite},
+      {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulGated", MatmulGated},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},

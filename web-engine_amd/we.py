@@ -79,6 +79,7 @@ SIGNATURES = {
     "we_stream_join": (_I, [_P]),
     "we_host_alloc": (_I, [_P, _SZ, _P]),
     "we_host_free": (_I, [_P, _P]),
+    "we_host_span": (_I, [_P, _P, ctypes.c_size_t]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
     "we_wait_ticket": (_I, [_P, _U64]),
     "we_record_compute": (_I, [_P, _P]),
@@ -414,9 +415,12 @@ def _wdt(dtype):
 
 def linear(graph, x, w, m, x_dtype=F32, y_dtype=F32, gelu_tanh=False):
     """y[m, n] = x[m, k] . W^T (+ bias) (+ lora up.scale * (x . down^T) . up^T, added in place): src/model/ops.ts:61-73.
-    The bias (and optional tanh GELU) run in the GEMM epilogue instead of separate passes."""
+    The bias (and optional tanh GELU) run in the GEMM epilogue instead of separate passes. GELU applies to the whole
+    sum, as a caller of the reference applies it to what linear returns: with LoRA it runs after the update is added
+    (one in-place pass), not in the base GEMM's epilogue."""
     y = graph.buffer(m * w.n * ELEM_BYTES[y_dtype])
-    flags = (EPI_BIAS if w.bias is not None else 0) | (EPI_GELU if gelu_tanh else 0)
+    fuse_gelu = gelu_tanh and w.lora is None
+    flags = (EPI_BIAS if w.bias is not None else 0) | (EPI_GELU if fuse_gelu else 0)
     graph.matmul(matmul_params(m, w.n, w.k, w.scale, graph=graph), x_dtype, x, _wdt(w.dtype), w.buffer, y_dtype, y,
                  scales=w.scales, group=w.group if _wdt(w.dtype) == INT4 else 0, bias=w.bias, flags=flags)
     if w.lora is None:
@@ -427,6 +431,8 @@ def linear(graph, x, w, m, x_dtype=F32, y_dtype=F32, gelu_tanh=False):
     t = _narrow_linear(graph, x, down, m, x_dtype)
     graph.matmul(matmul_params(m, up.n, up.k, up.scale, graph=graph), F32, t, _wdt(up.dtype), up.buffer, y_dtype, y,
                  flags=EPI_ACCUMULATE)
+    if gelu_tanh:
+        graph.elementwise(OP_GELU_TANH, m * w.n, 1, y_dtype, y, None, None, y)
     return y
 
 
