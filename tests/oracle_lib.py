@@ -362,11 +362,14 @@ def dequant_int4(words, scales, rows, k, group):
 
 
 def gelu_tanh(v):
-    """Vectorized float64 tanh GELU, the formula of or_gelu_tanh (PyTorch gelu(approximate="tanh"),
-    src/kernels/elementwise.ts:25-29), for checks over millions of outputs; pinned to or_gelu_tanh and the torch
-    golden in test_oracle."""
+    """Vectorized float64 tanh GELU (PyTorch gelu(approximate="tanh"), src/kernels/elementwise.ts:25-29), for checks
+    over millions of outputs: 0.5 v (1 + tanh u) written as v / (1 + e^(-2u)), the same function without the
+    cancellation of 1 + tanh u for negative v (below v = -5 the tanh form rounds to 0 where the value is ~1e-10
+    and smaller). Pinned to or_gelu_tanh (to 1e-12) and the torch golden in test_oracle."""
     v = np.asarray(v, np.float64)
-    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v * v * v)))
+    u = np.sqrt(2.0 / np.pi) * (v + 0.044715 * v * v * v)
+    with np.errstate(over="ignore"):
+        return v / (1.0 + np.exp(-2.0 * u))
 
 
 def rel_error(got, ref):
