@@ -144,6 +144,15 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
  * three bf16 planes whose sum is the f32 value exactly, so every product keeps all 24 mantissa bits). */
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
+/* we_matmul that allocates nothing. No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving or decode loops, harnesses that forbid hipMalloc). Same arguments,
+ * kernels and results as we_matmul; the split-K partial sums that small-M GEMMs (M <= 64, and larger M with few
+ * output tiles) keep in scratch go to a fixed per-GPU device array of 16 MiB instead of the context's scratch,
+ * which holds every M <= 64 shape. A GEMM whose split plan needs more fails with WE_EINVAL, "... needs <n> bytes of
+ * split-K scratch; the allocation-free entry point has 16777216 (use we_matmul)". Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (the two compute streams, or two contexts) race. */
+int we_matmul_noalloc(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                      const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
 /* we_matmul with the gated residual of the reference's gatedAdd (src/kernels/elementwise.ts:52-58, used after the
  * attention output and MLP down projections, src/model/block.ts:60-64 and :80) fused into the epilogue:
  *   y = residual + gate[col] * v,  v = the value we_matmul would store (scale, bias, GELU)

@@ -94,6 +94,14 @@ struct AttnLaunch {
 size_t attention_scratch_bytes(const AttnLaunch& L);
 hipError_t attention_launch(const AttnLaunch& L, hipStream_t stream);
 
+// Scratch of the allocation-free entry point (noalloc.hip): a file-scope device array of this many bytes per GPU.
+// It holds the split-K partial sums of we_matmul_noalloc (about 4-6 MB for any M <= 64).
+constexpr size_t kNoallocScratchBytes = 16u << 20;
+// Looks up the array's address on `device`, which must be current; once per device (later calls return at once).
+hipError_t noalloc_scratch_init(int device);
+// The address noalloc_scratch_init found on `device`, or null before it succeeded.
+void* noalloc_scratch(int device);
+
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
 hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,

@@ -55,6 +55,7 @@ struct we_ctx {
   // graph is destroyed
   std::map<void*, int> scratch_refs;
   std::vector<void*> retired;
+  hipError_t noalloc_status = hipErrorNotInitialized;  // the device's allocation-free scratch lookup
 };
 
 namespace {
@@ -183,6 +184,9 @@ int we_ctx_create(int device, we_ctx** out) {
   };
   if (hipSetDevice(device) != hipSuccess) return cleanup(WE_EHIP);
   if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return cleanup(WE_EHIP);
+  // the allocation-free entry point's scratch array on this device (kept per device; its failure is reported by
+  // we_matmul_noalloc, the only user)
+  ctx->noalloc_status = we::noalloc_scratch_init(device);
   for (auto& st : ctx->lanes)
     if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return cleanup(WE_EHIP);
   ctx->compute = ctx->lanes[0];
@@ -599,12 +603,20 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
 namespace {
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res);
+                const float* gate, const void* res, bool noalloc = false);
 }  // namespace
 
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
               const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags) {
   return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, nullptr, nullptr);
+}
+
+int we_matmul_noalloc(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                      const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->noalloc_status != hipSuccess)
+    return hip_fail(ctx, ctx->noalloc_status, "allocation-free scratch of this device");
+  return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, nullptr, nullptr, true);
 }
 
 int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
@@ -621,7 +633,7 @@ int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const v
 namespace {
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res) {
+                const float* gate, const void* res, bool noalloc) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
@@ -734,11 +746,22 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     const uint32_t force = split_env ? (uint32_t)strtoul(split_env, nullptr, 10) : 0u;
     const we::GemmReducePlan rp = we::gemm_reduce_plan(L, force);
     if (rp.rsplits > 1) {
-      const int rc = ensure_scratch(ctx, rp.scratch_bytes);
-      if (rc) return rc;
+      if (noalloc) {
+        // the device's fixed scratch array: no allocation, a hard size limit
+        if (rp.scratch_bytes > we::kNoallocScratchBytes)
+          return fail(ctx, WE_EINVAL,
+                      "this GEMM (M %u, N %u, K %u) needs %zu bytes of split-K scratch; the allocation-free entry "
+                      "point has %zu (use we_matmul)",
+                      p->m, p->n, p->k, rp.scratch_bytes, we::kNoallocScratchBytes);
+        L.scratch = we::noalloc_scratch(ctx->device);
+        if (!L.scratch) return fail(ctx, WE_EHIP, "allocation-free scratch of device %d is not set up", ctx->device);
+      } else {
+        const int rc = ensure_scratch(ctx, rp.scratch_bytes);
+        if (rc) return rc;
+        L.scratch = ctx->scratch;
+      }
       L.rsplits = rp.rsplits;
       L.rkc = rp.rkc;
-      L.scratch = ctx->scratch;
     }
   }
   hipError_t e = we::gemm_launch(L, ctx->compute);

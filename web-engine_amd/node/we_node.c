@@ -459,7 +459,7 @@ static napi_value KSplitFor(napi_env env, napi_callback_info info) {
 }
 
 /* matmul(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags) */
-static napi_value Matmul(napi_env env, napi_callback_info info) {
+static napi_value matmul_call(napi_env env, napi_callback_info info, int noalloc) {
   args_t a;
   if (!get_args(env, info, &a, 12)) return NULL;
   we_ctx* ctx = ptr_arg(&a, 0);
@@ -481,9 +481,15 @@ static napi_value Matmul(napi_env env, napi_callback_info info) {
     napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
     return NULL;
   }
-  return status(env, ctx, we_matmul(ctx, (const we_matmul_params*)pdata, xdt, x, wdt, w, scales, group, ydt, y,
-                                    (const float*)bias, flags));
+  const we_matmul_params* p = (const we_matmul_params*)pdata;
+  return status(env, ctx, noalloc ? we_matmul_noalloc(ctx, p, xdt, x, wdt, w, scales, group, ydt, y, (const float*)bias, flags)
+                                  : we_matmul(ctx, p, xdt, x, wdt, w, scales, group, ydt, y, (const float*)bias, flags));
 }
+
+static napi_value Matmul(napi_env env, napi_callback_info info) { return matmul_call(env, info, 0); }
+
+/* matmulNoalloc(...): the arguments of matmul; allocates nothing (split-K scratch in a fixed per-GPU array) */
+static napi_value MatmulNoalloc(napi_env env, napi_callback_info info) { return matmul_call(env, info, 1); }
 
 /* matmulGated(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags, gate, residual):
  * y = residual + gate * v, the reference's gatedAdd after the GEMM fused into its epilogue */
@@ -919,7 +925,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
-      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulGated", MatmulGated},
+      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},

@@ -90,6 +90,7 @@ SIGNATURES = {
     "we_ksplit_for": (_U32, [_U32, _U32, _U32]),
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
+    "we_matmul_noalloc": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
     "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
     "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _U32, _P, _U32]),
@@ -338,6 +339,11 @@ class Graph:
             self.check(self.lib.we_matmul_gated(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
                                                 _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags,
                                                 _addr(gate), _addr(residual)))
+
+    def matmul_noalloc(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0):
+        """we_matmul_noalloc: we_matmul with its split-K scratch in the GPU's fixed array (allocates nothing)."""
+        self.check(self.lib.we_matmul_noalloc(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                              _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags))
 
     def peak(self, kind, workgroups, iters, out):
         """One dispatch of a peak kernel (timePeak, src/bench/peak.ts): returns its operation count."""
