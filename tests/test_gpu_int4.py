@@ -57,7 +57,9 @@ def test_qwen2_decode_shape_full(graph, m):
     assert O.rel_error(got32, want) < 1e-5
 
 
-@pytest.mark.parametrize("m,n,k,group,x_dt", [(1, 40, 128, 64, we.F16), (3, 33, 192, 64, we.F16),
+@pytest.mark.parametrize("m,n,k,group,x_dt", [(1, 40, 128, 64, we.F16), (1, 100, 1024, 128, we.F16),
+                                              (1, 37, 4096, 64, we.F16), (1, 50, 576, 64, we.F16),
+                                              (1, 24, 640, 320, we.F16), (3, 33, 192, 64, we.F16),
                                               (32, 64, 256, 128, we.F16), (33, 70, 320, 64, we.F16),
                                               (70, 31, 128, 64, we.F16), (5, 64, 256, 64, we.BF16),
                                               (9, 50, 192, 64, we.F32)])

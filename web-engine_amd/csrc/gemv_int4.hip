@@ -589,6 +589,122 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
   }
 }
 
+// ------------------------------------------------------------------------------------------------------
+// Decode kernel for M = 1 with f16 x (the decode shape). Every weight byte a wave needs is requested at its
+// start, straight into registers (K / 32 16-byte pieces per row, 16 lanes per row, up to 8 pieces per lane),
+// so the whole matrix is in flight at once, as in a streaming read: no LDS ring whose refills wait on the
+// arithmetic. x (interleaved per 8 values like the pipe kernel's) and the workgroup's scale tile go through
+// LDS; they are requested before the weights, so waiting for them never waits for the weight stream.
+//  * A workgroup of 4 waves owns 16 rows n (4 per wave, 16 lanes each): N / 16 workgroups, about 4.6 per CU at
+//    N = 18944, all resident at once (about 90 VGPRs and 10 KB of LDS each).
+//  * Lane (row, l) holds pieces P = l + 16 j: k = 32 P .. 32 P + 31, inside one scale group (group >= 64).
+//    Each word of a piece is 8 nibbles, unpacked exactly to f16 pairs ordered (k0, k4), (k1, k5), ... and
+//    multiplied with x by v_dot2_f32_f16 (products exact, f32 sums); the piece's f32 sum times its group's
+//    f16 scale adds to the lane's total.
+//  * The 16 lanes of a row are summed by a butterfly of cross-lane adds (fixed order), then one lane
+//    runs the epilogue.
+// a.x * b.x + a.y * b.y + c for two packed f16 pairs (v_dot2_f32_f16). The words come in by value: a
+// __builtin_bit_cast of a vector component expression (v.y) reads component 0 with this compiler.
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+
+constexpr int DIRECT_NP = 8;                                     // pieces per lane at most: K <= 4096
+constexpr int DIRECT_XMAX = DIRECT_NP * 16 * 32 * 2;             // staged x: K f16 values
+constexpr int DIRECT_SMAX = 16 * (DIRECT_NP * 16 * 32 / 64) * 2;  // scale tile: 16 rows x K / 64 groups
+
+template <int NP>  // pieces per lane: ceil(K / 512)
+__global__ void __launch_bounds__(256) int4_gemv_direct_kernel(Int4Args a) {
+  __shared__ __attribute__((aligned(16))) char xs[DIRECT_XMAX];
+  __shared__ __attribute__((aligned(16))) char ss[DIRECT_SMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, rl = wave * 4 + (lane >> 4);  // the lane's row among the workgroup's 16
+  const uint32_t n0 = blockIdx.x * 16, row = n0 + rl;
+  const uint32_t npc = a.k / 32;  // 16-byte pieces per row, at most 16 NP
+  const uint32_t gshift = a.gshift, ng = a.k / a.group;
+
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, (int)a.s_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
+
+  // x: K / 8 chunks of 16 bytes, at most two per thread
+  const uint32_t xchunks = a.k / 8;
+  u32x4 xv[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint32_t idx = tid + 256 * j;
+    xv[j] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, idx < xchunks ? (a.x_offset + idx * 8) * 2 : kInvalid, 0, 0));
+  }
+  // the scale tile s[n0 .. n0 + 16, :] is contiguous: 16-byte pieces, or halves for the last column tile
+  const uint32_t s_pieces = ng * 2;
+  const bool s_whole = n0 + 16 <= a.n;
+  constexpr int SH = DIRECT_SMAX / 2 / 256;
+  u32x4 sv = {0u, 0u, 0u, 0u};
+  uint16_t sh[SH] = {};
+  if (s_whole) {
+    sv = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)tid < s_pieces ? n0 * ng * 2 + tid * 16 : kInvalid, 0, 0));
+  } else {
+#pragma unroll
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + 256 * j;
+      sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < 16 * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
+    }
+  }
+  // the weights: all of the lane's pieces at once (pieces past the row read as zeros and are skipped below)
+  u32x4 wv[NP];
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    const uint32_t pc = (uint32_t)(l16 + 16 * j);
+    const uint32_t o = row < a.n && pc < npc ? row * (a.k / 2) + pc * 16 : kInvalid;
+    wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint32_t idx = tid + 256 * j;
+    if (idx < xchunks) *(u32x4*)(xs + idx * 16) = interleave8(xv[j]);
+  }
+  if (s_whole) {
+    if ((uint32_t)tid < s_pieces) *(u32x4*)(ss + tid * 16) = sv;
+  } else {
+#pragma unroll
+    for (int j = 0; j < SH; j++) {
+      const uint32_t i = tid + 256 * j;
+      if (i < 16 * ng) *(uint16_t*)(ss + i * 2) = sh[j];
+    }
+  }
+  // x and scales visible to every wave; unlike __syncthreads this does not wait for the weight loads
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const uint32_t m_lo = 0x000f000fu, m_hi = 0x00f000f0u;
+  const uint16_t* srow = (const uint16_t*)ss + rl * ng;
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    {  // pieces past the row's end (K % 512 != 0) are dropped by a select
+      const uint32_t pc = (uint32_t)(l16 + 16 * j);
+      const char* xp = xs + pc * 64;  // the piece's 4 chunks of 8 x values (inside xs for every pc)
+      float c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const u32x4 q = int4x8_to_f16_il(wv[j][e], m_lo, m_hi);
+        const u32x4 xx = *(const u32x4*)(xp + e * 16);
+        c0 = dot2_f16(xx.x, q.x, c0);
+        c1 = dot2_f16(xx.y, q.y, c1);
+        c0 = dot2_f16(xx.z, q.z, c0);
+        c1 = dot2_f16(xx.w, q.w, c1);
+      }
+      const float part = __builtin_fmaf(c0 + c1, f16_to_f32(srow[(pc >> (1 + gshift)) & 63u]), acc);
+      acc = pc < npc ? part : acc;
+    }
+  }
+  // the row's 16 lanes: butterfly over lane bits 3, 2, 1, 0 (every lane ends with the same sum)
+#pragma unroll
+  for (int d = 8; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 16);
+  if (l16 == 0 && row < a.n) int4_store(a, 0, row, acc);
+}
+
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   const int xb = L.x_dtype == F32 ? 4 : 2;
   const uint64_t x_need = L.k ? ((uint64_t)L.x_offset + (uint64_t)(L.m - 1) * L.x_stride + L.k) * xb : 0;
@@ -625,13 +741,31 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   const bool generic = path && !strcmp(path, "generic");
   const bool ring = L.x_dtype != F32 && L.m <= 16 && (64u << gshift) == L.group && !generic;
   const bool pipe = ring && !path && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.k / 64 <= 4 * (uint32_t)PIPE_MAXB;
-  if (ring && !pipe && L.k / L.group <= 64) {
+  // M = 1, f16 x, K <= 4096: every weight in flight at once (WE_INT4_PATH=pipe selects the ring kernel)
+  const bool direct = L.m == 1 && L.x_dtype == F16 && (64u << gshift) == L.group && L.k % 64 == 0 &&
+                      L.k <= (uint32_t)(DIRECT_NP * 16 * 32) && !path;
+  if (direct) {
+    const dim3 gd((L.n + 15) / 16), bd(256);
+    switch ((L.k / 32 + 15) / 16) {
+      case 1: hipLaunchKernelGGL(int4_gemv_direct_kernel<1>, gd, bd, 0, stream, a); break;
+      case 2: hipLaunchKernelGGL(int4_gemv_direct_kernel<2>, gd, bd, 0, stream, a); break;
+      case 3: hipLaunchKernelGGL(int4_gemv_direct_kernel<3>, gd, bd, 0, stream, a); break;
+      case 4: hipLaunchKernelGGL(int4_gemv_direct_kernel<4>, gd, bd, 0, stream, a); break;
+      case 5: hipLaunchKernelGGL(int4_gemv_direct_kernel<5>, gd, bd, 0, stream, a); break;
+      case 6: hipLaunchKernelGGL(int4_gemv_direct_kernel<6>, gd, bd, 0, stream, a); break;
+      case 7: hipLaunchKernelGGL(int4_gemv_direct_kernel<7>, gd, bd, 0, stream, a); break;
+      default: hipLaunchKernelGGL(int4_gemv_direct_kernel<8>, gd, bd, 0, stream, a); break;
+    }
+    return hipGetLastError();
+  }
+  const bool force_pipe = path && !strcmp(path, "pipe");
+  if (ring && !pipe && !force_pipe && L.k / L.group <= 64) {
     dim3 gs((L.n + 63) / 64);
     if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_shared_kernel<F16>, gs, dim3(256 * SK_WPT), 0, stream, a);
     else hipLaunchKernelGGL(int4_gemv_shared_kernel<BF16>, gs, dim3(256 * SK_WPT), 0, stream, a);
     return hipGetLastError();
   }
-  if (pipe) {
+  if (pipe || (force_pipe && ring && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.k / 64 <= 4 * (uint32_t)PIPE_MAXB)) {
     if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_pipe_kernel<F16>, grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL(int4_gemv_pipe_kernel<BF16>, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
