@@ -77,6 +77,11 @@ int we_buf_free(we_ctx* ctx, void* buf);                   /* back to the pool; 
 int we_buf_upload(we_ctx* ctx, void* buf, size_t offset, const void* src, size_t bytes); /* queue.writeBuffer */
 int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size_t bytes); /* Graph.read */
 int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes);
+/* Graph.read without blocking (src/gpu/graph.ts:109-119, whose mapAsync resolves later): queues the copy of
+ * `bytes` at buf + offset into pinned memory of this context (we_host_alloc) after the work queued so far, and
+ * returns a ticket; the data is there once we_ticket_wait (or we_ticket_done) reports the ticket done. */
+int we_buf_download_async(we_ctx* ctx, const void* buf, size_t offset, void* pinned_dst, size_t bytes,
+                          uint64_t* ticket);
 int we_mark(we_ctx* ctx, size_t* mark);                                         /* Graph.mark */
 int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep);     /* Graph.release */
 int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes); /* Graph.stats */
@@ -109,6 +114,15 @@ int we_stream_copy(we_ctx* ctx, void* dst, const void* pinned_src, size_t bytes,
 int we_wait_ticket(we_ctx* ctx, uint64_t ticket);   /* compute stream waits for a copy ticket */
 int we_record_compute(we_ctx* ctx, uint64_t* ticket); /* ticket for the compute work queued so far */
 int we_ticket_done(we_ctx* ctx, uint64_t ticket, int* done);
+/* Blocks the calling host thread until the ticket's work is done: the wait behind a Promise of
+ * device.queue.onSubmittedWorkDone() (src/model/weights.ts:128) or of an asynchronous read. It touches only the
+ * ticket's event, so a binding may call it from a worker thread while its main thread keeps using ctx; a failure's
+ * message is in we_last_error(NULL) of the waiting thread. Tickets live in a ring of 1024 events: a wait must start
+ * before 1024 newer tickets exist and should end before that many more are made (the slot is then re-recorded). */
+int we_ticket_wait(we_ctx* ctx, uint64_t ticket);
+/* Three tickets, for the work queued so far on compute stream 0, compute stream 1 and the copy stream: all three
+ * done is device.queue.onSubmittedWorkDone() (src/model/weights.ts:128, src/gpu/run-ahead.ts:5). */
+int we_record_all(we_ctx* ctx, uint64_t tickets[3]);
 
 /* ---- timing on the compute stream (hipEvents) ---- */
 int we_timer_start(we_ctx* ctx);

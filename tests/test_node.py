@@ -4,8 +4,11 @@ CPU: the addon loads under `node`, exports one function per entry point of inclu
 (matmulParams image and messages, kSplitFor) equals the oracle's, and index.js readHeader / readTensor read
 .safetensors files through the native reader with the reference's messages.
 GPU: tests/node_driver.js runs linear (fp8 + bias, fp8 + GELU, fp8 + LoRA, int4), norm, rotate, attention, the
-elementwise ops and a pinned-host stream copy through the addon; the results are checked here against the
-oracle with the bars of the matching C-ABI tests (test_gpu_matmul, test_gpu_int4, test_gpu_norm_rope,
+elementwise ops and a pinned-host stream copy through the addon, then the reference's own call shapes:
+Graph.run(code, bindings, workgroups) keyed by shader source (linear + addBias, LoRA, split-K + layer sum, norm
+with Params from device.queue.writeBuffer, rotate, elementwise with a { buffer, offset, size } binding),
+`await graph.device.queue.onSubmittedWorkDone()` and concurrent asynchronous reads; the results are checked here
+against the oracle with the bars of the matching C-ABI tests (test_gpu_matmul, test_gpu_int4, test_gpu_norm_rope,
 test_gpu_elementwise, test_gpu_attention)."""
 import json
 import pathlib
@@ -43,7 +46,8 @@ EXPORTS = {
     "we_graph_destroy": "graphDestroy", "we_peak": "peak", "we_read_peak": "readPeak", "we_st_open": "stOpen", "we_st_close": "stClose", "we_st_count": "stCount",
     "we_st_info": "stInfo", "we_st_find": "stFind", "we_st_metadata_count": "stMetadataCount",
     "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead", "we_stream_select": "streamSelect",
-    "we_stream_fork": "streamFork", "we_stream_join": "streamJoin",
+    "we_stream_fork": "streamFork", "we_stream_join": "streamJoin", "we_buf_download_async": "downloadAsync",
+    "we_ticket_wait": "waitTicketAsync", "we_record_all": "recordAll",
 }
 
 
@@ -107,6 +111,44 @@ def test_context_free_errors_throw_with_the_message():
                     'try { a.bufAlloc(null, 16); } catch (e) { r.push(e.message); }'
                     'console.log(JSON.stringify(r));')
     assert got == ["context is null", "context is null"]
+
+
+def test_graph_run_table_and_its_errors():
+    """registerKernels maps every reference export name it is given; Graph.run refuses an unregistered shader
+    and a wrong binding count before touching the device (a Graph without a context is enough here)."""
+    got = node_eval('''
+const we = require("./index.js");
+const ref = { matmulWgsl: (w, i = "rows", { splitK = false, accumulate = false } = {}) => `m ${w} ${splitK} ${accumulate}`,
+  rmsnormWgsl: "n", ropeKernel: (p) => `r ${p}`, ropeWgsl: "r interleaved", layerSumWgsl: "l", swigluWgsl: "s",
+  sigmoidGateWgsl: "sg", gatedAddWgsl: "ga", addBiasWgsl: "ab", geluTanhWgsl: "g", addWgsl: "a", siluWgsl: "si" };
+const out = { count: we.registerKernels(ref) };
+const g = Object.create(we.Graph.prototype);
+try { g.run("unknown\\nsecond line", [], [1]); } catch (e) { out.unknown = e.message; }
+try { g.run("n", [null, null], [1]); } catch (e) { out.count6 = e.message; }
+try { g.run("ga", [null, null, null, null], [1]); } catch (e) { out.count5 = e.message; }
+try { we.registerKernels({ rmsnormWgsl: 3 }); } catch (e) { out.notText = e.message; }
+console.log(JSON.stringify(out));''')
+    assert got["count"] == 20
+    assert got["unknown"].startswith('Graph.run: no MI355X kernel is registered for this shader ("unknown");')
+    assert got["count6"] == "Graph.run: rmsnorm takes 6 bindings (Params first), got 2"
+    assert got["count5"] == "Graph.run: elementwise takes 5 bindings (Params first), got 4"
+    assert got["notText"] == "registerKernels: rmsnormWgsl is not WGSL source text"
+
+
+def test_type_declarations_cover_the_module():
+    """index.d.ts declares exactly what index.js exports, and every Graph method it declares exists."""
+    import re
+    dts = (NODE_DIR / "index.d.ts").read_text()
+    declared = set(re.findall(r"^export (?:const|function|class) (\w+)", dts, re.M))
+    body = dts[dts.index("export class Graph {"):]
+    body = body[: body.index("\n}\n")]
+    methods = set(re.findall(r"^  (?:static )?(\w+)\(", body, re.M)) - {"constructor"}
+    got = node_eval('const w = require("./index.js"); const g = Object.create(w.Graph.prototype);'
+                    'console.log(JSON.stringify({ keys: Object.keys(w), methods: %s.filter((m) => '
+                    'typeof g[m] !== "function" && typeof w.Graph[m] !== "function") }))' % json.dumps(sorted(methods)))
+    assert declared == set(got["keys"])
+    assert got["methods"] == []
+    assert {"run", "read", "onSubmittedWorkDone", "writeBuffer", "buffer", "slice", "copy", "release"} <= methods
 
 
 def test_safetensors_through_the_addon(tmp_path):
@@ -254,6 +296,30 @@ def test_graph_steps_through_the_addon(tmp_path):
     cases.append(dict(name="stream", op="stream", x=_write(tmp_path, "blob", blob)))
     checks["stream"] = (np.uint8, lambda g: np.array_equal(g, blob))
 
+    # the same steps as Graph.run(code, bindings, workgroups) calls keyed by the reference's shader sources
+    by_name = {c["name"]: c for c in cases}
+    cases.append(dict(by_name["fp8_bias"], name="run_fp8_bias", op="runLinear"))
+    checks["run_fp8_bias"] = checks["fp8_bias"]
+    cases.append(dict(by_name["lora"], name="run_lora", op="runLinear"))
+    checks["run_lora"] = checks["lora"]
+    ms, ns, ks = 5, 12, 1024  # kSplitFor(5, 12, 1024) = 4: split-K partials, then the layer sum
+    xs = (rng.standard_normal(ms * ks)).astype(np.float32)
+    ws = (rng.standard_normal(ns * ks).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    split_want = O.matmul(O.matmul_params(ms, ns, ks, 0.5), O.F32, xs, O.BF16, ws)
+    cases.append(dict(name="run_split", op="runNarrow", m=ms, x=_write(tmp_path, "xs", xs),
+                      w=dict(file=_write(tmp_path, "ws", ws), dtype="bf16", scale=0.5, n=ns, k=ks)))
+    checks["run_split"] = (np.float32, lambda g: O.rel_error(g, split_want) < 1e-5)
+    cases.append(dict(by_name["norm"], name="run_norm", op="runNorm"))
+    checks["run_norm"] = checks["norm"]
+    cases.append(dict(by_name["rotate"], name="run_rotate", op="runRotate"))
+    checks["run_rotate"] = checks["rotate"]
+    cases.append(dict(name="run_gatedAdd", op="runElementwise", code="gatedAddWgsl", inputs=[fa, fb, fg],
+                      sizes=[ne, de], sliceLast=True))
+    checks["run_gatedAdd"] = checks["gatedAdd"]
+    cases.append(dict(name="run_swiglu", op="runElementwise", code="swigluWgsl", inputs=[fa, fb], sizes=[ne]))
+    checks["run_swiglu"] = checks["swiglu"]
+    cases.append(dict(name="run_unknown", op="runUnknown", expectError=True))
+
     (tmp_path / "spec.json").write_text(json.dumps(dict(cases=cases)))
     print(f"[node] {len(cases)} cases in {tmp_path}", flush=True)
     out = subprocess.run([NODE, str(ROOT / "tests" / "node_driver.js"), str(tmp_path)], capture_output=True,
@@ -262,7 +328,11 @@ def test_graph_steps_through_the_addon(tmp_path):
     assert out.returncode == 0
     result = json.loads((tmp_path / "result.json").read_text())
     assert result["device"]["arch"].startswith("gfx950")
-    assert result["errors"] == {"lora_rank3": "LoRA shapes do not fit the linear layer"}
+    assert result["errors"]["lora_rank3"] == "LoRA shapes do not fit the linear layer"
+    assert result["errors"]["run_unknown"].startswith("Graph.run: no MI355X kernel is registered for this shader")
+    assert len(result["errors"]) == 2
+    assert result["registered"] == 20  # 9 matmul variants, rmsnorm, 2 rope pairings, layer sum, 7 elementwise
+    assert result["concurrentReads"] == [1, 2, 3]
     assert result["reusedDelta"] >= 1 and result["zeroed"]
     failed = []
     for name, (dtype, ok) in checks.items():

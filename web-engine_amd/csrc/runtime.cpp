@@ -4,6 +4,7 @@
 // points that hand off to the kernels.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -38,7 +39,7 @@ struct we_ctx {
   std::map<uintptr_t, size_t> pinned;                     // pinned host allocations
   uint64_t created = 0, reused = 0, created_bytes = 0;
   std::vector<hipEvent_t> tickets;
-  uint64_t next_ticket = 1;
+  std::atomic<uint64_t> next_ticket{1};  // read by we_ticket_wait from other host threads
   void* scratch = nullptr;  // kernel scratch (split-K partial sums, attention V^T) of the selected compute
   bool capturing = false;   // stream, grown on demand; between we_graph_begin and we_graph_end
   size_t scratch_bytes = 0;
@@ -169,6 +170,8 @@ int ticket_valid(we_ctx* ctx, uint64_t t) {
 }  // namespace
 
 extern "C" {
+
+int we_host_span(we_ctx* ctx, const void* p, size_t bytes);
 
 int we_ctx_create(int device, we_ctx** out) {
   if (!out) return fail(nullptr, WE_EINVAL, "output pointer is null");
@@ -312,6 +315,36 @@ int we_buf_download(we_ctx* ctx, const void* buf, size_t offset, void* dst, size
   return WE_OK;
 }
 
+int we_buf_download_async(we_ctx* ctx, const void* buf, size_t offset, void* pinned_dst, size_t bytes,
+                          uint64_t* ticket) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  if (!ticket) return fail(ctx, WE_EINVAL, "output pointer is null");
+  int rc = check_span(ctx, (const char*)buf + offset, bytes, "download source");
+  if (rc) return rc;
+  rc = we_host_span(ctx, pinned_dst, bytes);
+  if (rc) return rc;
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  if (bytes)
+    HIP_OK(ctx, hipMemcpyAsync(pinned_dst, (const char*)buf + offset, bytes, hipMemcpyDeviceToHost, ctx->compute),
+           "download");
+  return new_ticket(ctx, ctx->compute, ticket);
+}
+
+int we_ticket_wait(we_ctx* ctx, uint64_t ticket) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  // reads only the ticket's event (created with the context), so another host thread may keep using ctx; the
+  // message of a failure goes to the context-free slot of this thread, not to ctx
+  if (ticket == 0 || ticket >= ctx->next_ticket)
+    return fail(nullptr, WE_EINVAL, "unknown ticket %llu", (unsigned long long)ticket);
+  if (ticket + kTicketRing < ctx->next_ticket)
+    return fail(nullptr, WE_EINVAL, "ticket %llu expired (more than %zu tickets since)", (unsigned long long)ticket,
+                kTicketRing);
+  const hipError_t e = hipEventSynchronize(ticket_event(ctx, ticket));
+  if (e != hipSuccess) return fail(nullptr, WE_EHIP, "hipEventSynchronize: %s", hipGetErrorString(e));
+  return WE_OK;
+}
+
 int we_buf_copy(we_ctx* ctx, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (bytes == 0) return WE_OK;
@@ -366,6 +399,16 @@ int we_sync(we_ctx* ctx) {
 }
 
 // ------------------------------------------------------------------------------------------ two compute streams
+
+int we_record_all(we_ctx* ctx, uint64_t tickets[3]) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  if (!tickets) return fail(ctx, WE_EINVAL, "output pointer is null");
+  int rc = new_ticket(ctx, ctx->lanes[0], &tickets[0]);
+  if (!rc) rc = new_ticket(ctx, ctx->lanes[1], &tickets[1]);
+  if (!rc) rc = new_ticket(ctx, ctx->copy, &tickets[2]);
+  return rc;
+}
 
 int we_stream_select(we_ctx* ctx, int stream) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");

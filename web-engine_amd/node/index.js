@@ -12,12 +12,78 @@ const ELEM_BYTES = { [F32]: 4, [F16]: 2, [BF16]: 2, [FP8]: 1 };
 const EPI = { ACCUMULATE: 1, SPLIT_K: 2, BIAS: 4, GELU_TANH: 8 };
 const OP = { SWIGLU: 0, SIGMOID_GATE: 1, GATED_ADD: 2, ADD_BIAS: 3, GELU_TANH: 4, ADD: 5, SILU: 6 };
 
-const ptrOf = (b) => (b == null ? null : typeof b === "bigint" ? b : b.ptr);
+// A binding is a buffer { ptr, size }, a Graph.slice of one, the reference's { buffer, offset, size } form, or a
+// BigInt address.
+const ptrOf = (b) =>
+  b == null ? null : typeof b === "bigint" ? b : b.buffer !== undefined ? b.buffer.ptr + BigInt(b.offset || 0) : b.ptr;
+const ownerOf = (b) => (b != null && typeof b === "object" && b.buffer !== undefined ? b.buffer : b);
+const offsetOf = (b) => (b != null && typeof b === "object" && b.buffer !== undefined ? b.offset || 0 : 0);
+
+// Graph.run's table: the WGSL source text of a reference shader -> the MI355X kernel computing the same thing.
+const KERNELS = new Map();
+// the reference's elementwise exports (src/kernels/elementwise.ts:38-86): [name, op, inputs between params and out]
+const ELEMENTWISE = [
+  ["swigluWgsl", OP.SWIGLU, 2], ["sigmoidGateWgsl", OP.SIGMOID_GATE, 2], ["gatedAddWgsl", OP.GATED_ADD, 3],
+  ["addBiasWgsl", OP.ADD_BIAS, 2], ["geluTanhWgsl", OP.GELU_TANH, 1], ["addWgsl", OP.ADD, 2], ["siluWgsl", OP.SILU, 1],
+];
+const PARAM_BYTES = { matmul: 52, rmsnorm: 16, rope: 12, layerSum: 12, elementwise: 8 };
+const SHADOW_MAX = 256; // buffers made from data up to this size keep a host copy, so run() reads Params without a sync
+
+/**
+ * Fills Graph.run's table from the reference's kernel exports, given by their reference names (e.g. the modules
+ * src/kernels/matmul.ts, rmsnorm.ts, rope.ts, elementwise.ts and text.ts spread into one object):
+ *   matmulWgsl (the function, src/kernels/matmul.ts:118: fp8 / bf16 / f32 weights x plain, splitK, accumulate),
+ *   matmulFp8Wgsl / matmulBf16Wgsl / matmulF32Wgsl, rmsnormWgsl, ropeKernel or ropeWgsl / ropeHalfWgsl,
+ *   layerSumWgsl, and swigluWgsl, sigmoidGateWgsl, gatedAddWgsl, addBiasWgsl, geluTanhWgsl, addWgsl, siluWgsl.
+ * Returns how many sources the table maps. Shaders outside this list (conv3x3, attention parts, the VAE's) have
+ * no MI355X kernel here, and Graph.run throws for them.
+ */
+function registerKernels(ref) {
+  const put = (name, code, kernel) => {
+    if (typeof code !== "string") throw new TypeError(`registerKernels: ${name} is not WGSL source text`);
+    KERNELS.set(code, kernel);
+  };
+  if (ref.matmulWgsl !== undefined) {
+    for (const w of ["fp8", "bf16", "f32"]) {
+      put(`matmulWgsl("${w}")`, ref.matmulWgsl(w, "rows", {}), { op: "matmul", weights: DTYPES[w], flags: 0 });
+      put(`matmulWgsl("${w}", splitK)`, ref.matmulWgsl(w, "rows", { splitK: true }),
+          { op: "matmul", weights: DTYPES[w], flags: EPI.SPLIT_K });
+      put(`matmulWgsl("${w}", accumulate)`, ref.matmulWgsl(w, "rows", { accumulate: true }),
+          { op: "matmul", weights: DTYPES[w], flags: EPI.ACCUMULATE });
+    }
+  }
+  for (const [name, w] of [["matmulFp8Wgsl", FP8], ["matmulBf16Wgsl", BF16], ["matmulF32Wgsl", F32]])
+    if (ref[name] !== undefined) put(name, ref[name], { op: "matmul", weights: w, flags: 0 });
+  if (ref.rmsnormWgsl !== undefined) put("rmsnormWgsl", ref.rmsnormWgsl, { op: "rmsnorm" });
+  if (ref.ropeKernel !== undefined) {
+    put('ropeKernel("interleaved")', ref.ropeKernel("interleaved"), { op: "rope", half: false });
+    put('ropeKernel("half")', ref.ropeKernel("half"), { op: "rope", half: true });
+  }
+  if (ref.ropeWgsl !== undefined) put("ropeWgsl", ref.ropeWgsl, { op: "rope", half: false });
+  if (ref.ropeHalfWgsl !== undefined) put("ropeHalfWgsl", ref.ropeHalfWgsl, { op: "rope", half: true });
+  if (ref.layerSumWgsl !== undefined) put("layerSumWgsl", ref.layerSumWgsl, { op: "layerSum" });
+  for (const [name, op, inputs] of ELEMENTWISE)
+    if (ref[name] !== undefined) put(name, ref[name], { op: "elementwise", kind: op, inputs });
+  return KERNELS.size;
+}
+
+const bindingCount = (k) => (k.op === "matmul" ? 4 : k.op === "rmsnorm" ? 6 : k.op === "rope" ? 5 : k.op === "layerSum" ? 4 : k.inputs + 2);
 
 class Graph {
   /** src/gpu/graph.ts:35: one context (device, streams, pool) per graph. */
   constructor(device = 0) {
     this.ctx = addon.create(device);
+    this.shadow = new WeakMap(); // buffer -> host copy of its bytes (small buffers made from data: Params)
+    this.staging = new Map();    // size -> free pinned blocks for read()
+    this.pending = 0;            // reads and onSubmittedWorkDone waits not yet settled
+    // graph.device.queue as the reference's callers use it (src/model/weights.ts:128, src/gpu/graph.ts:47)
+    this.device = {
+      queue: {
+        writeBuffer: (buffer, offset, data, dataOffset, size) => this.writeBuffer(buffer, offset, data, dataOffset, size),
+        onSubmittedWorkDone: () => this.onSubmittedWorkDone(),
+        submit: () => {},
+      },
+    };
   }
 
   /** src/gpu/graph.ts:38-54: a device buffer with this data, or zeroed with this many bytes (pooled by size). */
@@ -25,8 +91,90 @@ class Graph {
     const bytes = typeof data === "number" ? data : data.byteLength;
     const size = Math.max(4, Math.ceil(bytes / 4) * 4);
     const ptr = addon.bufAlloc(this.ctx, size);
-    if (typeof data !== "number" && data.byteLength) addon.upload(this.ctx, ptr, 0, data);
-    return { ptr, size };
+    const buffer = { ptr, size };
+    if (typeof data !== "number" && data.byteLength) {
+      addon.upload(this.ctx, ptr, 0, data);
+      if (data.byteLength <= SHADOW_MAX) {
+        const view = ArrayBuffer.isView(data) ? new Uint8Array(data.buffer, data.byteOffset, data.byteLength) : new Uint8Array(data);
+        this.shadow.set(buffer, Uint8Array.from(view));
+      }
+    }
+    return buffer;
+  }
+
+  /**
+   * GPUQueue.writeBuffer: `data` at byte `offset` of `buffer`; `dataOffset` and `size` count elements of a typed
+   * array, bytes of an ArrayBuffer (WebGPU's rule). The upload is done when this returns.
+   */
+  writeBuffer(buffer, offset, data, dataOffset = 0, size) {
+    const unit = ArrayBuffer.isView(data) ? data.BYTES_PER_ELEMENT || 1 : 1;
+    const base = ArrayBuffer.isView(data) ? data.byteOffset : 0;
+    const raw = ArrayBuffer.isView(data) ? data.buffer : data;
+    const total = ArrayBuffer.isView(data) ? data.byteLength : data.byteLength;
+    const begin = dataOffset * unit;
+    const bytes = size === undefined ? total - begin : size * unit;
+    if (begin < 0 || bytes < 0 || begin + bytes > total) throw new RangeError("writeBuffer: range runs past the data");
+    const view = new Uint8Array(raw, base + begin, bytes);
+    const owner = ownerOf(buffer);
+    const at = offsetOf(buffer) + offset;
+    addon.upload(this.ctx, ptrOf(owner), at, view);
+    const sh = this.shadow.get(owner);
+    if (sh !== undefined) {
+      if (at + bytes <= sh.byteLength) sh.set(view, at);
+      else this.shadow.delete(owner);
+    }
+  }
+
+  /** The first `bytes` of a Params binding: the host copy when there is one, else a (waiting) download. */
+  paramsOf(binding, bytes) {
+    const owner = ownerOf(binding), off = offsetOf(binding);
+    const sh = this.shadow.get(owner);
+    if (sh !== undefined && off + bytes <= sh.byteLength) return sh.slice(off, off + bytes).buffer;
+    return addon.download(this.ctx, ptrOf(binding), 0, bytes);
+  }
+
+  /**
+   * src/gpu/graph.ts:76-89: queues one dispatch of a reference shader, with its bindings in order (Params first).
+   * The shader is looked up in the table registerKernels fills and runs as the MI355X kernel that computes the
+   * same thing; its Params are decoded here. `workgroups` is accepted for the reference's signature: the MI355X
+   * kernels size their own grids (a split-K matmul takes its slice count from Params.k_split, as the reference's
+   * kernel does).
+   */
+  run(code, bindings, workgroups) {
+    const k = KERNELS.get(code);
+    if (k === undefined) {
+      const head = typeof code === "string" ? code.trim().split("\n")[0].slice(0, 60) : String(code);
+      throw new Error(`Graph.run: no MI355X kernel is registered for this shader ("${head}"); registerKernels maps the reference's WGSL exports`);
+    }
+    if (!Array.isArray(bindings) || bindings.length !== bindingCount(k))
+      throw new Error(`Graph.run: ${k.op} takes ${bindingCount(k)} bindings (Params first), got ${Array.isArray(bindings) ? bindings.length : typeof bindings}`);
+    const raw = this.paramsOf(bindings[0], PARAM_BYTES[k.op]);
+    const u = new Uint32Array(raw), f = new Float32Array(raw);
+    const b = (i) => ptrOf(bindings[i]);
+    let out;
+    switch (k.op) {
+      case "matmul": // [p, x, w, y]: f32 x and y (src/kernels/matmul.ts:127-132)
+        addon.matmul(this.ctx, u, F32, b(1), k.weights, b(2), null, 0, F32, b(3), null, k.flags);
+        out = 3;
+        break;
+      case "rmsnorm": // [p, x, weight, scale, shift, out], Params { rows, d, eps: f32, offset: f32 }
+        addon.rmsnorm(this.ctx, u[0], u[1], f[2], f[3], F32, b(1), b(2), b(3), b(4), b(5));
+        out = 5;
+        break;
+      case "rope": // [p, x, cos, sin, out], Params { tokens, heads, pairs }
+        addon.rope(this.ctx, u[0], u[1], u[2], k.half ? 1 : 0, F32, b(1), b(2), b(3), b(4));
+        out = 4;
+        break;
+      case "layerSum": // [p, x, w, out], Params { tokens, layers, dim }
+        addon.layerSum(this.ctx, u[0], u[1], u[2], b(1), b(2), b(3));
+        out = 3;
+        break;
+      default: // elementwise: [p, inputs..., out], Params { n, d }
+        addon.elementwise(this.ctx, k.kind, u[0], u[1], F32, b(1), k.inputs > 1 ? b(2) : null,
+                          k.inputs > 2 ? b(3) : null, b(k.inputs + 1));
+        out = k.inputs + 1;
+    }
+    this.shadow.delete(ownerOf(bindings[out])); // the kernel writes it: a host copy would go stale
   }
 
   /** src/gpu/graph.ts:57-60 */
@@ -37,13 +185,45 @@ class Graph {
   /** Work is queued on the context's stream as it is issued; nothing is held back. */
   submit() {}
 
-  /** src/gpu/graph.ts:109-119: runs everything queued, then copies `bytes` of `buffer` back. */
+  /**
+   * src/gpu/graph.ts:109-119: copies `bytes` of `buffer` back after everything queued before. The copy goes to
+   * pinned memory on the selected compute stream and the wait runs on a worker thread, so the event loop keeps
+   * running meanwhile; the Promise resolves to an ArrayBuffer.
+   */
   async read(buffer, bytes = buffer.size) {
-    return addon.download(this.ctx, buffer.ptr, 0, bytes);
+    if (bytes === 0) return new ArrayBuffer(0);
+    const size = Math.max(4096, 2 ** Math.ceil(Math.log2(bytes)));
+    const free = this.staging.get(size);
+    const pinned = free !== undefined && free.length ? free.pop() : addon.hostAlloc(this.ctx, size);
+    const ticket = addon.downloadAsync(this.ctx, ptrOf(buffer), 0, pinned, bytes);
+    this.pending++;
+    try {
+      await addon.waitTicketAsync(this.ctx, ticket);
+      return addon.hostRead(this.ctx, pinned, bytes);
+    } finally {
+      this.pending--;
+      if (this.ctx !== null) {
+        if (!this.staging.has(size)) this.staging.set(size, []);
+        this.staging.get(size).push(pinned);
+      }
+    }
+  }
+
+  /**
+   * GPUQueue.onSubmittedWorkDone (src/model/weights.ts:128, src/gpu/run-ahead.ts:5): resolves once the work queued
+   * so far on both compute streams and the copy stream has finished; waits on worker threads.
+   */
+  onSubmittedWorkDone() {
+    const tickets = addon.recordAll(this.ctx);
+    this.pending++;
+    return Promise.all(tickets.map((t) => addon.waitTicketAsync(this.ctx, t))).then(
+      () => { this.pending--; },
+      (e) => { this.pending--; throw e; });
   }
 
   copy(src, srcOffset, dst, dstOffset, size) {
-    addon.copy(this.ctx, src.ptr, srcOffset, dst.ptr, dstOffset, size);
+    addon.copy(this.ctx, ptrOf(src), srcOffset, ptrOf(dst), dstOffset, size);
+    this.shadow.delete(ownerOf(dst));
   }
 
   mark() {
@@ -63,9 +243,12 @@ class Graph {
     return addon.stats(this.ctx);
   }
 
+  /** Frees everything. Settle (await) every read() and onSubmittedWorkDone() first: their waits use the context. */
   destroy() {
-    if (this.ctx !== null) addon.destroy(this.ctx);
+    if (this.pending) throw new Error(`Graph.destroy: ${this.pending} read() / onSubmittedWorkDone() promises still pending; await them first`);
+    if (this.ctx !== null) addon.destroy(this.ctx); // frees the pinned staging blocks with the context
     this.ctx = null;
+    this.staging.clear();
   }
 
   sync() {
@@ -329,6 +512,6 @@ module.exports = {
   addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP,
   matmulParams, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
-  SafetensorsError, readHeader, readTensor,
+  SafetensorsError, readHeader, readTensor, registerKernels,
   lastError: (graph) => addon.lastError(graph ? graph.ctx : null),
 };

@@ -12,6 +12,8 @@
 #define NAPI_VERSION 8
 #include <node_api.h>
 #include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "we.h"
@@ -394,6 +396,27 @@ static napi_value HostSpan(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_host_span(ctx, p, (size_t)bytes));
 }
 
+/* hostRead(ctx, ptr, bytes) -> ArrayBuffer: a copy of pinned memory of ctx (e.g. what downloadAsync wrote) */
+static napi_value HostRead(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 3)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* p = ptr_arg(&a, 1);
+  double bytes = f64_arg(&a, 2);
+  if (a.bad) return NULL;
+  if (!(bytes >= 0 && bytes <= 9007199254740991.0 && bytes == (double)(uint64_t)bytes)) {
+    napi_throw_range_error(env, NULL, "bytes must be a non-negative integer");
+    return NULL;
+  }
+  int rc = we_host_span(ctx, p, (size_t)bytes);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  void* data = NULL;
+  napi_value ab;
+  if (napi_create_arraybuffer(env, (size_t)bytes, &data, &ab) != napi_ok) return NULL;
+  if (bytes) memcpy(data, p, (size_t)bytes);
+  return ab;
+}
+
 static napi_value StreamCopy(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 5)) return NULL;
@@ -416,6 +439,104 @@ static napi_value WaitTicket(napi_env env, napi_callback_info info) {
   double t = f64_arg(&a, 1);
   if (a.bad) return NULL;
   return status(env, ctx, we_wait_ticket(ctx, (uint64_t)t));
+}
+
+/* downloadAsync(ctx, buf, offset, pinnedDst, bytes) -> ticket: the copy into pinned memory is queued, not done */
+static napi_value DownloadAsync(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* src = ptr_arg(&a, 1);
+  double off = f64_arg(&a, 2);
+  void* dst = ptr_arg(&a, 3);
+  double bytes = f64_arg(&a, 4);
+  if (a.bad) return NULL;
+  uint64_t t = 0;
+  int rc = we_buf_download_async(ctx, src, (size_t)off, dst, (size_t)bytes, &t);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)t);
+}
+
+/* waitTicketAsync(ctx, ticket) -> Promise<void>: we_ticket_wait runs on a libuv worker thread, so the event loop
+ * keeps running while the GPU works (the mapAsync / onSubmittedWorkDone promises of src/gpu/graph.ts:117 and
+ * src/model/weights.ts:128). */
+typedef struct {
+  napi_async_work work;
+  napi_deferred deferred;
+  we_ctx* ctx;
+  uint64_t ticket;
+  int rc;
+  char msg[512];
+} ticket_wait_t;
+
+static void ticket_wait_exec(napi_env env, void* data) {
+  (void)env;
+  ticket_wait_t* w = (ticket_wait_t*)data;
+  w->rc = we_ticket_wait(w->ctx, w->ticket);
+  if (w->rc != WE_OK) snprintf(w->msg, sizeof w->msg, "%s", we_last_error(NULL));
+}
+
+static void ticket_wait_done(napi_env env, napi_status st, void* data) {
+  ticket_wait_t* w = (ticket_wait_t*)data;
+  if (st == napi_ok && w->rc == WE_OK) {
+    napi_resolve_deferred(env, w->deferred, undefined(env));
+  } else {
+    napi_value msg, err;
+    napi_create_string_utf8(env, st == napi_ok ? w->msg : "ticket wait cancelled", NAPI_AUTO_LENGTH, &msg);
+    napi_create_error(env, NULL, msg, &err);
+    napi_reject_deferred(env, w->deferred, err);
+  }
+  napi_delete_async_work(env, w->work);
+  free(w);
+}
+
+static napi_value WaitTicketAsync(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double t = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  if (!ctx) {
+    napi_throw_error(env, NULL, "context is null");
+    return NULL;
+  }
+  ticket_wait_t* w = (ticket_wait_t*)calloc(1, sizeof *w);
+  if (!w) {
+    napi_throw_error(env, NULL, "out of host memory");
+    return NULL;
+  }
+  w->ctx = ctx;
+  w->ticket = (uint64_t)t;
+  napi_value promise, name;
+  napi_create_promise(env, &w->deferred, &promise);
+  napi_create_string_utf8(env, "we.waitTicketAsync", NAPI_AUTO_LENGTH, &name);
+  if (napi_create_async_work(env, NULL, name, ticket_wait_exec, ticket_wait_done, w, &w->work) != napi_ok) {
+    free(w);
+    napi_throw_error(env, NULL, "could not create the ticket wait");
+    return NULL;
+  }
+  if (napi_queue_async_work(env, w->work) != napi_ok) {
+    napi_delete_async_work(env, w->work);
+    free(w);
+    napi_throw_error(env, NULL, "could not queue the ticket wait");
+    return NULL;
+  }
+  return promise;
+}
+
+/* recordAll(ctx) -> [t0, t1, tCopy]: tickets for the work queued so far on both compute streams and the copy stream */
+static napi_value RecordAll(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 1)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  if (a.bad) return NULL;
+  uint64_t t[3] = {0, 0, 0};
+  int rc = we_record_all(ctx, t);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  napi_value arr;
+  napi_create_array_with_length(env, 3, &arr);
+  for (uint32_t i = 0; i < 3; i++) napi_set_element(env, arr, i, num(env, (double)t[i]));
+  return arr;
 }
 
 static napi_value RecordCompute(napi_env env, napi_callback_info info) {
@@ -923,8 +1044,9 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
-      {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan},
+      {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
+      {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},
       {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},

@@ -80,6 +80,9 @@ SIGNATURES = {
     "we_host_alloc": (_I, [_P, _SZ, _P]),
     "we_host_free": (_I, [_P, _P]),
     "we_host_span": (_I, [_P, _P, ctypes.c_size_t]),
+    "we_buf_download_async": (_I, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint64)]),
+    "we_ticket_wait": (_I, [_P, ctypes.c_uint64]),
+    "we_record_all": (_I, [_P, _P]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
     "we_wait_ticket": (_I, [_P, _U64]),
     "we_record_compute": (_I, [_P, _P]),
