@@ -22,11 +22,13 @@ is launched on):
   * traffic: HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this script, scaled by
     what the same counters read for the elementwise add kernel of known traffic that this script also
     launches (calibration); the measured values live in profiles/traffic.json;
-  * cpu_baseline: the float64 triple loop of the reference's tests (the oracle's restatement), on one
-    host core, on a time-bounded sample of rows of the up-projection, extrapolated.
+  * cpu_baseline: the same workload on the host's cores: an f32 AVX-512 GEMM on every CPU of the process's
+    affinity (oracle/cpu_gemm.c; the headline CPU number) and the float64 triple loop of the reference's tests
+    on one core, over C1-C4, with the CPU model and core counts; sampled rows are extrapolated and say so.
 """
 import argparse
 import json
+import os
 import pathlib
 import sys
 import time
@@ -301,28 +303,118 @@ def calibration_copy(g, nbytes=256 << 20):
     return {"kernel": "elementwise_kernel<F32> (add)", "read_bytes": 2 * nbytes, "write_bytes": nbytes}
 
 
+def host_info():
+    """The host the CPU numbers come from: CPU model, online CPUs, this process's affinity, vector ISA."""
+    model, flags = "unknown", set()
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    affinity = sorted(os.sched_getaffinity(0))
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(affinity),
+            "isa": [f for f in ("avx2", "fma", "avx512f", "avx512_bf16", "amx_bf16") if f in flags]}
+
+
+def _timed(fn, min_s=0.0):
+    """Seconds per call of fn: one call, repeated until min_s has passed (best of the repeats)."""
+    best, total = float("inf"), 0.0
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        best, total = min(best, dt), total + dt
+        if total >= min_s:
+            return best
+
+
 def cpu_baseline(budget_s):
-    """The reference's CPU path for this op is the float64 triple loop of tests/gpu/matmul.test.ts:26-35;
-    it is timed here through the oracle's C restatement on one core over whole rows of the up-projection
-    until the time budget is used, then extrapolated to TFLOP/s."""
+    """The reference's CPU path for this op is the float64 triple loop of tests/gpu/matmul.test.ts:26-35.
+
+    Two legs, both on the same inputs' shapes as the GPU run:
+      * faithful: that loop through the oracle's C restatement (or_matmul_f64), one core, float64 accumulation;
+        C1 (64 x 3072 x 3072) in full, and whole rows of C2 / the C3 up-projection / C4 (M = 1) until about
+        `budget_s` is used, extrapolated to the full M;
+      * strong: oracle/cpu_gemm.c on every CPU of this process's affinity (at most 16), f32 accumulation, AVX-512
+        when present: C1 in full, the C3 MLP step (up + GELU-tanh + down) and C2 on 192 sampled rows
+        extrapolated to M = 4096 (the cost is linear in M at these sizes), C4 in full at M = 1, 8, 16.
+    The headline value is the strong leg on the benchmarked workload (the C3 MLP step)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
-    m, n, k = 4096, 12288, 3072
     rng = np.random.default_rng(7)
-    rows_max = 64
-    x = bf16_bits(rng.standard_normal(rows_max * k, dtype=np.float32))
-    w = fp8_finite_codes(rng, n * k)
-    p = O.matmul_params(rows_max, n, k, 0.02)
-    rows = 0
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    hidden, mlp_n, mt = 3072, 12288, 4096
+    w_up, w_down = fp8_finite_codes(rng, mlp_n * hidden), fp8_finite_codes(rng, hidden * mlp_n)
+    w_qkv = bf16_bits(rng.normal(0, 0.02, 9216 * hidden).astype(np.float32))
+    w_c1 = fp8_finite_codes(rng, 3072 * 3072)
+    x_c1 = rng.standard_normal(64 * 3072).astype(np.float16).view(np.uint16)
+    n4, k4, g4 = 18944, 3584, 64
+    w4 = rng.integers(0, 2 ** 32, n4 * k4 // 8, dtype=np.uint64).astype(np.uint32)
+    s4 = np.abs(rng.normal(0, 0.01, n4 * k4 // g4)).astype(np.float16).view(np.uint16)
+    int4_bytes = lambda m: n4 * k4 // 2 + n4 * (k4 // g4) * 2 + m * k4 * 2 + m * n4 * 2
+
+    # ---- strong leg
+    rows = 192
+    xs = bf16_bits(rng.standard_normal(rows * hidden, dtype=np.float32))
+
+    def mlp_step():  # as on the GPU: GELU in the up GEMM's epilogue, bf16 hidden activations
+        h = O.cpu_matmul(rows, mlp_n, hidden, 0.02, O.BF16, xs, O.FP8, w_up, y_dtype=O.BF16, threads=threads,
+                         gelu=True)
+        O.cpu_matmul(rows, hidden, mlp_n, 0.02, O.BF16, h, O.FP8, w_down, y_dtype=O.BF16, threads=threads)
+
+    t_mlp = _timed(mlp_step, 1.0)
+    mlp_flop = 2 * 2 * mt * hidden * mlp_n
+    strong = {"c3_mlp_step": {"tflops": 2 * 2 * rows * hidden * mlp_n / t_mlp / 1e12,
+                              "ms_extrapolated": t_mlp * mt / rows * 1e3,
+                              "sample": f"{rows} of {mt} rows (up + GELU + down), extrapolated"}}
+    t = _timed(lambda: O.cpu_matmul(rows, 9216, hidden, 1.0, O.BF16, xs, O.BF16, w_qkv, y_dtype=O.BF16,
+                                    threads=threads), 0.5)
+    strong["c2_bf16_qkv_4096x9216x3072"] = {"tflops": 2 * rows * 9216 * hidden / t / 1e12,
+                                           "sample": f"{rows} of {mt} rows, extrapolated"}
+    t = _timed(lambda: O.cpu_matmul(64, 3072, 3072, 0.02, O.F16, x_c1, O.FP8, w_c1, y_dtype=O.F16,
+                                    threads=threads), 0.5)
+    strong["c1_fp8_64x3072x3072"] = {"us": t * 1e6, "tflops": 2 * 64 * 3072 * 3072 / t / 1e12, "sample": "full"}
+    for m in (1, 8, 16):
+        x4 = rng.standard_normal(m * k4).astype(np.float16).view(np.uint16)
+        t = _timed(lambda: O.cpu_matmul(m, n4, k4, 1.0, O.F16, x4, O.INT4, w4, s4, g4, y_dtype=O.F16,
+                                        threads=threads), 0.5)
+        strong[f"c4_int4_M{m}"] = {"us": t * 1e6, "gbs": int4_bytes(m) / t / 1e9, "sample": "full"}
+
+    # ---- faithful leg: float64 loop, one core
+    faithful = {}
+    share = max(0.5, (budget_s - 2.5) / 3)  # the C4 row below takes about 2.5 s
+    xf = bf16_bits(rng.standard_normal(64 * hidden, dtype=np.float32))
+    for name, m_full, n, x_dt, x, w, w_dt in (
+            ("c1_fp8_64x3072x3072", 64, 3072, O.F16, x_c1, w_c1, O.FP8),
+            ("c3_up_4096x12288x3072", mt, mlp_n, O.BF16, xf, w_up, O.FP8),
+            ("c2_bf16_qkv_4096x9216x3072", mt, 9216, O.BF16, xf, w_qkv, O.BF16)):
+        p = O.matmul_params(64, n, hidden, 0.02)
+        done, t0 = 0, time.perf_counter()
+        while done < 64 and (done == 0 or time.perf_counter() - t0 < share):
+            O.matmul_rows(p, x_dt, x, w_dt, w, done, done + 1)
+            done += 1
+        t = time.perf_counter() - t0
+        faithful[name] = {"tflops": 2 * done * n * hidden / t / 1e12,
+                          "sample": f"{done} of {m_full} rows, {t:.1f} s, extrapolated"}
+    x4 = rng.standard_normal(k4).astype(np.float16).view(np.uint16)
     t0 = time.perf_counter()
-    while rows < rows_max and (time.perf_counter() - t0) < budget_s:
-        O.matmul_rows(p, O.BF16, x, O.FP8, w, rows, rows + 1)
-        rows += 1
-    dt = time.perf_counter() - t0
-    tflops = 2.0 * rows * n * k / dt / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{rows} of {m} rows of the up-projection ({n}x{k} fp8 weights), float64 triple loop, "
-                      f"{dt:.1f} s, extrapolated"}
+    O.matmul(O.matmul_params(1, n4, k4, 1.0), O.F16, x4, O.INT4, w4, scales=s4, group=g4)
+    t = time.perf_counter() - t0
+    faithful["c4_int4_M1"] = {"us": t * 1e6, "gbs": int4_bytes(1) / t / 1e9, "sample": "full"}
+
+    head = strong["c3_mlp_step"]
+    return {"value": head["tflops"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"the benchmarked MLP step (up GEMM + GELU-tanh + down GEMM) on {rows} of {mt} token rows, "
+                      f"oracle/cpu_gemm.c, f32 accumulation, {threads} threads, AVX-512: "
+                      f"{'yes' if O.lib.cb_has_avx512() else 'no'}; extrapolated to M = {mt} "
+                      f"({head['ms_extrapolated']:.0f} ms per step)",
+            "host": host_info(), "strong": strong,
+            "faithful": dict(faithful, cores=1,
+                             note="float64 triple loop of tests/gpu/matmul.test.ts:26-35 (or_matmul_f64)"),
+            "mlp_flop_per_step": mlp_flop}
 
 
 def measured_traffic(name):

@@ -58,6 +58,13 @@ int or_matmul_params_make(uint32_t m, uint32_t n, uint32_t k, float scale, int64
                           int64_t y_stride, int64_t x_offset, int64_t w_offset, int64_t y_offset, int64_t k_split,
                           or_matmul_params* out, char* msg, size_t msg_len);
 uint32_t or_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
+
+/* ---- strong CPU baseline (cpu_gemm.c): y = scale * x . W^T (then tanh GELU when `gelu`), f32 accumulation,
+ * `threads` host threads, AVX-512 when `avx512` and the host has it; contiguous layout, y dtype F32 / F16 / BF16.
+ * 0 or -1. */
+int cb_matmul(int threads, int avx512, uint32_t m, uint32_t n, uint32_t k, float scale, int x_dtype, const void* x,
+              int w_dtype, const void* w, const uint16_t* scales, uint32_t group, int y_dtype, int gelu, void* y);
+int cb_has_avx512(void);
 uint32_t or_ksplit_chunk(uint32_t k, uint32_t k_split);
 void or_matmul_f64(const or_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                    const uint16_t* w_scales, uint32_t group, int flags, double* y);

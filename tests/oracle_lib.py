@@ -63,6 +63,9 @@ def _load():
         "or_gelu_tanh": (d, [d]), "or_gelu_tanh_shader": (f, [f]), "or_sigmoid": (d, [d]),
         "or_elementwise_f64": (None, [ctypes.c_int, sz, sz, P, P, P, P]),
         "or_rel_error": (d, [P, P, sz]), "or_compare": (None, [P, P, sz, P, P, P]),
+        "cb_matmul": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, u32, u32, u32, f, ctypes.c_int, P, ctypes.c_int, P,
+                                     P, u32, ctypes.c_int, ctypes.c_int, P]),
+        "cb_has_avx512": (ctypes.c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -170,6 +173,19 @@ def matmul_rows(p, x_dtype, x, w_dtype, w, row_begin, row_end, scales=None, grou
     y = np.zeros(p.m * p.y_stride + p.y_offset, np.float64)
     lib.or_matmul_f64_rows(ctypes.byref(p), x_dtype, ptr(x), w_dtype, ptr(w), ptr(scales), group, row_begin, row_end,
                            ptr(y))
+    return y
+
+
+def cpu_matmul(m, n, k, scale, x_dtype, x, w_dtype, w, scales=None, group=0, y_dtype=F32, threads=1, avx512=True,
+               gelu=False):
+    """The strong CPU baseline (oracle/cpu_gemm.c): f32 accumulation on `threads` host threads; contiguous
+    x [m, k], W [n, k]; tanh GELU on the result when `gelu`; returns y [m * n] as float32 (F32) or the 16-bit
+    codes (F16 / BF16)."""
+    y = np.empty(m * n, np.float32 if y_dtype == F32 else np.uint16)
+    rc = lib.cb_matmul(threads, 1 if avx512 else 0, m, n, k, scale, x_dtype, ptr(x), w_dtype, ptr(w), ptr(scales),
+                       group, y_dtype, 1 if gelu else 0, ptr(y))
+    if rc != 0:
+        raise ValueError("cb_matmul refused its arguments")
     return y
 
 
