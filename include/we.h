@@ -85,6 +85,16 @@ int we_buf_download_async(we_ctx* ctx, const void* buf, size_t offset, void* pin
 int we_mark(we_ctx* ctx, size_t* mark);                                         /* Graph.mark */
 int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep);     /* Graph.release */
 int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created_bytes); /* Graph.stats */
+/* Failure injection and debugging, additive (the reference meets these failures through WebGPU's out-of-memory
+ * error scope, src/probe/measure.ts:27-38, and hides stale data by zeroing reused buffers, src/gpu/graph.ts:48-51):
+ *  - we_set_alloc_cap: the device bytes the context may hold at once (pool buffers + kernel scratch; 0 = no cap).
+ *    An allocation past it fails as a full device does: WE_ENOMEM, and the context stays usable. `held` (may be
+ *    NULL) receives the bytes held now. Taking a buffer from the pool allocates nothing and is never refused.
+ *  - we_set_poison: on (1), we_buf_free and we_release fill each buffer they pool with 0xff bytes (NaN as f32,
+ *    bf16, f16 and e4m3) on the compute stream, after the work queued so far, so a kernel that reads a freed
+ *    buffer reads NaN instead of stale plausible values. Reused buffers are still zeroed by we_buf_alloc. */
+int we_set_alloc_cap(we_ctx* ctx, uint64_t bytes, uint64_t* held);
+int we_set_poison(we_ctx* ctx, int on);
 int we_sync(we_ctx* ctx); /* device.queue.onSubmittedWorkDone(), called from src/model/weights.ts:128 */
 
 /* Two compute streams. No counterpart in the reference, whose WebGPU queue is one ordered stream: for

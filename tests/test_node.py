@@ -47,7 +47,8 @@ EXPORTS = {
     "we_st_info": "stInfo", "we_st_find": "stFind", "we_st_metadata_count": "stMetadataCount",
     "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead", "we_stream_select": "streamSelect",
     "we_stream_fork": "streamFork", "we_stream_join": "streamJoin", "we_buf_download_async": "downloadAsync",
-    "we_ticket_wait": "waitTicketAsync", "we_record_all": "recordAll",
+    "we_ticket_wait": "waitTicketAsync", "we_record_all": "recordAll", "we_set_alloc_cap": "setAllocCap",
+    "we_set_poison": "setPoison",
 }
 
 

@@ -669,28 +669,26 @@ bool fast_supported(const GemmLaunch& L, uint32_t kc) {
 
 constexpr uint32_t kCUs = 256;
 
-// Tile shape by predicted occupancy (fp8 weights). A 256 x 256 tile (one per CU) is the fastest per FLOP when
-// its tiles fill whole waves of the 256 CUs; 128 x 128 tiles (two per CU) lose ~10% per tile but quantize 4x
-// finer (4096 x 9216 x 3072 in one process: 256 x 192 206 us, 128 x 128 225 us); 256 x 128 (one per CU) ~10%. Utilization = tiles / (waves * slots); measured on MI355X, this picks the
-// faster layout for the DiT shapes (M = 512 .. 4096, N = 3072 .. 12288, K = 3072 / 12288).
+// Tile shape by predicted speed. score = the tile shape's own speed relative to 256 x 256 (one per CU, the
+// fastest per FLOP) times util^0.3, util being the fraction of workgroup slots busy over the launch's rounds (the
+// last round of tiles is partly empty). The weak exponent is measured: the chip runs at its power limit, so a
+// partly empty last round runs at higher clocks and costs far less than a full one. Both factors come from the
+// tile sweep (bench.py --sweep; bf16 activations, fp8 weights, M = 4096 and 8740): 256 x 192 does 0.93 of
+// 256 x 256's work per unit time at equal occupancy, 128 x 128 (two per CU) 0.86, 256 x 128 0.83; 8740 x 6144 x
+// 6144 at util 0.82 still runs fastest in 256 x 256 tiles (1110 TFLOP/s against 1044 for 128 x 128 at 0.92),
+// while 4096 x 3072 x 12288 (256 x 256: one round at 0.75) goes to 256 x 192 (1191 against 1163).
+// With 16-bit weights 128 x 128 tiles fit one per CU only and lose to the ping-pong tiles
+// (4096 x 9216 x 3072 bf16: 780 against 1011 TFLOP/s), so only the two 256-row shapes compete there.
 int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
   if (m <= 32) return GEMM_CFG_32x64;
   if (m <= 64) return GEMM_CFG_64x64;
-  // score = measured efficiency of the tile shape relative to 256 x 256 at equal occupancy, times the
-  // predicted fraction of workgroup slots busy over the launch (the last round of tiles is partly
-  // empty). Measured on MI355X in one process (fp8, M = 4096, steady clocks): 256 x 192 does ~0.85 of
-  // the work per unit time of 256 x 256 (4096 x 12288 x 3072 + GELU: 274 vs 254 us, 4 rounds vs 3), and
-  // wins where it fills the CUs better (4096 x 9216 x 3072: 207 vs 229 us; 4096 x 3072 x 3072: 71 vs
-  // 73 us; 4096 x 3072 x 12288: 251 vs 252 us).
-  // With 16-bit weights 128 x 128 tiles fit one per CU only and lose to the ping-pong tiles
-  // (4096 x 9216 x 3072 bf16: 347 vs 274 us), so only the two 256-row shapes compete there.
   struct Cand {
     int cfg;
     uint32_t bm, bn, per_cu;
     double base;
   };
-  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, 0.85},
-                        {GEMM_CFG_128x128, 128, 128, 2, 0.90}, {GEMM_CFG_256x128, 256, 128, 1, 0.90}};
+  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, 0.93},
+                        {GEMM_CFG_128x128, 128, 128, 2, 0.86}, {GEMM_CFG_256x128, 256, 128, 1, 0.83}};
   int best = GEMM_CFG_128x128;
   double best_score = -1.0;
   for (const Cand& c : cands) {
@@ -699,7 +697,7 @@ int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
     const uint64_t tiles = (uint64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * splits;
     const uint64_t slots = (uint64_t)kCUs * c.per_cu;
     const uint64_t waves = (tiles + slots - 1) / slots;
-    const double score = c.base * (double)tiles / (double)(waves * slots);
+    const double score = c.base * pow((double)tiles / (double)(waves * slots), 0.3);
     if (score > best_score + 1e-9) {
       best_score = score;
       best = c.cfg;

@@ -103,6 +103,7 @@ hipError_t noalloc_scratch_init(int device);
 void* noalloc_scratch(int device);
 
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+hipError_t launch_fill(void* p, size_t bytes, uint8_t byte, hipStream_t s);
 hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
 hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
                                float* out, hipStream_t s);

@@ -13,19 +13,24 @@ static inline unsigned grid_for(size_t n, unsigned threads, unsigned cap = 1u <<
 }
 
 // ------------------------------------------------------------------ zero fill (Graph's zero shader, src/gpu/graph.ts:14-21)
-__global__ void zero_kernel(u32x4* p16, size_t n16, uint8_t* tail, size_t ntail) {
+// and the poison fill of freed buffers (every byte 0xff: NaN as f32, bf16, f16 and e4m3)
+__global__ void fill_kernel(u32x4* p16, size_t n16, uint8_t* tail, size_t ntail, uint32_t byte) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) p16[i] = u32x4{0, 0, 0, 0};
-  if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+  const uint32_t word = byte * 0x01010101u;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    p16[i] = u32x4{word, word, word, word};
+  if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = (uint8_t)byte;
 }
 
-hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+hipError_t launch_fill(void* p, size_t bytes, uint8_t byte, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
   const size_t n16 = bytes / 16, tail = bytes % 16;
-  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n16 ? n16 : 1, 256, 4096)), dim3(256), 0, s, (u32x4*)p, n16,
-                     (uint8_t*)p + n16 * 16, tail);
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n16 ? n16 : 1, 256, 4096)), dim3(256), 0, s, (u32x4*)p, n16,
+                     (uint8_t*)p + n16 * 16, tail, (uint32_t)byte);
   return hipGetLastError();
 }
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) { return launch_fill(p, bytes, 0, s); }
 
 // ------------------------------------------------------------------ unpackFp8 (src/kernels/fp8.ts:24-36)
 __global__ void unpack_fp8_kernel(const uint8_t* packed, size_t n, const float* scale, float* out) {

@@ -57,6 +57,11 @@ struct we_ctx {
   std::map<void*, int> scratch_refs;
   std::vector<void*> retired;
   hipError_t noalloc_status = hipErrorNotInitialized;  // the device's allocation-free scratch lookup
+  // failure injection: device bytes the context may hold (pool + scratch; 0 = no cap) and the bytes it holds;
+  // poison: freed buffers are filled with 0xff bytes (NaN in every float format) on the compute stream
+  size_t alloc_cap = 0, held_bytes = 0;
+  bool poison = false;
+  std::map<void*, size_t> scratch_sizes;  // bytes of every scratch block (current, other lane's, retired)
 };
 
 namespace {
@@ -93,6 +98,23 @@ int hip_fail(we_ctx* ctx, hipError_t e, const char* what) {
     if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
   } while (0)
 
+// hipMalloc under the context's allocation cap (we_set_alloc_cap): a cap reached fails like a full device
+hipError_t capped_malloc(we_ctx* ctx, void** p, size_t bytes) {
+  if (ctx->alloc_cap && ctx->held_bytes + bytes > ctx->alloc_cap) return hipErrorOutOfMemory;
+  const hipError_t e = hipMalloc(p, bytes);
+  if (e == hipSuccess) ctx->held_bytes += bytes;
+  return e;
+}
+
+hipError_t scratch_free(we_ctx* ctx, void* p) {
+  auto it = ctx->scratch_sizes.find(p);
+  if (it != ctx->scratch_sizes.end()) {
+    ctx->held_bytes -= it->second < ctx->held_bytes ? it->second : ctx->held_bytes;
+    ctx->scratch_sizes.erase(it);
+  }
+  return hipFree(p);
+}
+
 // Scratch for kernels of this context (split-K partial sums, attention V^T), at least `bytes`. Calls are ordered on the
 // compute stream, so one buffer serves them all; growing it waits for the work that may still read it.
 int ensure_scratch(we_ctx* ctx, size_t bytes) {
@@ -106,15 +128,17 @@ int ensure_scratch(we_ctx* ctx, size_t bytes) {
       ctx->retired.push_back(ctx->scratch);  // a live graph replays into it: keep it until that graph goes
     } else {
       HIP_OK(ctx, hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
-      HIP_OK(ctx, hipFree(ctx->scratch), "hipFree scratch");
+      HIP_OK(ctx, scratch_free(ctx, ctx->scratch), "hipFree scratch");
     }
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;
   }
   const size_t want = ((bytes < (16u << 20) ? (16u << 20) : bytes) + 4095) / 4096 * 4096;
   void* p = nullptr;
-  const hipError_t e = hipMalloc(&p, want);
-  if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
+  const hipError_t e = capped_malloc(ctx, &p, want);
+  if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "scratch of %zu bytes: %s%s", want, hipGetErrorString(e),
+                                   ctx->alloc_cap ? " (allocation cap set)" : "");
+  ctx->scratch_sizes[p] = want;
   ctx->scratch = p;
   ctx->scratch_bytes = want;
   return WE_OK;
@@ -261,8 +285,10 @@ int we_buf_alloc(we_ctx* ctx, size_t bytes, void** out) {
     ctx->allocs[(uintptr_t)p].req = req;
     ctx->reused++;
   } else {
-    hipError_t e = hipMalloc(&p, size);
-    if (e != hipSuccess) return fail(ctx, WE_ENOMEM, "hipMalloc(%zu): %s", size, hipGetErrorString(e));
+    hipError_t e = capped_malloc(ctx, &p, size);
+    if (e != hipSuccess)
+      return fail(ctx, WE_ENOMEM, "hipMalloc(%zu): %s%s", size, hipGetErrorString(e),
+                  ctx->alloc_cap ? " (allocation cap set)" : "");
     ctx->allocs[(uintptr_t)p] = Alloc{size, req};
     ctx->created++;
     ctx->created_bytes += size;
@@ -282,6 +308,11 @@ int we_buf_free(we_ctx* ctx, void* buf) {
   if (it == ctx->allocs.end()) return fail(ctx, WE_EINVAL, "we_buf_free: not a buffer of this context");
   for (size_t i = 0; i < ctx->owned.size(); i++)
     if (ctx->owned[i] == buf) {
+      if (ctx->poison) {
+        HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+        const hipError_t e = we::launch_fill(buf, it->second.size, 0xff, ctx->compute);
+        if (e != hipSuccess) return hip_fail(ctx, e, "poison fill");
+      }
       ctx->owned.erase(ctx->owned.begin() + (long)i);
       ctx->pool[it->second.size].push_back(buf);
       return WE_OK;
@@ -369,14 +400,34 @@ int we_release(we_ctx* ctx, size_t mark, void* const* keep, size_t n_keep) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
   if (mark > ctx->owned.size()) return fail(ctx, WE_EINVAL, "mark %zu is past the %zu live buffers", mark, ctx->owned.size());
+  if (ctx->poison) HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   std::vector<void*> later(ctx->owned.begin() + (long)mark, ctx->owned.end());
   ctx->owned.resize(mark);
+  hipError_t e = hipSuccess;
   for (void* b : later) {
     bool kept = false;
     for (size_t i = 0; i < n_keep && !kept; i++) kept = keep[i] == b;
-    if (kept) ctx->owned.push_back(b);
-    else ctx->pool[ctx->allocs[(uintptr_t)b].size].push_back(b);
+    if (kept) {
+      ctx->owned.push_back(b);
+      continue;
+    }
+    const size_t size = ctx->allocs[(uintptr_t)b].size;
+    if (ctx->poison && e == hipSuccess) e = we::launch_fill(b, size, 0xff, ctx->compute);
+    ctx->pool[size].push_back(b);
   }
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "poison fill");
+}
+
+int we_set_alloc_cap(we_ctx* ctx, uint64_t bytes, uint64_t* held) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  ctx->alloc_cap = (size_t)bytes;
+  if (held) *held = ctx->held_bytes;
+  return WE_OK;
+}
+
+int we_set_poison(we_ctx* ctx, int on) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  ctx->poison = on != 0;
   return WE_OK;
 }
 
@@ -592,7 +643,7 @@ int we_graph_destroy(we_ctx* ctx, we_graph* graph) {
       ctx->scratch_refs.erase(held);
       for (size_t i = 0; i < ctx->retired.size(); i++)
         if (ctx->retired[i] == graph->scratch) {  // outgrown meanwhile and no graph left on it
-          (void)hipFree(graph->scratch);
+          (void)scratch_free(ctx, graph->scratch);
           ctx->retired.erase(ctx->retired.begin() + (long)i);
           break;
         }

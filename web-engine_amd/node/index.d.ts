@@ -92,6 +92,10 @@ export class Graph {
   free(buffer: Buffer): void;
   /** src/gpu/graph.ts:32 */
   readonly stats: { created: number; reused: number; createdBytes: number };
+  /** Failure injection: device allocations past `bytes` held (0 = no cap) throw; returns the bytes held now. */
+  setAllocCap(bytes: number): number;
+  /** Debugging: freed and released buffers are filled with NaN bytes once pooled. */
+  setPoison(on: boolean): void;
   /** Every read() and onSubmittedWorkDone() promise must have settled first. */
   destroy(): void;
   sync(): void;

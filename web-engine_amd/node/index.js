@@ -238,6 +238,16 @@ class Graph {
     addon.bufFree(this.ctx, buffer.ptr);
   }
 
+  /** Failure injection: device allocations past `bytes` held (0 = no cap) throw as a full device does. */
+  setAllocCap(bytes) {
+    return addon.setAllocCap(this.ctx, bytes);
+  }
+
+  /** Debugging: freed and released buffers are filled with NaN bytes once pooled. */
+  setPoison(on) {
+    addon.setPoison(this.ctx, on ? 1 : 0);
+  }
+
   /** src/gpu/graph.ts:32: buffers created vs taken from the pool, and bytes created. */
   get stats() {
     return addon.stats(this.ctx);

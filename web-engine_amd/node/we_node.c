@@ -338,6 +338,28 @@ static napi_value Stats(napi_env env, napi_callback_info info) {
 }
 
 /* ---- pinned host memory and streaming ---- */
+/* setAllocCap(ctx, bytes) -> bytes held now; setPoison(ctx, on) */
+static napi_value SetAllocCap(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  double bytes = f64_arg(&a, 1);
+  if (a.bad) return NULL;
+  uint64_t held = 0;
+  int rc = we_set_alloc_cap(ctx, (uint64_t)bytes, &held);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)held);
+}
+
+static napi_value SetPoison(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  int32_t on = i32_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_set_poison(ctx, on));
+}
+
 static napi_value HostAlloc(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 2)) return NULL;
@@ -1044,6 +1066,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
+      {"setAllocCap", SetAllocCap}, {"setPoison", SetPoison},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},

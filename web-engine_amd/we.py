@@ -83,6 +83,8 @@ SIGNATURES = {
     "we_buf_download_async": (_I, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint64)]),
     "we_ticket_wait": (_I, [_P, ctypes.c_uint64]),
     "we_record_all": (_I, [_P, _P]),
+    "we_set_alloc_cap": (_I, [_P, _U64, _P]),
+    "we_set_poison": (_I, [_P, ctypes.c_int]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
     "we_wait_ticket": (_I, [_P, _U64]),
     "we_record_compute": (_I, [_P, _P]),
@@ -275,6 +277,17 @@ class Graph:
         self.destroy()
 
     # ---- pinned host memory and streaming
+    def set_alloc_cap(self, nbytes):
+        """Failure injection: allocations past `nbytes` device bytes held (0 = no cap) fail with WE_ENOMEM.
+        Returns the bytes the context holds now."""
+        held = ctypes.c_uint64()
+        self.check(self.lib.we_set_alloc_cap(self.ctx, nbytes, ctypes.byref(held)))
+        return held.value
+
+    def set_poison(self, on):
+        """Debugging: freed / released buffers are filled with 0xff bytes (NaN) once pooled."""
+        self.check(self.lib.we_set_poison(self.ctx, 1 if on else 0))
+
     def host_alloc(self, nbytes):
         p = ctypes.c_void_p()
         self.check(self.lib.we_host_alloc(self.ctx, nbytes, ctypes.byref(p)))
