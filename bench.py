@@ -167,6 +167,68 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20):
     return {"us": ms * 1e3, "tflops": flop / ms / 1e9}
 
 
+# Tile configurations of the fast GEMM (WE_GEMM_CFG values) and the shapes the sweep times them on: the
+# benchmarked DiT shapes (M = 4096 image tokens, the M = 512 text stream) and the reference tuner's own shapes
+# (src/bench/tune.ts:5-9, 1928x1088 at 8740 tokens), all with fp8 weights unless named.
+SWEEP_CFGS = {0: "256x256", 1: "256x128", 2: "128x128", 3: "64x64", 4: "32x64", 5: "256x192"}
+SWEEP_SHAPES = [
+    ("C3 up + GELU", 4096, 12288, 3072, we.FP8, we.EPI_GELU),
+    ("C3 down", 4096, 3072, 12288, we.FP8, 0),
+    ("C2 QKV, bf16 weights", 4096, 9216, 3072, we.BF16, 0),
+    ("text QKV (M = 512)", 512, 9216, 3072, we.FP8, 0),
+    ("text down (M = 512)", 512, 3072, 12288, we.FP8, 0),
+    ("C1 (M = 64)", 64, 3072, 3072, we.FP8, 0),
+    ("tune: q / gate / out", 8740, 6144, 6144, we.FP8, 0),
+    ("tune: mlp gate / up", 8740, 16384, 6144, we.FP8, 0),
+    ("tune: mlp down", 8740, 6144, 16384, we.FP8, 0),
+]
+
+
+def sweep_tiles(g, rng, iters=10):
+    """The tile sweep behind the fast GEMM's tile pick (the role of tuneMatmul, src/bench/tune.ts:14-30): every
+    tile configuration on every sweep shape, bf16 activations and output, TFLOP/s from HIP events. Each shape is
+    warmed up first and the configurations are timed twice, in opposite orders, keeping the faster run, so no
+    configuration is measured on cold clocks. "auto" is the library's own pick (WE_GEMM_CFG unset)."""
+    import os
+    rows = []
+    for name, m, n, k, w_dt, flags in SWEEP_SHAPES:
+        x = g.buffer(bf16_bits(rng.standard_normal(m * k, dtype=np.float32)))
+        w = g.buffer(fp8_finite_codes(rng, n * k) if w_dt == we.FP8 else
+                     bf16_bits(rng.normal(0, 0.02, n * k).astype(np.float32)))
+        y = g.buffer(m * n * 2)
+        p = we.matmul_params(m, n, k, 0.02, graph=g)
+        flop = 2.0 * m * n * k
+
+        def run(_=0):
+            g.matmul(p, we.BF16, x, w_dt, w, we.BF16, y, flags=flags)
+
+        best = {}
+        order = ["auto"] + list(SWEEP_CFGS)
+        for _ in range(3):
+            run()
+        for sweep_pass in (order, order[::-1]):
+            for cfg in sweep_pass:
+                if cfg == "auto":
+                    os.environ.pop("WE_GEMM_CFG", None)
+                else:
+                    os.environ["WE_GEMM_CFG"] = str(cfg)
+                run()
+                reps = iters if m <= 512 or cfg not in (3, 4) else 2
+                ms = time_graph(g, run, 10, 1) if m <= 64 else time_launches(g, run, reps)
+                best[cfg] = min(best.get(cfg, float("inf")), ms)
+        os.environ.pop("WE_GEMM_CFG", None)
+        tflops = {("auto" if c == "auto" else SWEEP_CFGS[c]): flop / ms / 1e9 for c, ms in best.items()}
+        top = max(v for c, v in tflops.items() if c != "auto")
+        rows.append({"shape": name, "m": m, "n": n, "k": k, "weights": "fp8" if w_dt == we.FP8 else "bf16",
+                     "gelu": bool(flags), "tflops": tflops,
+                     "best": max((c for c in tflops if c != "auto"), key=tflops.get),
+                     "auto_frac_of_best": tflops["auto"] / top})
+        print(f"[sweep] {name}: " + ", ".join(f"{c} {v:.0f}" for c, v in tflops.items()), file=sys.stderr, flush=True)
+        for b in (x, w, y):
+            g.free(b)
+    return rows
+
+
 def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
     """The double-stream DiT block (512 text + 4096 image tokens, hidden 3072, 24 heads of 128, MLP 12288, fp8
     weights, bf16 activations): resident (weights already in HBM), the weight copies alone, and `layers`
@@ -434,6 +496,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["mlp", "int4", "block", "all"], default="all")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time every GEMM tile configuration on the sweep shapes and print that table instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the library has no multi-GPU "
@@ -444,6 +508,10 @@ def main():
     g = we.Graph(0)
     info = g.device_info()
     print(f"[bench] device {info}", file=sys.stderr, flush=True)
+    if args.sweep:
+        print(json.dumps({"sweep": sweep_tiles(g, rng), "device": info}), flush=True)
+        g.destroy()
+        return
     mlp = bench_mlp(g, args.steps, args.warmup, rng) if args.only in ("mlp", "all") else None
     print("[bench] mlp done", file=sys.stderr, flush=True)
     int4 = bench_int4(g, rng) if args.only in ("int4", "all") else None
