@@ -187,6 +187,21 @@ int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const v
                     const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
                     const float* gate, const void* residual);
 
+/* we_matmul with the elementwise step that consumes its output fused into the epilogue, as a product with a second
+ * operand `aux` of y's dtype and layout (y_offset, y_stride; aux may be y itself):
+ *   WE_MUL_SWIGLU:       y = silu(aux) * v, swiglu(gate, up) (src/kernels/elementwise.ts:38-43) with this GEMM as
+ *                        `up` and the gate projection's output as aux (the MLP of src/model/block.ts:74-81);
+ *   WE_MUL_SIGMOID_GATE: y = aux * sigmoid(v), sigmoidGate(a, gate) (elementwise.ts:45-50) with this GEMM as `gate`
+ *                        and the attention output as aux (src/model/block.ts:60-62).
+ * v is the value we_matmul would store (scale, then bias with WE_EPI_BIAS); other flags are refused, and int4
+ * weights give WE_EUNSUPPORTED. v is not rounded to y's dtype before the product (the unfused pair rounds it
+ * once more). No reference entry point: the reference runs these steps as their own passes. */
+#define WE_MUL_SWIGLU 1
+#define WE_MUL_SIGMOID_GATE 2
+int we_matmul_mul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                  const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags, int mul,
+                  const void* aux);
+
 /* ---- norms and rotary: rmsnormWgsl (src/kernels/rmsnorm.ts:13-48) / norm() (src/model/ops.ts:78-82),
  * ropeKernel (src/kernels/rope.ts:59-77) / rotate() (src/model/ops.ts:89-93) ---- */
 /* out = x / sqrt(mean(x^2) + eps) * (offset + weight) * (1 + scale) + shift; scale/shift may be NULL */

@@ -559,3 +559,82 @@ def test_gated_residual_refusals(graph):
         graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, flags=we.EPI_SPLIT_K, gate=b)
     with pytest.raises(we.WeError, match="residual replaces accumulate"):
         graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, flags=we.EPI_ACCUMULATE, gate=b, residual=b)
+
+
+def _sigmoid(v):
+    with np.errstate(over="ignore"):  # exp(-v) -> inf for very negative v: sigmoid -> 0, its limit
+        return 1.0 / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize("mul", [we.MUL_SWIGLU, we.MUL_SIGMOID_GATE])
+@pytest.mark.parametrize("case", ["fast_full", "fast_ragged", "small_m_split", "generic_f32", "f16_out", "bias"])
+def test_product_epilogue_equals_gemm_then_the_elementwise_step(graph, case, mul, monkeypatch):
+    """y = silu(aux) * v (swiglu with the GEMM as `up`) or aux * sigmoid(v) (sigmoidGate with the GEMM as `gate`),
+    v the scaled (biased) product, against the f64 oracle of the product followed by the reference's formula
+    (src/kernels/elementwise.ts:38-50), on every epilogue: the fast kernel's whole-tile and per-value paths, the
+    split-K reduce pass (small M), the general kernel (f32 operands) and f16 output."""
+    shapes = {"fast_full": (512, 384, 256, we.BF16, we.FP8, we.BF16), "fast_ragged": (300, 520, 208, we.BF16, we.FP8, we.BF16),
+              "small_m_split": (48, 3072, 3072, we.F16, we.FP8, we.F16), "generic_f32": (70, 90, 128, we.F32, we.F32, we.F32),
+              "f16_out": (256, 256, 192, we.F16, we.F16, we.F16), "bias": (512, 384, 256, we.BF16, we.FP8, we.F32)}
+    m, n, k, x_dt, w_dt, y_dt = shapes[case]
+    rng = np.random.default_rng(len(case) + 10 * mul)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    scale = 0.05 if w_dt == we.FP8 else 1.0
+    bias = rng.uniform(-.5, .5, n).astype(np.float32) if case == "bias" else None
+    aux_store, aux_vals = _store(rng.standard_normal(m * n) * 2, y_dt)
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    mark = graph.mark()
+    xb, wb, ab = graph.buffer(x_store), graph.buffer(w_store), graph.buffer(aux_store)
+    yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
+    bb = graph.buffer(bias) if bias is not None else None
+    if case == "generic_f32":
+        monkeypatch.setenv("WE_GEMM_PATH", "generic")
+    graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=we.EPI_BIAS if bias is not None else 0, mul=mul, aux=ab)
+    got = decode(graph.read(yb), y_dt)
+    graph.release(mark)
+    v = O.matmul(O.matmul_params(m, n, k, scale), ox, x_oracle, ow, w_oracle)
+    if bias is not None:
+        v = v + np.tile(bias.astype(np.float64), m)
+    want = aux_vals * _sigmoid(aux_vals) * v if mul == we.MUL_SWIGLU else aux_vals * _sigmoid(v)
+    assert O.rel_error(got, want) < TOL[y_dt], (case, mul)
+
+
+@pytest.mark.parametrize("mul", [we.MUL_SWIGLU, we.MUL_SIGMOID_GATE])
+def test_product_epilogue_in_place_and_against_the_unfused_pair(graph, mul):
+    """aux = y (the block writes the product over the gate / attention output) gives the same bits as a separate
+    aux buffer; with f32 output the fused result equals linear + the elementwise kernel to f32 rounding."""
+    m, n, k = 512, 384, 256
+    rng = np.random.default_rng(20 + mul)
+    x = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
+    w, _, _ = make_weights(rng, n, k, we.FP8)
+    aux = rng.standard_normal(m * n).astype(np.float32) * 2
+    p = we.matmul_params(m, n, k, 0.05, graph=graph)
+    mark = graph.mark()
+    xb, wb = graph.buffer(x), graph.buffer(w)
+    sep, inplace, v, pair = graph.buffer(m * n * 4), graph.buffer(aux), graph.buffer(m * n * 4), graph.buffer(m * n * 4)
+    ab = graph.buffer(aux)
+    graph.matmul(p, we.BF16, xb, we.FP8, wb, we.F32, sep, mul=mul, aux=ab)
+    graph.matmul(p, we.BF16, xb, we.FP8, wb, we.F32, inplace, mul=mul, aux=inplace)
+    graph.matmul(p, we.BF16, xb, we.FP8, wb, we.F32, v)
+    op = we.OP_SWIGLU if mul == we.MUL_SWIGLU else we.OP_SIGMOID_GATE
+    graph.elementwise(op, m * n, 1, we.F32, ab, v, None, pair)
+    a, b, c = (graph.read(t, dtype=np.float32).astype(np.float64) for t in (sep, inplace, pair))
+    graph.release(mark)
+    assert np.array_equal(a, b)
+    assert O.rel_error(a, c) < 1e-6
+
+
+def test_product_epilogue_refusals(graph):
+    p = we.matmul_params(4, 4, 4, 1.0, graph=graph)
+    b = graph.buffer(64)
+    with pytest.raises(we.WeError, match="aux is null"):
+        graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, mul=we.MUL_SWIGLU, aux=None)
+    with pytest.raises(we.WeError, match="unknown product epilogue 3"):
+        graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, mul=3, aux=b)
+    for flags in (we.EPI_GELU, we.EPI_ACCUMULATE, we.EPI_SPLIT_K):
+        with pytest.raises(we.WeError, match="takes only WE_EPI_BIAS"):
+            graph.matmul(p, we.F32, b, we.F32, b, we.F32, b, flags=flags, mul=we.MUL_SIGMOID_GATE, aux=b)
+    with pytest.raises(we.WeError, match="int4 weights have no product epilogue") as e:
+        graph.matmul(p, we.F16, b, we.INT4, b, we.F32, b, scales=b, group=64, mul=we.MUL_SWIGLU, aux=b)
+    assert e.value.code == 4

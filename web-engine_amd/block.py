@@ -3,7 +3,8 @@
 - `positions`, `rope_tables`: src/kernels/rope.ts:14-36 (host-side, f64 angles stored as f32).
 - `block`: the Krea single-stream block of src/model/block.ts:91-105 (attend :40-65, mlp :74-81, modulation
   :33-37), step for step through the operator API of we.py, freeing each temporary after its last use; the
-  sigmoid gate and SwiGLU write over their first input instead of a new buffer.
+  sigmoid gate runs in the gate projection's epilogue and SwiGLU in the up projection's, each writing over its
+  first input instead of a new buffer.
 - `DoubleBlock`: the double-stream DiT block (text and image streams with their own weights, one joint
   attention), built from the same steps with a persistent workspace so a forward allocates nothing:
     mod_s = tvec + table_s;  h_s = norm1_s(x_s) * (1 + prescale_s) + preshift_s
@@ -98,18 +99,16 @@ def _attend(graph, w, cfg, h, rows, rope, dtype):
     o = we.attention(graph, q, k, v, we.AttentionShape(rows, cfg.heads, cfg.kv_heads, cfg.head_dim), dtype)
     for b in (q, k, v):
         graph.free(b)
-    g = we.linear(graph, h, w.gate, rows, x_dtype=dtype, y_dtype=dtype)
-    graph.elementwise(we.OP_SIGMOID_GATE, rows * cfg.hidden, 1, dtype, o, g, None, o)  # o * sigmoid(g), in place
-    graph.free(g)
+    # o * sigmoid(h . gate^T): the sigmoid gate in the gate projection's epilogue, written over o
+    we.linear(graph, h, w.gate, rows, x_dtype=dtype, y_dtype=dtype, sigmoid_gate_of=o, out=o)
     return _used(graph, o, lambda y: we.linear(graph, y, w.wo, rows, x_dtype=dtype, y_dtype=dtype))
 
 
 def _mlp(graph, w, cfg, h, rows, dtype):
     """src/model/block.ts:74-81"""
     gate = we.linear(graph, h, w.mlp_gate, rows, x_dtype=dtype, y_dtype=dtype)
-    up = we.linear(graph, h, w.mlp_up, rows, x_dtype=dtype, y_dtype=dtype)
-    graph.elementwise(we.OP_SWIGLU, rows * cfg.mlp, 1, dtype, gate, up, None, gate)  # silu(gate) * up, in place
-    graph.free(up)
+    # silu(gate) * (h . up^T): swiglu in the up projection's epilogue, written over gate
+    we.linear(graph, h, w.mlp_up, rows, x_dtype=dtype, y_dtype=dtype, swiglu_gate=gate, out=gate)
     return _used(graph, gate, lambda y: we.linear(graph, y, w.mlp_down, rows, x_dtype=dtype, y_dtype=dtype))
 
 

@@ -143,6 +143,13 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 __device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + __expf(-v)); }
 
+// The product epilogues (GemmLaunch::mul): 1 swiglu (src/kernels/elementwise.ts:38-43) with the GEMM value as
+// `up` and aux as `gate`: (aux * sigmoid(aux)) * v; 2 sigmoidGate (:45-50) with the GEMM value as `gate`:
+// aux * sigmoid(v).
+__device__ __forceinline__ float mul_epilogue(uint32_t mul, float aux, float v) {
+  return mul == 1u ? aux * sigmoid(aux) * v : aux * sigmoid(v);
+}
+
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
 // 16-byte direct-to-LDS buffer load issued as inline asm: lane i writes dst + 16 i. The compiler does not

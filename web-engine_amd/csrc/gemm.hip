@@ -36,6 +36,7 @@ struct GemmArgs {
   uint32_t flags;
   uint32_t y_dtype;
   uint32_t aligned;   // 1: every 16-B chunk of x / W rows is 16-B aligned
+  uint32_t mul;       // product epilogue with res (GemmLaunch::mul), 0: none
 };
 
 // Planes per operand: 1 when the stored type is exact in the MFMA type; f16 under a bf16 MFMA needs
@@ -142,9 +143,16 @@ __device__ __forceinline__ void load_chunk(const void* base, size_t row_off, boo
   }
 }
 
-// One output value: y = val, y += val (accumulate) or y = res + val (gated residual), in the output dtype.
+// One output value: y = val, y += val (accumulate), y = res + val (gated residual) or the product epilogue with
+// res, in the output dtype.
 __device__ __forceinline__ void store_out(const GemmArgs& a, size_t o, float val) {
-  const void* add = a.res ? a.res : ((a.flags & WE_EPI_ACCUMULATE_BIT) ? a.y : nullptr);
+  if (a.mul) {
+    const float aux = a.y_dtype == F32    ? ((const float*)a.res)[o]
+                      : a.y_dtype == BF16 ? bf16_to_f32(((const uint16_t*)a.res)[o])
+                                          : f16_to_f32(((const uint16_t*)a.res)[o]);
+    val = mul_epilogue(a.mul, aux, val);
+  }
+  const void* add = a.mul ? nullptr : a.res ? a.res : ((a.flags & WE_EPI_ACCUMULATE_BIT) ? a.y : nullptr);
   if (a.y_dtype == F32) {
     ((float*)a.y)[o] = add ? ((const float*)add)[o] + val : val;
   } else if (a.y_dtype == BF16) {
@@ -442,6 +450,7 @@ hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream) {
   a.y_offset = L.y_offset;
   a.flags = L.flags;
   a.y_dtype = (uint32_t)L.y_dtype;
+  a.mul = (uint32_t)L.mul;
   const uint32_t splits = L.splits < 1 ? 1 : L.splits;
   a.kc = splits > 1 ? L.kc : L.k;
   const int xb = L.x_dtype == F32 ? 4 : 2;

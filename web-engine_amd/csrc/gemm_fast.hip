@@ -56,6 +56,7 @@ struct FastArgs {
   // splitk_reduce_kernel adds the slices and runs the epilogue
   float* part;
   uint32_t rsplits;
+  uint32_t mul;  // product epilogue with res (GemmLaunch::mul), 0: none
 };
 
 __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
@@ -111,6 +112,14 @@ __device__ __forceinline__ void store4(const FastArgs& a, size_t o, const float 
     const std::integral_constant<bool, YT == F16> tag;
     *p = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
   }
+}
+
+// one value of a y-typed operand (the product epilogue's aux) as f32
+template <int YT>
+__device__ __forceinline__ float load1(const void* p, size_t o) {
+  if constexpr (YT == F32) return ((const float*)p)[o];
+  else if constexpr (YT == BF16) return bf16_to_f32(((const uint16_t*)p)[o]);
+  else return f16_to_f32(((const uint16_t*)p)[o]);
 }
 
 template <int YT>
@@ -452,16 +461,20 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
   const size_t zrow = (a.flags & WE_EPI_SPLIT_K_BIT) ? (size_t)z * a.m : 0;  // the reference's partial rows
-  const void* addend = a.res ? a.res : (accum ? a.y : nullptr);
+  const void* aux = a.mul ? a.res : nullptr;  // the product epilogue's second operand
+  const void* addend = a.mul ? nullptr : a.res ? a.res : (accum ? a.y : nullptr);
   // Fast path (uniform branch): the wave's whole sub-tile lies inside y, 4-value stores are allowed, and
-  // there is no bias; either plain stores or the gated residual (gate and addend both present): per row
-  // one base pointer, stores at constant offsets from it, GELU and gating chosen outside the loops (the
-  // general path below computes every case per value).
+  // there is no bias; plain stores, the gated residual (gate and addend both present) or a product epilogue:
+  // per row one base pointer, stores at constant offsets from it, GELU, gating and the product chosen outside
+  // the loops (the general path below computes every case per value).
   const uint32_t wrow0 = row0 + wm * WTM, wcol0 = col0 + wn * WTN;
-  const bool plain = !addend && !a.gate, gated = addend && a.gate;
-  if (a.vec_store && !has_bias && (plain || gated) && wrow0 + WTM <= a.m && wcol0 + WTN <= a.n) {
-    auto fast = [&](auto GELU, auto GATED) {
-      constexpr bool GT = decltype(GATED)::value;
+  const bool plain = !addend && !a.gate && !aux, gated = addend && a.gate;
+  if (a.vec_store && !has_bias && (plain || gated || aux) && wrow0 + WTM <= a.m && wcol0 + WTN <= a.n) {
+    // MODE 0 plain, 1 gated residual, 2 swiglu product, 3 sigmoidGate product
+    auto fast = [&](auto GELU, auto MODE) {
+      constexpr int MD = decltype(MODE)::value;
+      constexpr bool GT = MD == 1;
+      const void* other = MD == 1 ? addend : aux;  // the operand read beside the accumulators
       f32x4 gv[TN][4];  // the lane's gate values, the same for every row
       if constexpr (GT) {
 #pragma unroll
@@ -474,7 +487,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         const size_t yrow = (size_t)a.y_offset + (zrow + wrow0 + i * 32 + l32) * (size_t)a.y_stride + wcol0 + 4 * h;
         if constexpr (YT == F32) {
           float* p = (float*)a.y + yrow;
-          const float* r0 = GT ? (const float*)addend + yrow : nullptr;
+          const float* r0 = MD ? (const float*)other + yrow : nullptr;
 #pragma unroll
           for (int j = 0; j < TN; j++)
 #pragma unroll
@@ -486,11 +499,16 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
                 r[e] = decltype(GELU)::value ? gelu_tanh(t) : t;
               }
               if constexpr (GT) r = *(const f32x4*)(r0 + j * 32 + 8 * q) + gv[j][q] * r;
+              if constexpr (MD >= 2) {
+                const f32x4 ax = *(const f32x4*)(r0 + j * 32 + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 4; e++) r[e] = mul_epilogue(MD - 1, ax[e], r[e]);
+              }
               *(f32x4*)(p + j * 32 + 8 * q) = r;
             }
         } else {
           uint16_t* p = (uint16_t*)a.y + yrow;
-          const uint16_t* r0 = GT ? (const uint16_t*)addend + yrow : nullptr;
+          const uint16_t* r0 = MD ? (const uint16_t*)other + yrow : nullptr;
           const std::integral_constant<bool, YT == F16> tag;
 #pragma unroll
           for (int j = 0; j < TN; j++)
@@ -498,14 +516,15 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
             for (int q = 0; q < 4; q++) {
               float t[4];
               u32x2 old = {0u, 0u};
-              if constexpr (GT) old = *(const u32x2*)(r0 + j * 32 + 8 * q);
+              if constexpr (MD != 0) old = *(const u32x2*)(r0 + j * 32 + 8 * q);
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 t[e] = acc[i][j][4 * q + e] * a.scale;
                 if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
-                if constexpr (GT) {
+                if constexpr (MD != 0) {
                   const uint32_t hb = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
-                  t[e] = (YT == BF16 ? bf16_to_f32((uint16_t)hb) : f16_to_f32((uint16_t)hb)) + gv[j][q][e] * t[e];
+                  const float o = YT == BF16 ? bf16_to_f32((uint16_t)hb) : f16_to_f32((uint16_t)hb);
+                  t[e] = GT ? o + gv[j][q][e] * t[e] : mul_epilogue(MD - 1, o, t[e]);
                 }
               }
               *(u32x2*)(p + j * 32 + 8 * q) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
@@ -513,12 +532,17 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         }
       }
     };
-    if (gated) {
-      if (gelu) fast(std::true_type{}, std::true_type{});
-      else fast(std::false_type{}, std::true_type{});
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    if (aux) {  // the runtime refuses GELU with a product epilogue
+      if (a.mul == 1u) fast(std::false_type{}, std::integral_constant<int, 2>{});
+      else fast(std::false_type{}, std::integral_constant<int, 3>{});
+    } else if (gated) {
+      if (gelu) fast(std::true_type{}, I1{});
+      else fast(std::false_type{}, I1{});
     } else {
-      if (gelu) fast(std::true_type{}, std::false_type{});
-      else fast(std::false_type{}, std::false_type{});
+      if (gelu) fast(std::true_type{}, I0{});
+      else fast(std::false_type{}, I0{});
     }
     return;
   }
@@ -539,6 +563,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
           if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
           if (gelu) t = gelu_tanh(t);
           if (a.gate) t *= a.gate[c0 + e < a.n ? c0 + e : 0];
+          if (aux && c0 + e < a.n) t = mul_epilogue(a.mul, load1<YT>(aux, yrow + c0 + e), t);
           v[e] = t;
         }
         if (a.vec_store && c0 + 3 < a.n) {
@@ -587,16 +612,18 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
   const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
-  const void* addend = a.res ? a.res : (accum ? a.y : nullptr);
+  const void* aux = a.mul ? a.res : nullptr;
+  const void* addend = a.mul ? nullptr : a.res ? a.res : (accum ? a.y : nullptr);
+  const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     float t = v[e] * a.scale;
     if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
     if (gelu) t = gelu_tanh(t);
     if (a.gate) t *= a.gate[c0 + e < a.n ? c0 + e : 0];
+    if (aux && c0 + e < a.n) t = mul_epilogue(a.mul, load1<YT>(aux, yrow + c0 + e), t);
     v[e] = t;
   }
-  const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride;
   if (a.vec_store && full) {
     store4<YT>(a, yrow + c0, v, addend);
   } else {
@@ -764,6 +791,7 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.bias = L.bias;
   a.gate = L.gate;
   a.res = L.res;
+  a.mul = (uint32_t)L.mul;
   a.x_bytes = L.k ? (uint32_t)(((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2) : 0;
   a.w_bytes = L.k ? (uint32_t)(((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb) : 0;
   a.m = L.m;

@@ -30,6 +30,10 @@ struct GemmLaunch {
   // gate * v under ACCUMULATE).
   const float* gate;
   const void* res;
+  // product with a second operand of y's type and layout (res names it; gate NULL, no accumulate):
+  // 0 none, 1: y = silu(res) * v (swiglu with this GEMM as `up`), 2: y = res * sigmoid(v) (sigmoidGate with this
+  // GEMM as `gate`); v the value after scale and bias
+  int mul;
   int x_dtype, w_dtype, y_dtype;
   uint32_t m, n, k;
   float scale;

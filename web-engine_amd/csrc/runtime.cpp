@@ -697,7 +697,7 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
 namespace {
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res, bool noalloc = false);
+                const float* gate, const void* res, bool noalloc = false, int mul = 0);
 }  // namespace
 
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
@@ -724,10 +724,23 @@ int we_matmul_gated(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const v
   return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, gate, residual);
 }
 
+int we_matmul_mul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                  const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags, int mul,
+                  const void* aux) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (mul != WE_MUL_SWIGLU && mul != WE_MUL_SIGMOID_GATE) return fail(ctx, WE_EINVAL, "unknown product epilogue %d", mul);
+  if (!aux) return fail(ctx, WE_EINVAL, "aux is null");
+  if (flags & (WE_EPI_ACCUMULATE | WE_EPI_SPLIT_K | WE_EPI_GELU_TANH))
+    return fail(ctx, WE_EINVAL, "a product epilogue takes only WE_EPI_BIAS (flags 0x%x)", flags);
+  if (w_dtype == WE_INT4) return fail(ctx, WE_EUNSUPPORTED, "int4 weights have no product epilogue");
+  return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, nullptr, aux, false,
+                     mul);
+}
+
 namespace {
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res, bool noalloc) {
+                const float* gate, const void* res, bool noalloc, int mul) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
@@ -757,7 +770,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   if (!rc) rc = check_span(ctx, y, y_need, "y");
   if (!rc && (flags & WE_EPI_BIAS)) rc = check_span(ctx, bias, (uint64_t)p->n * 4, "bias");
   if (!rc && gate) rc = check_span(ctx, gate, (uint64_t)p->n * 4, "gate");
-  if (!rc && res) rc = check_span(ctx, res, y_need, "residual");
+  if (!rc && res) rc = check_span(ctx, res, y_need, mul ? "aux" : "residual");
   if (rc) return rc;
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
 
@@ -811,6 +824,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   L.bias = bias;
   L.gate = gate;
   L.res = res;
+  L.mul = mul;
   L.x_dtype = x_dtype;
   L.w_dtype = w_dtype;
   L.y_dtype = y_dtype;

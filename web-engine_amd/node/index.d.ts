@@ -32,6 +32,8 @@ export const DTYPES: { f32: 0; f16: 1; bf16: 2; fp8: 3; int4: 4 };
 /** Epilogue flags of Graph.matmul: += into y, split-K partial planes, + bias[n], tanh GELU. */
 export const EPI: { ACCUMULATE: 1; SPLIT_K: 2; BIAS: 4; GELU_TANH: 8 };
 export const OP: { SWIGLU: 0; SIGMOID_GATE: 1; GATED_ADD: 2; ADD_BIAS: 3; GELU_TANH: 4; ADD: 5; SILU: 6 };
+/** Product epilogues of Graph.matmul: y = silu(aux) * v, or aux * sigmoid(v). */
+export const MUL: { SWIGLU: 1; SIGMOID_GATE: 2 };
 
 /** The subset of GPUQueue the reference's callers use. */
 export interface Queue {
@@ -106,7 +108,7 @@ export class Graph {
 
   matmul(params: Uint32Array, xDtype: DType, x: Binding, wDtype: DType, w: Binding, yDtype: DType, y: Binding,
          opts?: { scales?: Binding | null; group?: number; bias?: Binding | null; flags?: number; gate?: Binding | null;
-                  residual?: Binding | null }): void;
+                  residual?: Binding | null; mul?: 0 | 1 | 2; aux?: Binding | null }): void;
   rmsnorm(rows: number, d: number, eps: number, offset: number, dtype: DType, x: Binding, weight: Binding,
           scale: Binding | null, shift: Binding | null, out: Binding): void;
   rope(tokens: number, heads: number, pairs: number, half: boolean, dtype: DType, x: Binding, cos: Binding,
@@ -159,7 +161,8 @@ export function matmulParams(shape: { m: number; n: number; k: number }, scale: 
 export function kSplitFor(m: number, n: number, k: number): number;
 /** src/model/ops.ts:61 */
 export function linear(graph: Graph, x: Binding, w: Linear, m: number,
-                       opts?: { xDtype?: DType; yDtype?: DType; geluTanh?: boolean }): Buffer;
+                       opts?: { xDtype?: DType; yDtype?: DType; geluTanh?: boolean; swigluGate?: Binding | null;
+                                sigmoidGateOf?: Binding | null; out?: Buffer | null }): Buffer;
 /** src/model/ops.ts:78 */
 export function norm(graph: Graph, x: Binding, weight: Binding, rows: number, d: number, mod: Mod | null, eps?: number,
                      offset?: number, dtype?: DType): Buffer;

@@ -11,6 +11,7 @@ const DTYPES = { f32: F32, f16: F16, bf16: BF16, fp8: FP8, int4: INT4 };
 const ELEM_BYTES = { [F32]: 4, [F16]: 2, [BF16]: 2, [FP8]: 1 };
 const EPI = { ACCUMULATE: 1, SPLIT_K: 2, BIAS: 4, GELU_TANH: 8 };
 const OP = { SWIGLU: 0, SIGMOID_GATE: 1, GATED_ADD: 2, ADD_BIAS: 3, GELU_TANH: 4, ADD: 5, SILU: 6 };
+const MUL = { SWIGLU: 1, SIGMOID_GATE: 2 };
 
 // A binding is a buffer { ptr, size }, a Graph.slice of one, the reference's { buffer, offset, size } form, or a
 // BigInt address.
@@ -285,10 +286,14 @@ class Graph {
   }
 
   // ---- the kernels, one call each ----
-  // gate (f32 [N]) given: y = residual + gate * v, the gatedAdd of src/model/block.ts:60-64 fused (matmulGated)
+  // gate (f32 [N]) given: y = residual + gate * v, the gatedAdd of src/model/block.ts:60-64 fused (matmulGated);
+  // mul given: y = silu(aux) * v (MUL.SWIGLU) or aux * sigmoid(v) (MUL.SIGMOID_GATE) (matmulMul)
   matmul(params, xDtype, x, wDtype, w, yDtype, y,
-         { scales = null, group = 0, bias = null, flags = 0, gate = null, residual = null } = {}) {
-    if (gate === null) {
+         { scales = null, group = 0, bias = null, flags = 0, gate = null, residual = null, mul = 0, aux = null } = {}) {
+    if (mul) {
+      addon.matmulMul(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
+                      ptrOf(bias), flags, mul, ptrOf(aux));
+    } else if (gate === null) {
       addon.matmul(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), ptrOf(scales), group, yDtype, ptrOf(y),
                    ptrOf(bias), flags);
     } else {
@@ -408,9 +413,26 @@ function narrowLinear(graph, x, w, m, xDtype = F32) {
  * The bias (and, on request, the tanh GELU) run in the GEMM epilogue. `w.dtype` may also be "int4" with
  * `w.scales` (f16 [n, k / group]) and `w.group`.
  */
-function linear(graph, x, w, m, { xDtype = F32, yDtype = F32, geluTanh = false } = {}) {
+function linear(graph, x, w, m, { xDtype = F32, yDtype = F32, geluTanh = false, swigluGate = null, sigmoidGateOf = null,
+                                  out = null } = {}) {
   const shape = { m, n: w.n, k: w.k };
-  const y = graph.buffer(m * w.n * ELEM_BYTES[yDtype]);
+  if (swigluGate !== null || sigmoidGateOf !== null) {
+    // the consumer fused: swiglu(swigluGate, linear) or sigmoidGate(sigmoidGateOf, linear) (src/model/ops.ts:102-104)
+    if (geluTanh || (swigluGate !== null && sigmoidGateOf !== null)) throw new Error("one fused consumer at a time, and not with GELU");
+    const aux = swigluGate !== null ? swigluGate : sigmoidGateOf;
+    const mul = swigluGate !== null ? MUL.SWIGLU : MUL.SIGMOID_GATE;
+    const y = out !== null ? out : graph.buffer(m * w.n * ELEM_BYTES[yDtype]);
+    if (!w.lora && wdt(w.dtype) !== INT4) {
+      graph.matmul(matmulParams(shape, w.scale, {}, graph), xDtype, x, wdt(w.dtype), w.buffer, yDtype, y,
+                   { bias: w.bias, flags: w.bias ? EPI.BIAS : 0, mul, aux });
+      return y;
+    }
+    const v = linear(graph, x, w, m, { xDtype, yDtype });
+    graph.elementwise(mul === MUL.SWIGLU ? OP.SWIGLU : OP.SIGMOID_GATE, m * w.n, 1, yDtype, aux, v, null, y);
+    graph.free(v);
+    return y;
+  }
+  const y = out !== null ? out : graph.buffer(m * w.n * ELEM_BYTES[yDtype]);
   // GELU applies to the whole sum (a caller of the reference applies it to what linear returns): with LoRA it
   // runs in place after the update is added, not in the base GEMM's epilogue
   const flags = (w.bias ? EPI.BIAS : 0) | (geluTanh && !w.lora ? EPI.GELU_TANH : 0);
@@ -519,7 +541,7 @@ function readTensor(st, tensor, limit, dst, threads, offset = 0) {
 }
 
 module.exports = {
-  addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP,
+  addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP, MUL,
   matmulParams, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
   SafetensorsError, readHeader, readTensor, registerKernels,

@@ -664,6 +664,35 @@ static napi_value MatmulGated(napi_env env, napi_callback_info info) {
                                           (const float*)bias, flags, (const float*)gate, res));
 }
 
+/* matmulMul(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags, mul, aux): we_matmul_mul */
+static napi_value MatmulMul(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 14)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* pdata = NULL;
+  size_t plen = 0;
+  bytes_of(&a, 1, &pdata, &plen);
+  int32_t xdt = i32_arg(&a, 2);
+  void* x = ptr_arg(&a, 3);
+  int32_t wdt = i32_arg(&a, 4);
+  void* w = ptr_arg(&a, 5);
+  void* scales = ptr_arg(&a, 6);
+  uint32_t group = u32_arg(&a, 7);
+  int32_t ydt = i32_arg(&a, 8);
+  void* y = ptr_arg(&a, 9);
+  void* bias = ptr_arg(&a, 10);
+  uint32_t flags = u32_arg(&a, 11);
+  int32_t mul = i32_arg(&a, 12);
+  void* aux = ptr_arg(&a, 13);
+  if (a.bad) return NULL;
+  if (plen != sizeof(we_matmul_params)) {
+    napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
+    return NULL;
+  }
+  return status(env, ctx, we_matmul_mul(ctx, (const we_matmul_params*)pdata, xdt, x, wdt, w, scales, group, ydt, y,
+                                        (const float*)bias, flags, mul, aux));
+}
+
 /* ---- norms, rotary, elementwise ---- */
 static napi_value RmsNorm(napi_env env, napi_callback_info info) {
   args_t a;
@@ -1070,7 +1099,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},
-      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated},
+      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul},
       {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},

@@ -30,6 +30,7 @@ F32, F16, BF16, FP8, INT4 = 0, 1, 2, 3, 4
 DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
 ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
+MUL_SWIGLU, MUL_SIGMOID_GATE = 1, 2
 OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
 PEAK_F32, PEAK_F16, PEAK_I8, PEAK_MFMA_BF16 = range(4)
 
@@ -95,6 +96,7 @@ SIGNATURES = {
     "we_ksplit_for": (_U32, [_U32, _U32, _U32]),
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
+    "we_matmul_mul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _I, _P]),
     "we_matmul_noalloc": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
     "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
@@ -346,9 +348,14 @@ class Graph:
 
     # ---- raw ops (one dispatch each)
     def matmul(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0, gate=None,
-               residual=None):
-        """we_matmul; with `gate` (f32 [N]) we_matmul_gated: y = residual + gate * v (gatedAdd fused)."""
-        if gate is None:
+               residual=None, mul=0, aux=None):
+        """we_matmul; with `gate` (f32 [N]) we_matmul_gated: y = residual + gate * v (gatedAdd fused); with `mul`
+        we_matmul_mul: y = silu(aux) * v (MUL_SWIGLU) or aux * sigmoid(v) (MUL_SIGMOID_GATE)."""
+        if mul:
+            self.check(self.lib.we_matmul_mul(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                              _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags, mul,
+                                              _addr(aux)))
+        elif gate is None:
             self.check(self.lib.we_matmul(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
                                           _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags))
         else:
@@ -435,12 +442,31 @@ def _wdt(dtype):
     return DTYPES[dtype] if isinstance(dtype, str) else dtype
 
 
-def linear(graph, x, w, m, x_dtype=F32, y_dtype=F32, gelu_tanh=False):
+def linear(graph, x, w, m, x_dtype=F32, y_dtype=F32, gelu_tanh=False, swiglu_gate=None, sigmoid_gate_of=None,
+           out=None):
     """y[m, n] = x[m, k] . W^T (+ bias) (+ lora up.scale * (x . down^T) . up^T, added in place): src/model/ops.ts:61-73.
     The bias (and optional tanh GELU) run in the GEMM epilogue instead of separate passes. GELU applies to the whole
     sum, as a caller of the reference applies it to what linear returns: with LoRA it runs after the update is added
-    (one in-place pass), not in the base GEMM's epilogue."""
-    y = graph.buffer(m * w.n * ELEM_BYTES[y_dtype])
+    (one in-place pass), not in the base GEMM's epilogue.
+    The step that consumes the result may be fused too: swiglu_gate=g returns swiglu(g, linear) (src/model/ops.ts:102)
+    and sigmoid_gate_of=a returns sigmoidGate(a, linear) (ops.ts:104), both in the epilogue when there is no LoRA.
+    `out` (optional) receives the result instead of a new buffer; it may be the gate / a operand itself."""
+    if swiglu_gate is not None or sigmoid_gate_of is not None:
+        if gelu_tanh or (swiglu_gate is not None and sigmoid_gate_of is not None):
+            raise WeError(1, "one fused consumer at a time, and not with GELU")
+        aux = swiglu_gate if swiglu_gate is not None else sigmoid_gate_of
+        mul = MUL_SWIGLU if swiglu_gate is not None else MUL_SIGMOID_GATE
+        y = out if out is not None else graph.buffer(m * w.n * ELEM_BYTES[y_dtype])
+        if w.lora is None and _wdt(w.dtype) != INT4:
+            graph.matmul(matmul_params(m, w.n, w.k, w.scale, graph=graph), x_dtype, x, _wdt(w.dtype), w.buffer,
+                         y_dtype, y, bias=w.bias, flags=EPI_BIAS if w.bias is not None else 0, mul=mul, aux=aux)
+            return y
+        v = linear(graph, x, w, m, x_dtype, y_dtype)
+        op = OP_SWIGLU if mul == MUL_SWIGLU else OP_SIGMOID_GATE
+        graph.elementwise(op, m * w.n, 1, y_dtype, aux, v, None, y)  # swiglu(gate=aux, up=v), sigmoidGate(a=aux, gate=v)
+        graph.free(v)
+        return y
+    y = out if out is not None else graph.buffer(m * w.n * ELEM_BYTES[y_dtype])
     fuse_gelu = gelu_tanh and w.lora is None
     flags = (EPI_BIAS if w.bias is not None else 0) | (EPI_GELU if fuse_gelu else 0)
     graph.matmul(matmul_params(m, w.n, w.k, w.scale, graph=graph), x_dtype, x, _wdt(w.dtype), w.buffer, y_dtype, y,
