@@ -202,11 +202,32 @@ int we_matmul_mul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const voi
                   const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags, int mul,
                   const void* aux);
 
+/* A fused QKV projection with the q/k path of attend() (src/model/block.ts:53-56: per-head RMSNorm of q and k, then
+ * RoPE) in its epilogue. Output columns [0, q_heads * 128) are q heads, the next k_heads * 128 are k heads, the rest
+ * (v) is stored as we_matmul stores it. Each q / k head (128 values of a row t) is RMS-normalized (eps, offset,
+ * weight norm_q / norm_k f32 [128]) and, when cos / sin are given, rotated on rows t >= rope_from with interleaved
+ * pairs and cos / sin row t - rope_from (f32 [rows, 64]); the formulas of we_qk_norm_rope. x 16-bit, any weight but
+ * int4; flags: WE_EPI_BIAS only. Where the GEMM's tile is aligned to heads (256 x 128 or 128 x 128 tiles, no
+ * split-K plan; 16-bit y; e.g. a 512-token text stream) the norm and rotation run in the epilogue, and the value is not rounded to y's
+ * dtype before the norm; otherwise the call runs the GEMM and then we_qk_norm_rope over the q and k columns, in
+ * place. No reference entry point: the reference runs linear, norm and rotate as separate passes. */
+int we_matmul_qk_norm_rope(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype,
+                           const void* w, int y_dtype, void* y, const float* bias, uint32_t flags, uint32_t q_heads,
+                           uint32_t k_heads, float eps, float offset, const float* norm_q, const float* norm_k,
+                           uint32_t rope_from, const float* cos_t, const float* sin_t);
+
 /* ---- norms and rotary: rmsnormWgsl (src/kernels/rmsnorm.ts:13-48) / norm() (src/model/ops.ts:78-82),
  * ropeKernel (src/kernels/rope.ts:59-77) / rotate() (src/model/ops.ts:89-93) ---- */
 /* out = x / sqrt(mean(x^2) + eps) * (offset + weight) * (1 + scale) + shift; scale/shift may be NULL */
 int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
                const float* weight, const float* scale, const float* shift, void* out);
+/* The modulation add of src/model/block.ts:33-37 (mod = tvec + table, the six vectors of a block) folded into the
+ * norm that first consumes it (block.ts:96: norm1 with prescale / preshift), one launch:
+ *   mod[j] = tvec[j] + table[j] for j < mod_n (for the block's later consumers: gates, norm2);
+ *   out = we_rmsnorm(x) with scale = mod[0:d], shift = mod[d:2d], computed in the kernel with the same f32 adds.
+ * tvec, table, mod: f32 [mod_n], mod_n >= 2 d; mod may not overlap tvec, table, x or out. rows, d >= 1. */
+int we_rmsnorm_mod(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                   const float* weight, const float* tvec, const float* table, uint32_t mod_n, float* mod, void* out);
 /* x [tokens, heads, 2*pairs]; cos/sin f32 [tokens, pairs]; half = 0 interleaved pairs, 1 (j, j+pairs) */
 int we_rope(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
             const float* cos_t, const float* sin_t, void* out);

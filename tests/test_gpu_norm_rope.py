@@ -167,3 +167,47 @@ def test_fused_qk_norm_rope_strided_in_place(graph, hd):
     assert np.array_equal(got[:, 1], graph.read(dense).view(np.uint16).reshape(tokens, row))
     assert np.array_equal(got[:, 0], qkv.reshape(tokens, 3, row)[:, 0])
     assert np.array_equal(got[:, 2], qkv.reshape(tokens, 3, row)[:, 2])
+
+
+@pytest.mark.parametrize("dtype,rows,d", [(we.F32, 7, 640), (we.F32, 5, 3072), (we.BF16, 300, 3072),
+                                          (we.F16, 9, 1000), (we.BF16, 4096, 3072)])
+def test_rmsnorm_mod_equals_the_add_then_the_norm(graph, dtype, rows, d):
+    """we_rmsnorm_mod (src/model/block.ts:33-37 folded into norm1, :96) writes mod = tvec + table and the
+    modulated norm; both equal, bit for bit, the separate add pass followed by we_rmsnorm on mod's first two
+    parts (every norm kernel: one wave per row, one block per row, the 16-bit vector kernel)."""
+    rng = np.random.default_rng(rows + d)
+    x = rng.standard_normal(rows * d).astype(np.float32)
+    if dtype == we.BF16:
+        x = O.bf16_rne(x)
+    elif dtype == we.F16:
+        x = x.astype(np.float16)
+    w = rng.uniform(-.3, .3, d).astype(np.float32)
+    tvec = rng.uniform(-1, 1, 6 * d).astype(np.float32)
+    table = rng.uniform(-1, 1, 6 * d).astype(np.float32)
+    mark = graph.mark()
+    xb, wb, tb, tab = graph.buffer(x), graph.buffer(w), graph.buffer(tvec), graph.buffer(table)
+    esz = we.ELEM_BYTES[dtype]
+    mod_f, out_f = graph.buffer(6 * d * 4), graph.buffer(rows * d * esz)
+    graph.rmsnorm_mod(rows, d, 1e-6, 1.0, dtype, xb, wb, tb, tab, 6 * d, mod_f, out_f)
+    mod_s, out_s = graph.buffer(6 * d * 4), graph.buffer(rows * d * esz)
+    graph.elementwise(we.OP_ADD, 6 * d, 1, we.F32, tb, tab, None, mod_s)
+    graph.rmsnorm(rows, d, 1e-6, 1.0, dtype, xb, wb, we.Graph.slice(mod_s, 0, d * 4), we.Graph.slice(mod_s, d * 4, d * 4),
+                  out_s)
+    got = [graph.read(b) for b in (mod_f, out_f, mod_s, out_s)]
+    graph.release(mark)
+    assert np.array_equal(got[0], got[2]) and np.array_equal(got[1], got[3])
+    assert np.array_equal(got[0].view(np.float32), tvec + table)
+
+
+def test_rmsnorm_mod_refuses_overlap_and_short_mod(graph):
+    d = 64
+    mark = graph.mark()
+    x, w, t = graph.buffer(d * 4), graph.buffer(d * 4), graph.buffer(6 * d * 4)
+    mod, out = graph.buffer(6 * d * 4), graph.buffer(d * 4)
+    with pytest.raises(we.WeError, match="may not overlap"):
+        graph.rmsnorm_mod(1, d, 1e-6, 1.0, we.F32, x, w, t, t, 6 * d, t, out)
+    with pytest.raises(we.WeError, match="less than 2 d"):
+        graph.rmsnorm_mod(1, d, 1e-6, 1.0, we.F32, x, w, t, t, d, mod, out)
+    with pytest.raises(we.WeError, match="must be positive"):
+        graph.rmsnorm_mod(0, d, 1e-6, 1.0, we.F32, x, w, t, t, 6 * d, mod, out)
+    graph.release(mark)

@@ -38,7 +38,7 @@ EXPORTS = {
     "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_host_span": "hostSpan", "we_stream_copy": "streamCopy",
     "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
     "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
-    "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_mul": "matmulMul", "we_rmsnorm": "rmsnorm",
+    "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_mul": "matmulMul", "we_matmul_qk_norm_rope": "matmulQkNormRope", "we_rmsnorm": "rmsnorm", "we_rmsnorm_mod": "rmsnormMod",
     "we_rope": "rope",
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",

@@ -7,9 +7,10 @@
   first input instead of a new buffer.
 - `DoubleBlock`: the double-stream DiT block (text and image streams with their own weights, one joint
   attention), built from the same steps with a persistent workspace so a forward allocates nothing:
-    mod_s = tvec + table_s;  h_s = norm1_s(x_s) * (1 + prescale_s) + preshift_s
+    mod_s = tvec + table_s;  h_s = norm1_s(x_s) * (1 + prescale_s) + preshift_s  (one launch: the norm writes mod_s)
     [q|k|v]_s = h_s . qkv_s^T (both streams write one [text + image, 3 hidden] buffer, text rows first)
-    q_s, k_s: per-head RMSNorm, then RoPE on the image rows (in place in that buffer)
+    q_s, k_s: per-head RMSNorm, then RoPE on the image rows (in the QKV GEMM's epilogue for the text stream,
+    whose 128 x 128 tiles align with heads; in place right after it for the image stream)
     o = attention(q, k, v) read straight from the fused rows;  x1_s = x_s + pregate_s * (o_s . proj_s^T)
     out_s = x1_s + postgate_s * down_s(gelu_tanh(up_s(norm2_s(x1_s) * (1 + postscale_s) + postshift_s)))
   The GELU runs in the up projection's epilogue, and both gated residuals in the epilogues of the output
@@ -75,7 +76,11 @@ class BlockWeights:
 def modulation(graph, tvec, table, hidden):
     """src/model/block.ts:33-37: mod = tvec + table; the six vectors as slices of it."""
     mod = we.add(graph, tvec, table, 6 * hidden)
-    return {name: we.Graph.slice(mod, i * hidden * 4, hidden * 4) for i, name in enumerate(MOD)}, mod
+    return _mod_parts(mod, hidden), mod
+
+
+def _mod_parts(mod, hidden):
+    return {name: we.Graph.slice(mod, i * hidden * 4, hidden * 4) for i, name in enumerate(MOD)}
 
 
 def _used(graph, x, f):
@@ -115,8 +120,11 @@ def _mlp(graph, w, cfg, h, rows, dtype):
 def block(graph, w, cfg, x, tvec, rope, dtype=we.F32):
     """src/model/block.ts:91-105: one Krea single-stream block; x [tokens, hidden] -> new [tokens, hidden]."""
     t, hidden = rope.tokens, cfg.hidden
-    mod, mod_buf = modulation(graph, tvec, w.table, hidden)
-    h = we.norm(graph, x, w.norm1, t, hidden, we.Mod(mod["prescale"], mod["preshift"]), cfg.eps, 1.0, dtype)
+    # modulation (block.ts:33-37) folded into norm1 (block.ts:96): one launch writes mod and h
+    mod_buf = graph.buffer(6 * hidden * 4)
+    h = graph.buffer(t * hidden * we.ELEM_BYTES[dtype])
+    graph.rmsnorm_mod(t, hidden, cfg.eps, 1.0, dtype, x, w.norm1, tvec, w.table, 6 * hidden, mod_buf, h)
+    mod = _mod_parts(mod_buf, hidden)
     a = _used(graph, h, lambda y: _attend(graph, w, cfg, y, t, rope, dtype))
     x1 = _used(graph, a, lambda y: we.gated_add(graph, x, y, mod["pregate"], t * hidden, hidden, dtype))
     h2 = we.norm(graph, x1, w.norm2, t, hidden, we.Mod(mod["postscale"], mod["postshift"]), cfg.eps, 1.0, dtype)
@@ -196,17 +204,22 @@ class DoubleBlock:
 
         def qkv_step(s):
             w, rows, r0, h = ws[s], self.rows[s], self.row0[s], self.h[s]
-            g.elementwise(we.OP_ADD, 6 * H, 1, we.F32, tvec, w.table, None, self.mod[s])
-            mod = self.mod[s]
-            g.rmsnorm(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1, sl(mod, 0, H * 4), sl(mod, H * 4, H * 4), h)
+            # mod = tvec + table (for the gates and norm2 below) written by norm1, which folds the add in
+            g.rmsnorm_mod(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1, tvec, w.table, 6 * H, self.mod[s], h)
+            # the fused QKV projection: per-head RMSNorm of q and k (and RoPE on the image stream) in the GEMM's
+            # epilogue where its tile is head-aligned (the text stream), else a pass right after it
             p = we.matmul_params(rows, 3 * H, H, w.qkv.scale, y_offset=r0 * 3 * H, graph=g)
-            g.matmul(p, dt, h, we.FP8, w.qkv.buffer, dt, self.qkv)
             rotate = s == 1
+            cos, sin = (rope_img.cos, rope_img.sin) if rotate else (None, None)
+            if hd == 128:
+                g.matmul_qk_norm_rope(p, dt, h, we.FP8, w.qkv.buffer, dt, self.qkv, heads, heads, cfg.eps, 1.0,
+                                      w.norm_q, w.norm_k, 0, cos, sin)
+                return
+            g.matmul(p, dt, h, we.FP8, w.qkv.buffer, dt, self.qkv)
             for part, norm_w in ((0, w.norm_q), (1, w.norm_k)):
                 base = sl(self.qkv, (r0 * 3 * H + part * H) * e, 0)
-                g.qk_norm_rope(rows, heads, hd, cfg.eps, 1.0, norm_w, 0 if rotate else rows, False,
-                               rope_img.cos if rotate else None, rope_img.sin if rotate else None, dt, base, base,
-                               x_stride=3 * H, out_stride=3 * H)
+                g.qk_norm_rope(rows, heads, hd, cfg.eps, 1.0, norm_w, 0 if rotate else rows, False, cos, sin, dt, base,
+                               base, x_stride=3 * H, out_stride=3 * H)
 
         def out_step(s):
             w, rows, r0, mod, h, u = ws[s], self.rows[s], self.row0[s], self.mod[s], self.h[s], self.u[s]

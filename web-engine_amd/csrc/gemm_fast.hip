@@ -57,6 +57,13 @@ struct FastArgs {
   float* part;
   uint32_t rsplits;
   uint32_t mul;  // product epilogue with res (GemmLaunch::mul), 0: none
+  // fused per-head RMSNorm + RoPE of the q / k columns (GemmLaunch::qk_*), qk_cols 0: none
+  uint32_t qk_cols, q_cols, qk_rope_from;
+  float qk_eps, qk_offset;
+  const float* qk_norm_q;
+  const float* qk_norm_k;
+  const float* qk_cos;
+  const float* qk_sin;
 };
 
 __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
@@ -455,6 +462,80 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     return;
   }
 
+  // ---- fused q/k epilogue (the q/k path of attend(), src/model/block.ts:53-56): a head of 128 columns is
+  // the 64 columns of waves wn and wn ^ 1 (WTN = 64, the tile aligned to heads), so each row's sum of squares
+  // is the two waves' partial sums, exchanged through LDS. Every wave of the workgroup takes this branch (the
+  // tile lies wholly inside the q/k columns), so the barriers below are uniform. Not in the ping-pong kernels:
+  // their 128 accumulators and double operand sets leave no registers for it (it made them spill).
+  if constexpr (WTN == 64 && WAVES_N % 2 == 0 && !PP) {
+    if (a.qk_cols && col0 < a.qk_cols) {
+      const bool has_bias_qk = (a.flags & WE_EPI_BIAS_BIT) != 0;
+      float ss[TM];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        ss[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            float t = acc[i][j][v] * a.scale;
+            if (has_bias_qk) t += a.bias[col0 + wn * WTN + j * 32 + 8 * (v >> 2) + 4 * h + (v & 3)];
+            acc[i][j][v] = t;
+            ss[i] += t * t;
+          }
+        ss[i] += __shfl_xor(ss[i], 32, 64);  // lanes l32 and l32 + 32 hold the same row
+      }
+      float* red = (float*)lds;  // [BM rows][WAVES_N] partial sums; every wave is done with the stages
+      lds_barrier();
+      if (h == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) red[(wm * WTM + i * 32 + l32) * WAVES_N + wn] = ss[i];
+      }
+      lds_barrier();
+      const uint32_t hcol0 = (uint32_t)(wn & 1) * 64;  // this wave's first column inside its head
+      const float* nw = (col0 + wn * WTN < a.q_cols ? a.qk_norm_q : a.qk_norm_k) + hcol0;
+      const std::integral_constant<bool, YT == F16> tag;
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const uint32_t rloc = wm * WTM + i * 32 + l32;
+        const float tot = red[rloc * WAVES_N + (wn & ~1)] + red[rloc * WAVES_N + (wn | 1)];
+        const float inv = 1.0f / sqrtf(tot / 128.0f + a.qk_eps);
+        const uint32_t row = row0 + rloc;
+        const bool rot = a.qk_cos && row >= a.qk_rope_from;
+        const size_t trow = rot ? (size_t)(row - a.qk_rope_from) * 64 : 0;
+        const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride + col0 + wn * WTN;
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const uint32_t cl = j * 32 + 8 * q + 4 * h;  // column inside the wave's 64 (and in the head: + hcol0)
+            const f32x4 wv = *(const f32x4*)(nw + cl);
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = acc[i][j][4 * q + e] * inv * (a.qk_offset + wv[e]);
+            if (rot) {
+              const uint32_t pr = (hcol0 + cl) / 2;  // pairs (y0, y1) and (y2, y3)
+              const f32x2 c2 = *(const f32x2*)(a.qk_cos + trow + pr), s2 = *(const f32x2*)(a.qk_sin + trow + pr);
+#pragma unroll
+              for (int p = 0; p < 2; p++) {
+                const float u = y[2 * p], v = y[2 * p + 1];
+                y[2 * p] = u * c2[p] - v * s2[p];
+                y[2 * p + 1] = v * c2[p] + u * s2[p];
+              }
+            }
+            if (row < a.m) {
+              if constexpr (YT == F32) {
+                *(f32x4*)((float*)a.y + yrow + cl) = f32x4{y[0], y[1], y[2], y[3]};
+              } else {
+                *(u32x2*)((uint16_t*)a.y + yrow + cl) = u32x2{pack2(y[0], y[1], tag), pack2(y[2], y[3], tag)};
+              }
+            }
+          }
+      }
+      return;
+    }
+  }
+
   // ---- epilogue: lane (l32, h) holds row l32 of each 32-row sub-tile and, for q = 0..3, the columns
   // 8q + 4h .. 8q + 4h + 3 of each 32-column sub-tile (accumulator entries 4q .. 4q + 3)
   const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
@@ -775,6 +856,20 @@ GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits) {
   return p;
 }
 
+bool gemm_qk_fusable(const GemmLaunch& L) {
+  if (L.generic || L.splits > 1 || L.flags & ~WE_EPI_BIAS_BIT || L.mul || L.gate || L.res) return false;
+  if (L.y_dtype == F32 || !fast_supported(L, L.k)) return false;
+  if (gemm_reduce_plan(L, 0).rsplits > 1) return false;
+  const int cfg = L.cfg >= 0 ? L.cfg : pick_fast_cfg(L.m, L.n, 1, L.w_dtype == FP8);
+  // head-aligned tiles with 64-column waves outside the ping-pong kernels: 256 x 128 (4 x 2), 128 x 128 (2 x 2)
+  if (cfg != GEMM_CFG_256x128 && cfg != GEMM_CFG_128x128) return false;
+  const uint32_t bn = cfg_bn(cfg);
+  return L.qk_cols % bn == 0 && L.q_cols % bn == 0 && L.qk_cols <= L.n && (L.y_stride % 4) == 0 &&
+         (L.y_offset % 4) == 0 && ((uintptr_t)L.y % 16) == 0 && ((uintptr_t)L.qk_norm_q % 16) == 0 &&
+         ((uintptr_t)L.qk_norm_k % 16) == 0 && ((uintptr_t)L.qk_cos % 8) == 0 && ((uintptr_t)L.qk_sin % 8) == 0 &&
+         (!L.bias || ((uintptr_t)L.bias % 4) == 0);
+}
+
 // Returns hipErrorNotSupported when the shape / dtypes / alignment are not for this path.
 hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   const bool reduce = L.rsplits > 1;
@@ -792,6 +887,15 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.gate = L.gate;
   a.res = L.res;
   a.mul = (uint32_t)L.mul;
+  a.qk_cols = L.qk_cols;
+  a.q_cols = L.q_cols;
+  a.qk_rope_from = L.qk_rope_from;
+  a.qk_eps = L.qk_eps;
+  a.qk_offset = L.qk_offset;
+  a.qk_norm_q = L.qk_norm_q;
+  a.qk_norm_k = L.qk_norm_k;
+  a.qk_cos = L.qk_cos;
+  a.qk_sin = L.qk_sin;
   a.x_bytes = L.k ? (uint32_t)(((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2) : 0;
   a.w_bytes = L.k ? (uint32_t)(((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb) : 0;
   a.m = L.m;

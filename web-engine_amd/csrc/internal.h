@@ -34,6 +34,16 @@ struct GemmLaunch {
   // 0 none, 1: y = silu(res) * v (swiglu with this GEMM as `up`), 2: y = res * sigmoid(v) (sigmoidGate with this
   // GEMM as `gate`); v the value after scale and bias
   int mul;
+  // fused q/k path of attention (GemmLaunch::qk_cols > 0): columns [0, qk_cols) are heads of 128 values, q heads
+  // below q_cols (norm weight qk_norm_q) and k heads above (qk_norm_k); each head is RMS-normalized (qk_eps,
+  // qk_offset) and, on rows >= qk_rope_from (when qk_cos is set), rotated with interleaved pairs, cos / sin row
+  // = row - qk_rope_from ([., 64] f32)
+  uint32_t qk_cols, q_cols, qk_rope_from;
+  float qk_eps, qk_offset;
+  const float* qk_norm_q;
+  const float* qk_norm_k;
+  const float* qk_cos;
+  const float* qk_sin;
   int x_dtype, w_dtype, y_dtype;
   uint32_t m, n, k;
   float scale;
@@ -106,6 +116,10 @@ hipError_t noalloc_scratch_init(int device);
 // The address noalloc_scratch_init found on `device`, or null before it succeeded.
 void* noalloc_scratch(int device);
 
+// Can gemm_fast_launch run this GEMM with the fused q/k epilogue (fast path, a head-aligned tile chosen, no
+// split-K plan)? qk_cols / q_cols must be set in L.
+bool gemm_qk_fusable(const GemmLaunch& L);
+
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_fill(void* p, size_t bytes, uint8_t byte, hipStream_t s);
 hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
@@ -117,6 +131,9 @@ hipError_t launch_layer_sum(uint32_t tokens, uint32_t layers, uint32_t dim, cons
                             hipStream_t s);
 hipError_t launch_rmsnorm(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
                           const float* weight, const float* scale, const float* shift, void* out, hipStream_t s);
+hipError_t launch_rmsnorm_mod(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                              const float* weight, const float* tvec, const float* table, uint32_t mod_n, float* mod,
+                              void* out, hipStream_t s);
 hipError_t launch_rope(uint32_t tokens, uint32_t heads, uint32_t pairs, int half, int dtype, const void* x,
                        const float* c, const float* sn, void* out, hipStream_t s);
 hipError_t launch_qk_norm_rope(uint32_t tokens, uint32_t heads, uint32_t head_dim, float eps, float offset,

@@ -129,10 +129,34 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // one wave per row (d <= 1024), several rows per block
+// The modulation add of src/model/block.ts:33-37 folded into the norm that first consumes it: scale / shift are
+// the timestep vector's parts and tscale / tshift the block table's, added per value as the separate add pass would
+// (scale[i] + tscale[i], one f32 add, the same bits); the launch also writes mo = ma + mb (the six vectors, for the
+// later consumers), spread over its threads. All NULL: plain norm.
+struct NormMod {
+  const float* tscale;
+  const float* tshift;
+  const float* ma;
+  const float* mb;
+  float* mo;
+  uint32_t mn;
+};
+
+__device__ __forceinline__ void norm_mod_side(const NormMod& md) {
+  if (!md.mo) return;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < md.mn; j += stride) md.mo[j] = md.ma[j] + md.mb[j];
+}
+
+__device__ __forceinline__ float mod_part(const float* p, const float* t, uint32_t i) {
+  return p ? (t ? p[i] + t[i] : p[i]) : 0.0f;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(uint32_t rows, uint32_t d, float eps, float offset,
                                                           const void* x, const float* weight, const float* scale,
-                                                          const float* shift, void* out) {
+                                                          const float* shift, void* out, NormMod md) {
+  norm_mod_side(md);
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -151,7 +175,7 @@ __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(uint32_t rows, uint32
   for (int j = 0; j < 16; j++) {
     const uint32_t i = lane + 64 * j;
     if (i < d) {
-      const float sc = scale ? scale[i] : 0.0f, sh = shift ? shift[i] : 0.0f;
+      const float sc = mod_part(scale, md.tscale, i), sh = mod_part(shift, md.tshift, i);
       store_from_f32<DT>(out, base + i, v[j] * inv * (offset + weight[i]) * (1.0f + sc) + sh);
     }
   }
@@ -161,7 +185,8 @@ __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(uint32_t rows, uint32
 template <int DT>
 __global__ void __launch_bounds__(256) rmsnorm_block_kernel(uint32_t rows, uint32_t d, float eps, float offset,
                                                            const void* x, const float* weight, const float* scale,
-                                                           const float* shift, void* out) {
+                                                           const float* shift, void* out, NormMod md) {
+  norm_mod_side(md);
   __shared__ float part[4];
   const uint32_t row = blockIdx.x;
   const size_t base = (size_t)row * d;
@@ -176,7 +201,7 @@ __global__ void __launch_bounds__(256) rmsnorm_block_kernel(uint32_t rows, uint3
   const float tot = part[0] + part[1] + part[2] + part[3];
   const float inv = 1.0f / sqrtf(tot / (float)d + eps);
   for (uint32_t i = threadIdx.x; i < d; i += 256) {
-    const float sc = scale ? scale[i] : 0.0f, sh = shift ? shift[i] : 0.0f;
+    const float sc = mod_part(scale, md.tscale, i), sh = mod_part(shift, md.tshift, i);
     store_from_f32<DT>(out, base + i, load_as_f32<DT>(x, base + i) * inv * (offset + weight[i]) * (1.0f + sc) + sh);
   }
 }
@@ -187,7 +212,8 @@ __global__ void __launch_bounds__(256) rmsnorm_block_kernel(uint32_t rows, uint3
 template <int DT, int NCH>
 __global__ void __launch_bounds__(256) rmsnorm_vec_kernel(uint32_t rows, uint32_t d, float eps, float offset,
                                                          const u32x4* x, const float* weight, const float* scale,
-                                                         const float* shift, u32x4* out) {
+                                                         const float* shift, u32x4* out, NormMod md) {
+  norm_mod_side(md);
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -222,10 +248,18 @@ __global__ void __launch_bounds__(256) rmsnorm_vec_kernel(uint32_t rows, uint32_
     if (scale) {
       *(f32x4*)&sc[0] = *(const f32x4*)(scale + 8 * c);
       *(f32x4*)&sc[4] = *(const f32x4*)(scale + 8 * c + 4);
+      if (md.tscale) {
+        *(f32x4*)&sc[0] += *(const f32x4*)(md.tscale + 8 * c);
+        *(f32x4*)&sc[4] += *(const f32x4*)(md.tscale + 8 * c + 4);
+      }
     }
     if (shift) {
       *(f32x4*)&sh[0] = *(const f32x4*)(shift + 8 * c);
       *(f32x4*)&sh[4] = *(const f32x4*)(shift + 8 * c + 4);
+      if (md.tshift) {
+        *(f32x4*)&sh[0] += *(const f32x4*)(md.tshift + 8 * c);
+        *(f32x4*)&sh[4] += *(const f32x4*)(md.tshift + 8 * c + 4);
+      }
     }
     float y[8];
 #pragma unroll
@@ -236,42 +270,60 @@ __global__ void __launch_bounds__(256) rmsnorm_vec_kernel(uint32_t rows, uint32_
 
 template <int DT>
 static bool rmsnorm_vec(uint32_t rows, uint32_t d, float eps, float offset, const void* x, const float* w,
-                        const float* sc, const float* sh, void* out, hipStream_t s) {
+                        const float* sc, const float* sh, void* out, const NormMod& md, hipStream_t s) {
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  if (d % 8 || d > 8 * 64 * 12 || !a16(x) || !a16(out) || !a16(w) || !a16(sc) || !a16(sh)) return false;
+  if (d % 8 || d > 8 * 64 * 12 || !a16(x) || !a16(out) || !a16(w) || !a16(sc) || !a16(sh) || !a16(md.tscale) ||
+      !a16(md.tshift))
+    return false;
   const dim3 g((rows + 3) / 4), t(256);
   const uint32_t nch = (d / 8 + 63) / 64;
   const u32x4 *xv = (const u32x4*)x;
   u32x4* ov = (u32x4*)out;
-  if (nch <= 4) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
-  else if (nch <= 6) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 6>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
-  else if (nch <= 8) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
-  else hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 12>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov);
+  if (nch <= 4) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov, md);
+  else if (nch <= 6) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 6>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov, md);
+  else if (nch <= 8) hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov, md);
+  else hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 12>), g, t, 0, s, rows, d, eps, offset, xv, w, sc, sh, ov, md);
   return true;
 }
 
 template <int DT>
 static void rmsnorm_dt(uint32_t rows, uint32_t d, float eps, float offset, const void* x, const float* w,
-                       const float* sc, const float* sh, void* out, hipStream_t s) {
+                       const float* sc, const float* sh, void* out, const NormMod& md, hipStream_t s) {
   if constexpr (DT != F32) {
-    if (d > 1024 && rmsnorm_vec<DT>(rows, d, eps, offset, x, w, sc, sh, out, s)) return;
+    if (d > 1024 && rmsnorm_vec<DT>(rows, d, eps, offset, x, w, sc, sh, out, md, s)) return;
   }
   if (d <= 1024)
     hipLaunchKernelGGL(rmsnorm_wave_kernel<DT>, dim3((rows + 3) / 4), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh,
-                       out);
+                       out, md);
   else
-    hipLaunchKernelGGL(rmsnorm_block_kernel<DT>, dim3(rows), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh, out);
+    hipLaunchKernelGGL(rmsnorm_block_kernel<DT>, dim3(rows), dim3(256), 0, s, rows, d, eps, offset, x, w, sc, sh, out,
+                       md);
+}
+
+static hipError_t rmsnorm_any(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                              const float* weight, const float* scale, const float* shift, void* out, const NormMod& md,
+                              hipStream_t s) {
+  if (rows == 0 || d == 0) return hipSuccess;
+  switch (dtype) {
+    case F16: rmsnorm_dt<F16>(rows, d, eps, offset, x, weight, scale, shift, out, md, s); break;
+    case BF16: rmsnorm_dt<BF16>(rows, d, eps, offset, x, weight, scale, shift, out, md, s); break;
+    default: rmsnorm_dt<F32>(rows, d, eps, offset, x, weight, scale, shift, out, md, s); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
                           const float* weight, const float* scale, const float* shift, void* out, hipStream_t s) {
-  if (rows == 0 || d == 0) return hipSuccess;
-  switch (dtype) {
-    case F16: rmsnorm_dt<F16>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
-    case BF16: rmsnorm_dt<BF16>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
-    default: rmsnorm_dt<F32>(rows, d, eps, offset, x, weight, scale, shift, out, s); break;
-  }
-  return hipGetLastError();
+  return rmsnorm_any(rows, d, eps, offset, dtype, x, weight, scale, shift, out, NormMod{}, s);
+}
+
+// mod = tvec + table (mod_n values) and out = rmsnorm(x) modulated by (tvec + table)[0:d] / [d:2d], one launch
+// (rows >= 1 and d >= 1: the caller checks)
+hipError_t launch_rmsnorm_mod(uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                              const float* weight, const float* tvec, const float* table, uint32_t mod_n, float* mod,
+                              void* out, hipStream_t s) {
+  const NormMod md{table, table + d, tvec, table, mod, mod_n};
+  return rmsnorm_any(rows, d, eps, offset, dtype, x, weight, tvec, tvec + d, out, md, s);
 }
 
 // ------------------------------------------------------------------ RoPE (src/kernels/rope.ts:45-77)

@@ -695,9 +695,20 @@ uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
 }
 
 namespace {
+// the q/k path of attend() fused into a QKV projection (we_matmul_qk_norm_rope)
+struct QkFuse {
+  uint32_t q_heads, k_heads;
+  float eps, offset;
+  const float* norm_q;
+  const float* norm_k;
+  uint32_t rope_from;
+  const float* cos_t;
+  const float* sin_t;
+};
+
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res, bool noalloc = false, int mul = 0);
+                const float* gate, const void* res, bool noalloc = false, int mul = 0, const QkFuse* qk = nullptr);
 }  // namespace
 
 int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
@@ -737,10 +748,33 @@ int we_matmul_mul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const voi
                      mul);
 }
 
+int we_matmul_qk_norm_rope(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype,
+                           const void* w, int y_dtype, void* y, const float* bias, uint32_t flags, uint32_t q_heads,
+                           uint32_t k_heads, float eps, float offset, const float* norm_q, const float* norm_k,
+                           uint32_t rope_from, const float* cos_t, const float* sin_t) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!p) return fail(ctx, WE_EINVAL, "params is null");
+  if (flags & ~WE_EPI_BIAS) return fail(ctx, WE_EINVAL, "the fused q/k projection takes only WE_EPI_BIAS (flags 0x%x)",
+                                        flags);
+  if (w_dtype == WE_INT4) return fail(ctx, WE_EUNSUPPORTED, "int4 weights have no fused q/k epilogue");
+  if ((uint64_t)(q_heads + k_heads) * 128 > p->n)
+    return fail(ctx, WE_EINVAL, "q and k heads (%u + %u of 128) exceed the %u output columns", q_heads, k_heads, p->n);
+  if ((cos_t == nullptr) != (sin_t == nullptr)) return fail(ctx, WE_EINVAL, "cos and sin go together");
+  int rc = check_span(ctx, norm_q, q_heads ? 128 * 4 : 0, "norm_q");
+  if (!rc) rc = check_span(ctx, norm_k, k_heads ? 128 * 4 : 0, "norm_k");
+  const uint64_t rot = cos_t && p->m > rope_from ? (uint64_t)(p->m - rope_from) * 64 * 4 : 0;
+  if (!rc) rc = check_span(ctx, cos_t, rot, "cos");
+  if (!rc) rc = check_span(ctx, sin_t, rot, "sin");
+  if (rc) return rc;
+  const QkFuse qk{q_heads, k_heads, eps, offset, norm_q, norm_k, rope_from, cos_t, sin_t};
+  return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, nullptr, 0, y_dtype, y, bias, flags, nullptr, nullptr, false, 0,
+                     &qk);
+}
+
 namespace {
 int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                 const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res, bool noalloc, int mul) {
+                const float* gate, const void* res, bool noalloc, int mul, const QkFuse* qk) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
@@ -849,6 +883,20 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   L.rsplits = 1;
   L.rkc = L.k;
   L.scratch = nullptr;
+  bool qk_fused = false;
+  if (qk && qk->q_heads + qk->k_heads) {
+    L.qk_cols = (qk->q_heads + qk->k_heads) * 128;
+    L.q_cols = qk->q_heads * 128;
+    L.qk_rope_from = qk->rope_from;
+    L.qk_eps = qk->eps;
+    L.qk_offset = qk->offset;
+    L.qk_norm_q = qk->norm_q;
+    L.qk_norm_k = qk->norm_k;
+    L.qk_cos = qk->cos_t;
+    L.qk_sin = qk->sin_t;
+    qk_fused = we::gemm_qk_fusable(L);
+    if (!qk_fused) L.qk_cols = L.q_cols = 0;  // the plain GEMM, then the q/k pass below
+  }
   const char* split_env = getenv("WE_GEMM_SPLITK");  // "off", or a slice count for sweeps
   if (!(split_env && strcmp(split_env, "off") == 0)) {
     const uint32_t force = split_env ? (uint32_t)strtoul(split_env, nullptr, 10) : 0u;
@@ -874,6 +922,20 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   }
   hipError_t e = we::gemm_launch(L, ctx->compute);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+  if (qk && !qk_fused) {
+    // no head-aligned tile for this shape: the q and k heads in a pass of their own, in place
+    const uint64_t yb = elem_bytes(y_dtype);
+    char* base = (char*)y + (uint64_t)p->y_offset * yb;
+    for (int part = 0; part < 2; part++) {
+      const uint32_t heads = part ? qk->k_heads : qk->q_heads;
+      if (!heads) continue;
+      char* hp = base + (uint64_t)(part ? qk->q_heads * 128 : 0) * yb;
+      e = we::launch_qk_norm_rope(p->m, heads, 128, qk->eps, qk->offset, part ? qk->norm_k : qk->norm_q,
+                                  qk->cos_t ? qk->rope_from : p->m, 0, qk->cos_t, qk->sin_t, y_dtype, hp, p->y_stride,
+                                  hp, p->y_stride, ctx->compute);
+      if (e != hipSuccess) return hip_fail(ctx, e, "qk norm rope launch");
+    }
+  }
   return WE_OK;
 }
 }  // namespace
@@ -906,6 +968,32 @@ int we_read_peak(we_ctx* ctx, const void* buf, size_t bytes, uint32_t* out) {
 }
 
 // ------------------------------------------------------------------------------------------ norms, rope, elementwise
+
+int we_rmsnorm_mod(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
+                   const float* weight, const float* tvec, const float* table, uint32_t mod_n, float* mod, void* out) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!is_act(dtype)) return fail(ctx, WE_EINVAL, "rmsnorm dtype %d is not f32 / f16 / bf16", dtype);
+  if (rows == 0 || d == 0) return fail(ctx, WE_EINVAL, "rows and d must be positive (rows %u, d %u)", rows, d);
+  if (mod_n < 2 * d) return fail(ctx, WE_EINVAL, "mod_n %u is less than 2 d = %u (scale and shift)", mod_n, 2 * d);
+  const uint64_t n = (uint64_t)rows * d * elem_bytes(dtype), mb = (uint64_t)mod_n * 4;
+  int rc = check_span(ctx, x, n, "x");
+  if (!rc) rc = check_span(ctx, out, n, "out");
+  if (!rc) rc = check_span(ctx, weight, (uint64_t)d * 4, "weight");
+  if (!rc) rc = check_span(ctx, tvec, mb, "tvec");
+  if (!rc) rc = check_span(ctx, table, mb, "table");
+  if (!rc) rc = check_span(ctx, mod, mb, "mod");
+  if (rc) return rc;
+  // mod is written while other threads read tvec / table / x: it may not overlap any of them
+  auto overlap = [](const void* a, uint64_t na, const void* b, uint64_t nb) {
+    return (const char*)a < (const char*)b + nb && (const char*)b < (const char*)a + na;
+  };
+  if (overlap(mod, mb, tvec, mb) || overlap(mod, mb, table, mb) || overlap(mod, mb, x, n) || overlap(mod, mb, out, n))
+    return fail(ctx, WE_EINVAL, "mod may not overlap tvec, table, x or out");
+  HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+  hipError_t e = we::launch_rmsnorm_mod(rows, d, eps, offset, dtype, x, weight, tvec, table, mod_n, mod, out,
+                                        ctx->compute);
+  return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "rmsnorm launch");
+}
 
 int we_rmsnorm(we_ctx* ctx, uint32_t rows, uint32_t d, float eps, float offset, int dtype, const void* x,
                const float* weight, const float* scale, const float* shift, void* out) {

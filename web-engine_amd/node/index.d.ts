@@ -109,8 +109,16 @@ export class Graph {
   matmul(params: Uint32Array, xDtype: DType, x: Binding, wDtype: DType, w: Binding, yDtype: DType, y: Binding,
          opts?: { scales?: Binding | null; group?: number; bias?: Binding | null; flags?: number; gate?: Binding | null;
                   residual?: Binding | null; mul?: 0 | 1 | 2; aux?: Binding | null }): void;
+  /** A QKV projection with the per-head RMSNorm + RoPE of its q / k heads (128 wide) fused in. */
+  matmulQkNormRope(params: Uint32Array, xDtype: DType, x: Binding, wDtype: DType, w: Binding, yDtype: DType, y: Binding,
+                   qHeads: number, kHeads: number, eps: number, offset: number, normQ: Binding, normK: Binding,
+                   opts?: { ropeFrom?: number; cos?: Binding | null; sin?: Binding | null; bias?: Binding | null;
+                            flags?: number }): void;
   rmsnorm(rows: number, d: number, eps: number, offset: number, dtype: DType, x: Binding, weight: Binding,
           scale: Binding | null, shift: Binding | null, out: Binding): void;
+  /** mod = tvec + table (modN f32) and out = rmsnorm(x) modulated by mod[0:d], mod[d:2d], in one launch. */
+  rmsnormMod(rows: number, d: number, eps: number, offset: number, dtype: DType, x: Binding, weight: Binding,
+             tvec: Binding, table: Binding, modN: number, mod: Binding, out: Binding): void;
   rope(tokens: number, heads: number, pairs: number, half: boolean, dtype: DType, x: Binding, cos: Binding,
        sin: Binding, out: Binding): void;
   qkNormRope(tokens: number, heads: number, headDim: number, eps: number, offset: number, weight: Binding,

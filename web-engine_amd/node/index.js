@@ -302,9 +302,23 @@ class Graph {
     }
   }
 
+  /** A QKV projection with the per-head RMSNorm + RoPE of its q / k heads (128 wide) fused in (the q/k path of
+   * attend(), src/model/block.ts:53-56). */
+  matmulQkNormRope(params, xDtype, x, wDtype, w, yDtype, y, qHeads, kHeads, eps, offset, normQ, normK,
+                   { ropeFrom = 0, cos = null, sin = null, bias = null, flags = 0 } = {}) {
+    addon.matmulQkNormRope(this.ctx, params, xDtype, ptrOf(x), wDtype, ptrOf(w), yDtype, ptrOf(y), ptrOf(bias), flags,
+                           qHeads, kHeads, eps, offset, ptrOf(normQ), ptrOf(normK), ropeFrom, ptrOf(cos), ptrOf(sin));
+  }
+
   rmsnorm(rows, d, eps, offset, dtype, x, weight, scale, shift, out) {
     addon.rmsnorm(this.ctx, rows, d, eps, offset, dtype, ptrOf(x), ptrOf(weight), ptrOf(scale), ptrOf(shift),
                   ptrOf(out));
+  }
+
+  /** mod = tvec + table (modN f32) and out = rmsnorm(x) modulated by mod[0:d], mod[d:2d], in one launch */
+  rmsnormMod(rows, d, eps, offset, dtype, x, weight, tvec, table, modN, mod, out) {
+    addon.rmsnormMod(this.ctx, rows, d, eps, offset, dtype, ptrOf(x), ptrOf(weight), ptrOf(tvec), ptrOf(table), modN,
+                     ptrOf(mod), ptrOf(out));
   }
 
   rope(tokens, heads, pairs, half, dtype, x, cos, sin, out) {

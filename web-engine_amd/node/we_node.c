@@ -18,7 +18,7 @@
 
 #include "we.h"
 
-#define MAXARGS 16
+#define MAXARGS 20
 
 typedef struct {
   napi_env env;
@@ -693,6 +693,38 @@ static napi_value MatmulMul(napi_env env, napi_callback_info info) {
                                         (const float*)bias, flags, mul, aux));
 }
 
+/* matmulQkNormRope(ctx, params, xDtype, x, wDtype, w, yDtype, y, bias, flags, qHeads, kHeads, eps, offset, normQ,
+ * normK, ropeFrom, cos, sin): we_matmul_qk_norm_rope */
+static napi_value MatmulQkNormRope(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 19)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  void* pdata = NULL;
+  size_t plen = 0;
+  bytes_of(&a, 1, &pdata, &plen);
+  int32_t xdt = i32_arg(&a, 2);
+  void* x = ptr_arg(&a, 3);
+  int32_t wdt = i32_arg(&a, 4);
+  void* w = ptr_arg(&a, 5);
+  int32_t ydt = i32_arg(&a, 6);
+  void* y = ptr_arg(&a, 7);
+  void* bias = ptr_arg(&a, 8);
+  uint32_t flags = u32_arg(&a, 9), qh = u32_arg(&a, 10), kh = u32_arg(&a, 11);
+  double eps = f64_arg(&a, 12), offset = f64_arg(&a, 13);
+  void *nq = ptr_arg(&a, 14), *nk = ptr_arg(&a, 15);
+  uint32_t rope_from = u32_arg(&a, 16);
+  void *c = ptr_arg(&a, 17), *sn = ptr_arg(&a, 18);
+  if (a.bad) return NULL;
+  if (plen != sizeof(we_matmul_params)) {
+    napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
+    return NULL;
+  }
+  return status(env, ctx, we_matmul_qk_norm_rope(ctx, (const we_matmul_params*)pdata, xdt, x, wdt, w, ydt, y,
+                                                 (const float*)bias, flags, qh, kh, (float)eps, (float)offset,
+                                                 (const float*)nq, (const float*)nk, rope_from, (const float*)c,
+                                                 (const float*)sn));
+}
+
 /* ---- norms, rotary, elementwise ---- */
 static napi_value RmsNorm(napi_env env, napi_callback_info info) {
   args_t a;
@@ -705,6 +737,22 @@ static napi_value RmsNorm(napi_env env, napi_callback_info info) {
   if (a.bad) return NULL;
   return status(env, ctx, we_rmsnorm(ctx, rows, d, (float)eps, (float)offset, dt, x, (const float*)wt,
                                      (const float*)sc, (const float*)sh, out));
+}
+
+/* rmsnormMod(ctx, rows, d, eps, offset, dtype, x, weight, tvec, table, modN, mod, out): we_rmsnorm_mod */
+static napi_value RmsNormMod(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 13)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t rows = u32_arg(&a, 1), d = u32_arg(&a, 2);
+  double eps = f64_arg(&a, 3), offset = f64_arg(&a, 4);
+  int32_t dt = i32_arg(&a, 5);
+  void *x = ptr_arg(&a, 6), *wt = ptr_arg(&a, 7), *tv = ptr_arg(&a, 8), *tb = ptr_arg(&a, 9);
+  uint32_t mod_n = u32_arg(&a, 10);
+  void *mod = ptr_arg(&a, 11), *out = ptr_arg(&a, 12);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_rmsnorm_mod(ctx, rows, d, (float)eps, (float)offset, dt, x, (const float*)wt,
+                                         (const float*)tv, (const float*)tb, mod_n, (float*)mod, out));
 }
 
 static napi_value Rope(napi_env env, napi_callback_info info) {
@@ -1099,8 +1147,8 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},
-      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul},
-      {"rmsnorm", RmsNorm},       {"rope", Rope},             {"elementwise", Elementwise},
+      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul}, {"matmulQkNormRope", MatmulQkNormRope},
+      {"rmsnorm", RmsNorm},       {"rmsnormMod", RmsNormMod},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
       {"timerStart", TimerStart}, {"timerStop", TimerStop},

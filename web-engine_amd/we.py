@@ -97,8 +97,11 @@ SIGNATURES = {
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
     "we_matmul_mul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _I, _P]),
+    "we_matmul_qk_norm_rope": (_I, [_P, _P, _I, _P, _I, _P, _I, _P, _P, _U32, _U32, _U32, _F, _F, _P, _P, _U32, _P,
+                                    _P]),
     "we_matmul_noalloc": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_rmsnorm": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _P]),
+    "we_rmsnorm_mod": (_I, [_P, _U32, _U32, _F, _F, _I, _P, _P, _P, _P, _U32, _P, _P]),
     "we_rope": (_I, [_P, _U32, _U32, _U32, _I, _I, _P, _P, _P, _P]),
     "we_qk_norm_rope": (_I, [_P, _U32, _U32, _U32, _F, _F, _P, _U32, _I, _P, _P, _I, _P, _U32, _P, _U32]),
     "we_attention": (_I, [_P, _U32, _U32, _U32, _U32, _I, _I, _P, _U32, _P, _U32, _P, _U32, _P, _U32]),
@@ -363,6 +366,15 @@ class Graph:
                                                 _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags,
                                                 _addr(gate), _addr(residual)))
 
+    def matmul_qk_norm_rope(self, params, x_dtype, x, w_dtype, w, y_dtype, y, q_heads, k_heads, eps, offset, norm_q,
+                            norm_k, rope_from=0, cos=None, sin=None, bias=None, flags=0):
+        """we_matmul_qk_norm_rope: a QKV projection whose q / k heads (128 wide) are RMS-normalized and rotated in
+        the GEMM's epilogue (or by a pass after it where no head-aligned tile fits)."""
+        self.check(self.lib.we_matmul_qk_norm_rope(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
+                                                   y_dtype, _addr(y), _addr(bias), flags, q_heads, k_heads, eps,
+                                                   offset, _addr(norm_q), _addr(norm_k), rope_from, _addr(cos),
+                                                   _addr(sin)))
+
     def matmul_noalloc(self, params, x_dtype, x, w_dtype, w, y_dtype, y, scales=None, group=0, bias=None, flags=0):
         """we_matmul_noalloc: we_matmul with its split-K scratch in the GPU's fixed array (allocates nothing)."""
         self.check(self.lib.we_matmul_noalloc(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
@@ -380,6 +392,11 @@ class Graph:
     def rmsnorm(self, rows, d, eps, offset, dtype, x, weight, scale, shift, out):
         self.check(self.lib.we_rmsnorm(self.ctx, rows, d, eps, offset, dtype, _addr(x), _addr(weight), _addr(scale),
                                        _addr(shift), _addr(out)))
+
+    def rmsnorm_mod(self, rows, d, eps, offset, dtype, x, weight, tvec, table, mod_n, mod, out):
+        """we_rmsnorm_mod: mod = tvec + table (mod_n f32) and out = rmsnorm(x) modulated by mod[0:d], mod[d:2d]."""
+        self.check(self.lib.we_rmsnorm_mod(self.ctx, rows, d, eps, offset, dtype, _addr(x), _addr(weight), _addr(tvec),
+                                           _addr(table), mod_n, _addr(mod), _addr(out)))
 
     def rope(self, tokens, heads, pairs, half, dtype, x, cos, sin, out):
         self.check(self.lib.we_rope(self.ctx, tokens, heads, pairs, 1 if half else 0, dtype, _addr(x), _addr(cos),
