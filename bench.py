@@ -13,8 +13,10 @@ is launched on):
   * roofline_int4: the int4 decode GEMV (M = 1, K = 3584, N = 18944, group 64): algorithmic bytes per
     launch (every tensor read or written once) over its average launch time, against HBM peak; 10
     weight copies rotate (> 256 MB) so no launch reads its weights from the Infinity Cache; M = 8 and 16
-    are reported beside it. These launches (~12 us) are shorter than the host's launch path, so they are
-    timed as replays of a HIP graph of 20 launches (HIP events around the replays, no host gaps);
+    are reported beside it. These launches (~10 us) are shorter than the host's launch path, so they are
+    timed as replays of a HIP graph of 20 launches (HIP events around the replays, no host gaps). A plain
+    streaming read of one weight copy (we_read_peak, same rotation and timing) is the same-size probe the
+    GEMV's rate is also reported against;
   * the dense bf16 GEMM at the DiT QKV shape and the small fp8 GEMM (M = 64);
   * c5_double_block: the double-stream DiT block (512 text + 4096 image tokens, hidden 3072, 24 heads,
     fp8 weights, bf16 activations) with its weights resident, the per-block weight copy from pinned host
@@ -140,6 +142,19 @@ def bench_int4(g, rng, iters=200, copies=10):
                         "frac_hbm": nbytes / ms / 1e6 / PEAK_HBM_GBS}
         g.free(x)
         g.free(y)
+    # the same-size read probe: one streaming read of a weight copy (we_read_peak), the same rotation and graph
+    # timing, i.e. what one launch that only reads these bytes achieves on this box
+    wbytes = n * k // 2
+    pout = g.buffer(we.read_peak_out_words(wbytes) * 4)
+
+    def probe(i):
+        g.read_peak(ws[i % copies], wbytes, pout)
+
+    for i in range(copies):
+        probe(i)
+    ms = time_graph(g, probe, 2 * copies, iters // (2 * copies))
+    out["read_probe_same_size"] = {"bytes": wbytes, "us": ms * 1e3, "gbs": wbytes / ms / 1e6}
+    g.free(pout)
     for b in ws + ss:
         g.free(b)
     return out
@@ -495,7 +510,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["mlp", "int4", "block", "all"], default="all")
+    ap.add_argument("--only", choices=["mlp", "int4", "block", "gemm", "all"], default="all")
     ap.add_argument("--sweep", action="store_true",
                     help="time every GEMM tile configuration on the sweep shapes and print that table instead")
     args = ap.parse_args()
@@ -520,7 +535,7 @@ def main():
     if args.only in ("block", "all"):
         extra["c5_double_block"] = bench_block(g, rng)
         print("[bench] block done", file=sys.stderr, flush=True)
-    if args.only == "all":
+    if args.only in ("gemm", "all"):
         extra["c2_bf16_qkv_4096x9216x3072"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
         extra["c1_fp8_64x3072x3072"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16)
     extra["calibration"] = calibration_copy(g)
@@ -554,8 +569,9 @@ def main():
         m1 = int4["M1"]
         line["roofline_int4"] = {"bound": "hbm", "achieved": m1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                  "frac": m1["gbs"] / PEAK_HBM_GBS, "traffic": measured_traffic("int4_decode_m1"),
-                                 "kernel": "int4_gemv_pipe_kernel<f16> M=1 K=3584 N=18944 group 64",
-                                 "algorithmic": f"{m1['bytes']} B per launch / {m1['us']:.2f} us"}
+                                 "kernel": "int4_gemv_direct_kernel<7> M=1 K=3584 N=18944 group 64 (f16 x)",
+                                 "algorithmic": f"{m1['bytes']} B per launch / {m1['us']:.2f} us",
+                                 "frac_of_same_size_read_probe": m1["gbs"] / int4["read_probe_same_size"]["gbs"]}
         if peaks:
             line["roofline_int4"]["frac_of_measured_peak"] = m1["gbs"] / peaks["hbm_read_gbs"]
     line.update(extra)
