@@ -473,10 +473,37 @@ constexpr int PP_NS = 4;
 // 32 reads first, runs out of registers and moves O between register ranges on every tile. Each
 // accumulator sees its MFMAs in the order of attn_pv16 / attn_scores16, so the results are the same.
 constexpr int PP_LA = 3;
-template <bool IS_F16, bool PV, bool SC>
+typedef short attn_v4s __attribute__((ext_vector_type(4)));
+
+// Per-lane constants of the transposing V read (VTR): the V tile sits in LDS key-major like the K tile (rows of
+// 128 dims, 16-byte chunk c of row r at chunk c ^ (r & 15)). ds_read_b64_tr_b16 hands lane 4a + b of each
+// 16-lane group element b of the 4-value rows that lanes a, a + 4, a + 8, a + 12 address (measured on gfx950).
+// Lane 4q + a' of a group therefore addresses key kq + q of dims d0 + 4a' .. + 3, and lane 4a + b receives
+// keys kq .. kq + 3 of dim d0 + 4a + b: the 16 lanes get 16 consecutive dims. With the group's dims
+// 32 db + (lane & 16) + (0..15) and kq = 4 hf (then 8 + 4 hf), a lane gathers the 8 keys {4hf .. 4hf + 3,
+// 8 + 4hf .. 8 + 4hf + 3} of its dim 32 db + c: the k order of its P fragment.
+struct VtrLane {
+  uint32_t base1, base2;  // byte offsets of (key kq + q, sub-chunk) for the two reads, before the chunk term
+  uint32_t k1, k2;        // kq + q of the two reads (the XOR swizzle key)
+  uint32_t cc;            // the lane's chunk inside its 32-dim block: (lane & 16) / 8 + a' / 2
+};
+
+__device__ __forceinline__ VtrLane vtr_lane(int lane) {
+  const int hf = lane >> 5, q = (lane & 15) >> 2, ap = lane & 3;
+  VtrLane v;
+  v.k1 = (uint32_t)(4 * hf + q);
+  v.k2 = v.k1 + 8u;
+  v.cc = (uint32_t)(((lane & 16) >> 3) + (ap >> 1));
+  const uint32_t sub = (uint32_t)(ap & 1) * 8u;
+  v.base1 = v.k1 * 256u + sub;
+  v.base2 = v.k2 * 256u + sub;
+  return v;
+}
+
+template <bool IS_F16, bool PV, bool SC, bool VTR = false>
 __device__ __forceinline__ void attn_mphase16(const char* vt, const char* ks, const u32x4 (&qf)[1][8],
                                               const u32x4 (&pf)[1][4], f32x16 (&o)[1][4], f32x16 (&sacc)[1][2],
-                                              int c, int hf) {
+                                              int c, int hf, const VtrLane& vl = VtrLane{}) {
   constexpr int N = (PV ? 16 : 0) + (SC ? 16 : 0);
   // step i is P V^T step i / 2 (even i) or scores step i / 2 (odd i) when both run, so the MFMAs of one
   // accumulator are 4 (P V^T) or 8 (scores) apart and none waits on the previous one's result
@@ -484,7 +511,16 @@ __device__ __forceinline__ void attn_mphase16(const char* vt, const char* ks, co
   constexpr auto idx = [](int i) { return PV && SC ? i / 2 : i; };
   auto frag = [&](auto I) -> u32x4 {
     constexpr int i = I;
-    if constexpr (is_pv(i)) {
+    if constexpr (is_pv(i) && VTR) {
+      constexpr int s = idx(i) / 4, db = idx(i) % 4;  // dims 32 db + c, keys 16 s .. 16 s + 15 of the V tile
+      const char* t = vt + s * 16 * 256;
+      const uint32_t o1 = vl.base1 + ((((uint32_t)(4 * db) + vl.cc) ^ vl.k1) << 4);
+      const uint32_t o2 = vl.base2 + ((((uint32_t)(4 * db) + vl.cc) ^ vl.k2) << 4);
+      const attn_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_v4s*)(t + o1));
+      const attn_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_v4s*)(t + o2));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      return u32x4{l2.x, l2.y, h2.x, h2.y};
+    } else if constexpr (is_pv(i)) {
       constexpr int s = idx(i) / 4, db = idx(i) % 4;  // V^T rows 32 db + c, keys 16 s .. 16 s + 15
       const int r = 32 * db + c;
       return *(const u32x4*)(vt + r * ATT_BN * 2 + (((2 * s + hf) ^ ((r >> 1) & 7)) << 4));
@@ -516,12 +552,13 @@ __device__ __forceinline__ void attn_mphase16(const char* vt, const char* ks, co
   });
 }
 
+// V tiles reach LDS key-major through the same direct-to-LDS loads as K (no V^T pre-pass); the P V^T
+// fragments are gathered from them by ds_read_b64_tr_b16 (VtrLane).
 template <bool IS_F16, bool CAUSAL>
-__global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint16_t* vtg, uint32_t tp,
-                                                         uint32_t kv_heads) {
+__global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, uint32_t kv_heads) {
   constexpr int DP = 128, NW = 8, IPW = 2;
   constexpr int KS_BYTES = ATT_BN * DP * 2;  // 16 KB
-  constexpr int STAGE = 2 * KS_BYTES;        // K + V^T
+  constexpr int STAGE = 2 * KS_BYTES;        // K + V
   __shared__ __attribute__((aligned(1024))) char lds[PP_NS * STAGE];
 
   uint32_t qblk, h;
@@ -546,10 +583,11 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
   const uint32_t kv_end = CAUSAL ? min(a.tokens, q0 + DMA_BM) : a.tokens;
   const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
   const uint32_t k_bytes = ((a.tokens - 1) * a.ks + kv_heads * DP) * 2;
+  const uint32_t v_bytes = ((a.tokens - 1) * a.vs + kv_heads * DP) * 2;
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.k, (short)0, (int)k_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vtg, (short)0, (int)(kv_heads * DP * tp * 2), 0x00020000);
-  // instruction j (0 .. 15) fills K rows 4j .. 4j + 3, or V^T rows 8j .. 8j + 7; wave w issues j = w + 8u
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)a.v, (short)0, (int)v_bytes, 0x00020000);
+  // instruction j (0 .. 15) fills K rows 4j .. 4j + 3, or V rows 4j .. 4j + 3 (keys past the last token load
+  // zeros); wave w issues j = w + 8u
   auto issue = [&](int t) {
     const uint32_t k0 = (uint32_t)t * ATT_BN;
     char* base = lds + (t % PP_NS) * STAGE;
@@ -563,10 +601,12 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
 #pragma unroll
     for (int u = 0; u < IPW; u++) {
       const int j = wave + NW * u;
-      const int row = 8 * j + (lane >> 3), phys = lane & 7, logical = phys ^ ((row >> 1) & 7);
-      dma16(rv, base + KS_BYTES + j * 1024, ((g * DP + row) * tp + k0 + logical * 8) * 2);
+      const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ (row & 15);
+      const uint32_t key = k0 + row;
+      dma16(rv, base + KS_BYTES + j * 1024, key < a.tokens ? (key * a.vs + g * DP + logical * 8) * 2 : kAttInvalid);
     }
   };
+  const VtrLane vl = vtr_lane(lane);
   // own loads of tile t complete; the tiles issued after it (at most PP_NS - 1) may still be in flight
   auto wait_tile = [&](int t) {
     const int ahead = min(nt - 1, max(PP_NS - 1, t + 1)) - t;
@@ -583,7 +623,7 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
   // tile t contributes to this wave's queries (causal: not entirely after them)
   auto active = [&](int t) { return !CAUSAL || (uint32_t)t * ATT_BN <= qw[0] + 31; };
   const char* kst = lds;             // K of tile t: kst + (t % PP_NS) * STAGE
-  const char* vst = lds + KS_BYTES;  // V^T of tile t
+  const char* vst = lds + KS_BYTES;  // V of tile t (key-major)
 
   f32x16 o[1][DP / 32];
   static_for<0, DP / 32>([&](auto D) { o[0][D] = f32x16{}; });
@@ -609,7 +649,7 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
     if (grp == 0 && t >= 2 && t + 2 < nt) issue(t + 2);
     const int cs = (t % PP_NS) * STAGE, ps = ((t - 1) % PP_NS) * STAGE;
     // causal: the scores of a tile no query of this wave sees are computed and left unused
-    if (active(t - 1)) attn_mphase16<IS_F16, true, true>(vst + ps, kst + cs, qf, pf, o, sacc, c, hf);
+    if (active(t - 1)) attn_mphase16<IS_F16, true, true, true>(vst + ps, kst + cs, qf, pf, o, sacc, c, hf, vl);
     if (grp == 1 && t + 1 < nt) wait_tile(t + 1);
     barrier();
     if (grp == 1 && t + 3 < nt) issue(t + 3);
@@ -637,7 +677,8 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, const uint1
     }
   }
   // M(nt): the last P V^T
-  if (active(nt - 1)) attn_mphase16<IS_F16, true, false>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c, hf);
+  if (active(nt - 1))
+    attn_mphase16<IS_F16, true, false, true>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c, hf, vl);
   if (grp == 0) barrier();  // both groups pass the same number of barriers
   attn_store16<DP, IS_F16>(o[0], l[0], qi[0], h, hf, a);
 }
@@ -772,10 +813,25 @@ hipError_t launch_attn(Kern kern, const AttnArgs& a, hipStream_t s) {
 
 }  // namespace
 
-size_t attention_scratch_bytes(const AttnLaunch& L) {
-  if (L.dtype == F32 || L.dim != 128 || L.tokens == 0 || L.heads == 0) return 0;
+namespace {
+// head dim 128, 16-bit, operand extents within the 32-bit buffer offsets: the DMA kernels
+bool attn_dma_ok(const AttnLaunch& L) {
+  if (L.dtype == F32 || L.dim != 128 || L.tokens == 0 || L.heads == 0) return false;
   const char* path = getenv("WE_ATTN_PATH");
-  if (path && strcmp(path, "registers") == 0) return 0;
+  if (path && strcmp(path, "registers") == 0) return false;
+  const uint64_t kb = ((uint64_t)(L.tokens - 1) * L.k_stride + (uint64_t)L.kv_heads * 128) * 2;
+  const uint64_t vb = ((uint64_t)(L.tokens - 1) * L.v_stride + (uint64_t)L.kv_heads * 128) * 2;
+  return kb < kAttInvalid && vb < kAttInvalid;
+}
+bool attn_ring_path() {
+  const char* path = getenv("WE_ATTN_PATH");
+  return path && strcmp(path, "ring") == 0;
+}
+}  // namespace
+
+// Only the ring kernel (WE_ATTN_PATH=ring) stages V^T through scratch; the default kernel reads V as it is.
+size_t attention_scratch_bytes(const AttnLaunch& L) {
+  if (!attn_dma_ok(L) || !attn_ring_path()) return 0;
   const size_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
   return (size_t)L.kv_heads * 128 * tp * 2;
 }
@@ -797,24 +853,24 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
   a.os = L.out_stride;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)L.dim);
   a.causal = L.causal;
-  if (L.scratch && attention_scratch_bytes(L) > 0) {
-    // head dim 128, 16-bit: V^T pre-pass, then the DMA-ring kernel
-    const uint32_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
-    uint16_t* vt = (uint16_t*)L.scratch;
-    hipLaunchKernelGGL(attn_vt_kernel, dim3(tp / 64, L.kv_heads), dim3(256), 0, s, (const uint16_t*)L.v, L.v_stride,
-                       L.tokens, tp, vt);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+  if (attn_dma_ok(L)) {
     a.nqb = (L.tokens + DMA_BM - 1) / DMA_BM;
     const dim3 grid(a.nqb * L.heads);
-    const char* path = getenv("WE_ATTN_PATH");
-    if (path && strcmp(path, "ring") == 0) {
+    if (attn_ring_path()) {
+      // the ring kernel: V^T pre-pass into scratch, then the one-phase DMA ring
+      if (!L.scratch) return hipErrorInvalidValue;
+      const uint32_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
+      uint16_t* vt = (uint16_t*)L.scratch;
+      hipLaunchKernelGGL(attn_vt_kernel, dim3(tp / 64, L.kv_heads), dim3(256), 0, s, (const uint16_t*)L.v, L.v_stride,
+                         L.tokens, tp, vt);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
       if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
       else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
     } else {
       const auto kern = L.dtype == F16 ? (L.causal ? attn_pp_kernel<true, true> : attn_pp_kernel<true, false>)
                                        : (L.causal ? attn_pp_kernel<false, true> : attn_pp_kernel<false, false>);
-      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
+      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
     }
     return hipGetLastError();
   }
