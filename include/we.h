@@ -160,6 +160,14 @@ int we_matmul_params_make(we_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, float
                           int64_t w_stride, int64_t y_stride, int64_t x_offset, int64_t w_offset, int64_t y_offset,
                           int64_t k_split, we_matmul_params* out);
 uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
+/* conv3x3Params (src/kernels/matmul.ts:268-272): the Params of a 3x3 convolution with padding 1 as a GEMM:
+ * M = height * width pixels, N = cout, K = 9 * cin, width and cin set; fails with "cin must be a multiple of 4,
+ * got <cin>". we_matmul with these Params reads x as a channel-last image [height, width, cin] (row m a pixel,
+ * k over (tap, channel), the 9 neighbours gathered in the kernel with zeros outside the image: the conv3x3 input
+ * of src/kernels/matmul.ts:74-83) and W as [cout, (ky, kx, cin)]. Plain epilogues only (scale, bias, GELU,
+ * accumulate, split-K); no int4 weights. */
+int we_conv3x3_params(we_ctx* ctx, uint32_t height, uint32_t width, uint32_t cin, uint32_t cout,
+                      we_matmul_params* out);
 
 /* y = x . W^T * scale with W [N, K] as stored (fp8 / bf16 / f16 / f32 / int4). Replaces matmulWgsl
  * (src/kernels/matmul.ts:118-178) dispatched by linear() (src/model/ops.ts:61-73).

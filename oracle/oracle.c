@@ -259,6 +259,20 @@ int or_matmul_params_make(uint32_t m, uint32_t n, uint32_t k, float scale, int64
 }
 
 /* src/model/ops.ts:38-45 — BUSY = 256 workgroups, MIN_SLICE = 256, TILE = 128. */
+/* src/kernels/matmul.ts:268-272 — conv3x3Params: M = height * width pixels, N = cout, K = 9 * cin, the conv
+ * input fields set; "cin must be a multiple of 4, got <cin>". */
+int or_conv3x3_params(uint32_t height, uint32_t width, uint32_t cin, uint32_t cout, or_matmul_params* out, char* msg,
+                      size_t msg_len) {
+  if (cin % 4) {
+    if (msg) snprintf(msg, msg_len, "cin must be a multiple of 4, got %u", cin);
+    return -1;
+  }
+  if (or_matmul_params_make(height * width, cout, 9 * cin, 1.0f, -1, -1, -1, -1, -1, -1, 1, out, msg, msg_len)) return -1;
+  out->width = width;
+  out->cin = cin;
+  return 0;
+}
+
 uint32_t or_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
   const uint32_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
   uint32_t want = (256 + tiles - 1) / tiles;
@@ -276,6 +290,16 @@ static double load_x(int dtype, const void* x, size_t i) {
     case OR_BF16: return or_bf16(((const uint16_t*)x)[i]);
     default: return ((const float*)x)[i];
   }
+}
+
+/* src/kernels/matmul.ts:74-83 — the conv3x3 input: x is a channel-last image [M / width, width, cin], row r is
+ * pixel r, k runs over (tap, channel): tap = k / cin reads pixel (r / width + tap / 3 - 1, r % width + tap % 3 - 1),
+ * zero outside the image. */
+static double load_x_conv(const or_matmul_params* p, int dtype, const void* x, uint32_t r, uint32_t kk) {
+  const uint32_t tap = kk / p->cin, c = kk % p->cin;
+  const int px = (int)(r % p->width) + (int)(tap % 3u) - 1, py = (int)(r / p->width) + (int)(tap / 3u) - 1;
+  if (px < 0 || py < 0 || px >= (int)p->width || py >= (int)(p->m / p->width)) return 0.0;
+  return load_x(dtype, x, ((size_t)py * p->width + (size_t)px) * p->cin + c);
 }
 
 static double load_w(int dtype, const void* w, const uint16_t* scales, uint32_t scales_per_row, uint32_t group,
@@ -312,7 +336,8 @@ static void matmul_rows(const or_matmul_params* p, int x_dtype, const void* x, i
       for (uint32_t c = 0; c < p->n; c++) {
         double s = 0.0;
         for (uint32_t kk = kb; kk < ke; kk++) {
-          const double xv = load_x(x_dtype, x, (size_t)p->x_offset + (size_t)r * p->x_stride + kk);
+          const double xv = p->width ? load_x_conv(p, x_dtype, x, r, kk)
+                                     : load_x(x_dtype, x, (size_t)p->x_offset + (size_t)r * p->x_stride + kk);
           const size_t widx = (size_t)p->w_offset + (size_t)c * p->w_stride + kk;
           s += xv * load_w(w_dtype, w, w_scales, spr, group, c, kk, widx);
         }

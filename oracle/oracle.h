@@ -58,6 +58,8 @@ int or_matmul_params_make(uint32_t m, uint32_t n, uint32_t k, float scale, int64
                           int64_t y_stride, int64_t x_offset, int64_t w_offset, int64_t y_offset, int64_t k_split,
                           or_matmul_params* out, char* msg, size_t msg_len);
 uint32_t or_ksplit_for(uint32_t m, uint32_t n, uint32_t k);
+int or_conv3x3_params(uint32_t height, uint32_t width, uint32_t cin, uint32_t cout, or_matmul_params* out, char* msg,
+                      size_t msg_len);
 
 /* ---- strong CPU baseline (cpu_gemm.c): y = scale * x . W^T (then tanh GELU when `gelu`), f32 accumulation,
  * `threads` host threads, AVX-512 when `avx512` and the host has it; contiguous layout, y dtype F32 / F16 / BF16.

@@ -20,6 +20,7 @@ const REF = {
 REF.matmulFp8Wgsl = REF.matmulWgsl("fp8");
 REF.matmulBf16Wgsl = REF.matmulWgsl("bf16");
 REF.matmulF32Wgsl = REF.matmulWgsl("f32");
+REF.conv3x3Wgsl = REF.matmulWgsl("f32", "conv3x3");
 const registered = we.registerKernels(REF);
 
 /** src/kernels/rmsnorm.ts:52-57 */
@@ -135,6 +136,12 @@ async function runCase(graph, c) {
       const out = graph.buffer(c.sizes[0] * 4);
       graph.run(REF[c.code], [graph.buffer(new Uint32Array([c.sizes[0], c.sizes[1] || 1])), ...inputs, out], [1]);
       return out;
+    }
+    case "runConv": {  // src/model/vae.ts:134-135: conv3x3Params, then Graph.run(conv3x3Wgsl, ...)
+      const { shape, params } = we.conv3x3Params(c.h, c.w, c.cin, c.cout, graph);
+      const y = graph.buffer(shape.m * shape.n * 4);
+      graph.run(REF.conv3x3Wgsl, [graph.buffer(params), load(graph, c.x), load(graph, c.weight), y], [1, 1]);
+      return y;
     }
     case "runUnknown":
       graph.run("// a shader with no MI355X kernel", [graph.buffer(new Uint32Array(2))], [1]);

@@ -50,6 +50,7 @@ def _load():
         "or_torch_randn": (None, [sz, ctypes.c_uint64, P]),
         "or_matmul_params_make": (ctypes.c_int, [u32, u32, u32, f, i64, i64, i64, i64, i64, i64, i64, P, P, sz]),
         "or_ksplit_for": (u32, [u32, u32, u32]), "or_ksplit_chunk": (u32, [u32, u32]),
+        "or_conv3x3_params": (ctypes.c_int, [u32, u32, u32, u32, P, P, sz]),
         "or_matmul_f64": (None, [P, ctypes.c_int, P, ctypes.c_int, P, P, u32, ctypes.c_int, P]),
         "or_matmul_f64_rows": (None, [P, ctypes.c_int, P, ctypes.c_int, P, P, u32, u32, u32, P]),
         "or_layer_sum": (None, [u32, u32, u32, P, P, P]),
@@ -187,6 +188,15 @@ def cpu_matmul(m, n, k, scale, x_dtype, x, w_dtype, w, scales=None, group=0, y_d
     if rc != 0:
         raise ValueError("cb_matmul refused its arguments")
     return y
+
+
+def conv3x3_params(height, width, cin, cout):
+    """conv3x3Params (src/kernels/matmul.ts:268-272); raises ValueError with the reference's message."""
+    p = Params()
+    msg = ctypes.create_string_buffer(200)
+    if lib.or_conv3x3_params(height, width, cin, cout, ctypes.byref(p), msg, 200):
+        raise ValueError(msg.value.decode())
+    return p
 
 
 def ksplit_for(m, n, k):

@@ -638,3 +638,58 @@ def test_product_epilogue_refusals(graph):
     with pytest.raises(we.WeError, match="int4 weights have no product epilogue") as e:
         graph.matmul(p, we.F16, b, we.INT4, b, we.F32, b, scales=b, group=64, mul=we.MUL_SWIGLU, aux=b)
     assert e.value.code == 4
+
+
+# ---- the conv3x3 input mode (src/kernels/matmul.ts:74-83, conv3x3Params :268-272) ----
+
+def test_conv3x3_matches_the_direct_convolution(graph):  # tests/gpu/image.test.ts:11-30
+    h, w, cin, cout = 5, 7, 8, 12
+    u = O.lcg(5, h * w * cin + cout * 9 * cin)
+    x = (u[: h * w * cin] * 2 - 1).astype(np.float32)
+    wt = (u[h * w * cin:] * 2 - 1).astype(np.float32)
+    mark = graph.mark()
+    y = we.conv3x3(graph, graph.buffer(x), graph.buffer(wt), h, w, cin, cout)
+    got = graph.read(y, dtype=np.float32).astype(np.float64)
+    graph.release(mark)
+    want = O.matmul(O.conv3x3_params(h, w, cin, cout), O.F32, x, O.F32, wt)
+    assert np.abs(got - want).max() < 1e-5  # the reference test's bar
+
+
+@pytest.mark.parametrize("x_dt,w_dt,y_dt,flags", [(we.BF16, we.FP8, we.BF16, 0), (we.F16, we.F16, we.F32, we.EPI_BIAS),
+                                                  (we.F32, we.BF16, we.F32, we.EPI_GELU),
+                                                  (we.BF16, we.FP8, we.F32, we.EPI_SPLIT_K)])
+def test_conv3x3_dtypes_ragged_and_epilogues(graph, x_dt, w_dt, y_dt, flags):
+    """cin = 12 (8-value chunks straddle two taps), odd height and width, several tiles; against the oracle's
+    conv addressing (itself pinned by a direct convolution in test_oracle.py)."""
+    h, w, cin, cout = 19, 23, 12, 70
+    rng = np.random.default_rng(x_dt * 10 + w_dt)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(h * w * cin).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, cout, 9 * cin, w_dt)
+    p = we.conv3x3_params(h, w, cin, cout, graph=graph)
+    p.scale = 0.05
+    bias = rng.uniform(-1, 1, cout).astype(np.float32) if flags & we.EPI_BIAS else None
+    op = O.conv3x3_params(h, w, cin, cout)
+    op.scale = 0.05
+    if flags & we.EPI_SPLIT_K:
+        p.k_split = op.k_split = 3
+    got = run(graph, p, x_store, x_dt, w_store, w_dt, y_dt, flags=flags, bias=bias)
+    want = O.matmul(op, ox, x_oracle, ow, w_oracle, split=bool(flags & we.EPI_SPLIT_K))
+    if bias is not None:
+        want = want + np.tile(bias.astype(np.float64), h * w)
+    if flags & we.EPI_GELU:
+        want = O.gelu_tanh(want)
+    tol = 1e-4 if flags & we.EPI_GELU else TOL[y_dt]
+    assert O.rel_error(got, want) < tol
+
+
+def test_conv3x3_refusals(graph):
+    with pytest.raises(we.WeError, match="cin must be a multiple of 4, got 6"):
+        we.conv3x3_params(4, 4, 6, 8, graph=graph)
+    p = we.conv3x3_params(4, 4, 8, 8, graph=graph)
+    b = graph.buffer(65536)
+    p.k = 64
+    with pytest.raises(we.WeError, match="K = 9 \\* cin"):
+        graph.matmul(p, we.F32, b, we.F32, b, we.F32, b)
+    p = we.conv3x3_params(4, 4, 8, 8, graph=graph)
+    with pytest.raises(we.WeError, match="int4 weights have no 3x3 convolution input"):
+        graph.matmul(p, we.F16, b, we.INT4, b, we.F32, b, scales=b, group=64)

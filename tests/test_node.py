@@ -38,7 +38,7 @@ EXPORTS = {
     "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_host_span": "hostSpan", "we_stream_copy": "streamCopy",
     "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
     "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
-    "we_ksplit_for": "kSplitFor", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_mul": "matmulMul", "we_matmul_qk_norm_rope": "matmulQkNormRope", "we_rmsnorm": "rmsnorm", "we_rmsnorm_mod": "rmsnormMod",
+    "we_ksplit_for": "kSplitFor", "we_conv3x3_params": "conv3x3Params", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_mul": "matmulMul", "we_matmul_qk_norm_rope": "matmulQkNormRope", "we_rmsnorm": "rmsnorm", "we_rmsnorm_mod": "rmsnormMod",
     "we_rope": "rope",
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
@@ -121,6 +121,7 @@ def test_graph_run_table_and_its_errors():
 const we = require("./index.js");
 const ref = { matmulWgsl: (w, i = "rows", { splitK = false, accumulate = false } = {}) => `m ${w} ${splitK} ${accumulate}`,
   rmsnormWgsl: "n", ropeKernel: (p) => `r ${p}`, ropeWgsl: "r interleaved", layerSumWgsl: "l", swigluWgsl: "s",
+  conv3x3Wgsl: "c3",
   sigmoidGateWgsl: "sg", gatedAddWgsl: "ga", addBiasWgsl: "ab", geluTanhWgsl: "g", addWgsl: "a", siluWgsl: "si" };
 const out = { count: we.registerKernels(ref) };
 const g = Object.create(we.Graph.prototype);
@@ -129,7 +130,7 @@ try { g.run("n", [null, null], [1]); } catch (e) { out.count6 = e.message; }
 try { g.run("ga", [null, null, null, null], [1]); } catch (e) { out.count5 = e.message; }
 try { we.registerKernels({ rmsnormWgsl: 3 }); } catch (e) { out.notText = e.message; }
 console.log(JSON.stringify(out));''')
-    assert got["count"] == 20
+    assert got["count"] == 21
     assert got["unknown"].startswith('Graph.run: no MI355X kernel is registered for this shader ("unknown");')
     assert got["count6"] == "Graph.run: rmsnorm takes 6 bindings (Params first), got 2"
     assert got["count5"] == "Graph.run: elementwise takes 5 bindings (Params first), got 4"
@@ -319,6 +320,15 @@ def test_graph_steps_through_the_addon(tmp_path):
     checks["run_gatedAdd"] = checks["gatedAdd"]
     cases.append(dict(name="run_swiglu", op="runElementwise", code="swigluWgsl", inputs=[fa, fb], sizes=[ne]))
     checks["run_swiglu"] = checks["swiglu"]
+    # a 3x3 convolution through Graph.run(conv3x3Wgsl) (tests/gpu/image.test.ts:11-30 data and bar)
+    hc, wc, cin, cout = 5, 7, 8, 12
+    uc = O.lcg(5, hc * wc * cin + cout * 9 * cin)
+    xc = (uc[: hc * wc * cin] * 2 - 1).astype(np.float32)
+    wcv = (uc[hc * wc * cin:] * 2 - 1).astype(np.float32)
+    conv_want = O.matmul(O.conv3x3_params(hc, wc, cin, cout), O.F32, xc, O.F32, wcv)
+    cases.append(dict(name="run_conv", op="runConv", h=hc, w=wc, cin=cin, cout=cout, x=_write(tmp_path, "xc", xc),
+                      weight=_write(tmp_path, "wc", wcv)))
+    checks["run_conv"] = (np.float32, lambda g: np.abs(g - conv_want).max() < 1e-5)
     cases.append(dict(name="run_unknown", op="runUnknown", expectError=True))
 
     (tmp_path / "spec.json").write_text(json.dumps(dict(cases=cases)))
@@ -332,7 +342,7 @@ def test_graph_steps_through_the_addon(tmp_path):
     assert result["errors"]["lora_rank3"] == "LoRA shapes do not fit the linear layer"
     assert result["errors"]["run_unknown"].startswith("Graph.run: no MI355X kernel is registered for this shader")
     assert len(result["errors"]) == 2
-    assert result["registered"] == 20  # 9 matmul variants, rmsnorm, 2 rope pairings, layer sum, 7 elementwise
+    assert result["registered"] == 21  # 9 matmul variants, conv3x3, rmsnorm, 2 rope pairings, layer sum, 7 elementwise
     assert result["concurrentReads"] == [1, 2, 3]
     assert result["reusedDelta"] >= 1 and result["zeroed"]
     failed = []

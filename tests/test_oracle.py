@@ -588,3 +588,39 @@ def test_rmsnorm_oracle_matches_torch_golden():
         # a dropped offset or eps cannot pass
         assert np.abs(O.rmsnorm(x, w, c["eps"], 1.0 - c["offset"], sc if c["modulated"] else None,
                                 sh if c["modulated"] else None) - want).max() > 1e-3
+
+
+def _direct_conv3x3(x, weight, h, w, cin, cout):
+    """tests/gpu/image.test.ts:16-28: the direct 3x3 convolution with zero padding, channel-last, in float64."""
+    xi = x.astype(np.float64).reshape(h, w, cin)
+    wt = weight.astype(np.float64).reshape(cout, 3, 3, cin)
+    pad = np.zeros((h + 2, w + 2, cin))
+    pad[1:-1, 1:-1] = xi
+    out = np.zeros((h, w, cout))
+    for ky in range(3):
+        for kx in range(3):
+            out += pad[ky:ky + h, kx:kx + w] @ wt[:, ky, kx, :].T
+    return out.ravel()
+
+
+def test_conv3x3_input_mode_equals_the_direct_convolution():
+    """The im2col addressing of the conv3x3 input (src/kernels/matmul.ts:74-83) through the oracle's GEMM equals
+    a direct convolution, on the reference test's data (tests/gpu/image.test.ts:11-30: LCG seed 5, x then weight,
+    values 2u - 1 as f32) and on a larger ragged case; the params carry the reference's check."""
+    h, w, cin, cout = 5, 7, 8, 12
+    u = O.lcg(5, h * w * cin + cout * 9 * cin)
+    x = (u[: h * w * cin] * 2 - 1).astype(np.float32)
+    wt = (u[h * w * cin:] * 2 - 1).astype(np.float32)
+    got = O.matmul(O.conv3x3_params(h, w, cin, cout), O.F32, x, O.F32, wt)
+    assert np.abs(got - _direct_conv3x3(x, wt, h, w, cin, cout)).max() < 1e-12
+    rng = np.random.default_rng(4)
+    h, w, cin, cout = 9, 13, 12, 20
+    x = rng.standard_normal(h * w * cin).astype(np.float32)
+    wt = rng.standard_normal(cout * 9 * cin).astype(np.float32)
+    got = O.matmul(O.conv3x3_params(h, w, cin, cout), O.F32, x, O.F32, wt)
+    assert np.abs(got - _direct_conv3x3(x, wt, h, w, cin, cout)).max() < 1e-10
+    # a mistake check: the taps are (ky, kx) = (tap / 3, tap % 3), not transposed
+    wrong = _direct_conv3x3(x, wt.reshape(cout, 3, 3, cin).transpose(0, 2, 1, 3).copy(), h, w, cin, cout)
+    assert np.abs(got - wrong).max() > 1.0
+    with pytest.raises(ValueError, match="cin must be a multiple of 4, got 6"):
+        O.conv3x3_params(4, 4, 6, 8)

@@ -37,6 +37,9 @@ struct GemmArgs {
   uint32_t y_dtype;
   uint32_t aligned;   // 1: every 16-B chunk of x / W rows is 16-B aligned
   uint32_t mul;       // product epilogue with res (GemmLaunch::mul), 0: none
+  // 3x3 convolution input (conv_width > 0): x is a channel-last image [m / conv_width rows, conv_width, conv_cin],
+  // row m of the GEMM is a pixel and k runs over (tap, channel) (src/kernels/matmul.ts:74-83)
+  uint32_t conv_width, conv_cin;
 };
 
 // Planes per operand: 1 when the stored type is exact in the MFMA type; f16 under a bf16 MFMA needs
@@ -143,6 +146,39 @@ __device__ __forceinline__ void load_chunk(const void* base, size_t row_off, boo
   }
 }
 
+// Eight k values [k, k + 8) of pixel `row` for the 3x3 convolution input, as load_chunk packs them: k runs over
+// (tap, channel) with K = 9 * cin, tap t reads pixel (py + t / 3 - 1, px + t % 3 - 1), zeros outside the image
+// (src/kernels/matmul.ts:74-83). cin is a multiple of 4, so each group of 4 values lies inside one tap.
+template <int SRC>
+__device__ __forceinline__ void load_conv8(const GemmArgs& a, uint32_t row, bool row_ok, uint32_t k, uint32_t k_end,
+                                           u32x4* raw) {
+  constexpr int BYTES = SRC == F32 ? 4 : 2;
+  uint32_t words[8 * BYTES / 4];
+#pragma unroll
+  for (int i = 0; i < 8 * BYTES / 4; i++) words[i] = 0;
+  const uint32_t width = a.conv_width, height = a.m / a.conv_width;
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    const uint32_t kk = k + 4u * g;
+    if (!row_ok || kk >= k_end) continue;
+    const uint32_t tap = kk / a.conv_cin, ch = kk % a.conv_cin;
+    const int px = (int)(row % width) + (int)(tap % 3u) - 1, py = (int)(row / width) + (int)(tap / 3u) - 1;
+    if (px < 0 || py < 0 || px >= (int)width || py >= (int)height) continue;
+    const size_t e = ((size_t)py * width + (size_t)px) * a.conv_cin + ch;
+    if constexpr (SRC == F32) {
+      const u32x4 v = *(const u32x4*)((const float*)a.x + e);
+#pragma unroll
+      for (int i = 0; i < 4; i++) words[4 * g + i] = v[i];
+    } else {
+      const u32x2 v = *(const u32x2*)((const uint16_t*)a.x + e);
+      words[2 * g] = v.x;
+      words[2 * g + 1] = v.y;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2 * BYTES / 4; i++) raw[i] = u32x4{words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]};
+}
+
 // One output value: y = val, y += val (accumulate), y = res + val (gated residual) or the product epilogue with
 // res, in the output dtype.
 __device__ __forceinline__ void store_out(const GemmArgs& a, size_t o, float val) {
@@ -229,8 +265,11 @@ gemm_kernel(GemmArgs a) {
       const int idx = i * C::T + tid;
       const int r = idx >> 3, c = idx & 7;
       const uint32_t row = row0 + r;
-      load_chunk<AT, 8>(a.x, (size_t)a.x_offset + (size_t)row * a.x_stride, row < a.m, kb + c * 8, k_end, aligned,
-                        ra[i]);
+      if (a.conv_width)
+        load_conv8<AT>(a, row, row < a.m, kb + c * 8, k_end, ra[i]);
+      else
+        load_chunk<AT, 8>(a.x, (size_t)a.x_offset + (size_t)row * a.x_stride, row < a.m, kb + c * 8, k_end, aligned,
+                          ra[i]);
     }
 #pragma unroll
     for (int i = 0; i < C::B_ITERS; i++) {
@@ -427,7 +466,7 @@ int pick_gemm_cfg(uint32_t m, uint32_t n, uint32_t splits) {
 }
 
 hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream) {
-  if (!L.generic) {
+  if (!L.generic && !L.conv_width) {
     const hipError_t e = gemm_fast_launch(L, stream);
     if (e != hipErrorNotSupported) return e;
   }
@@ -451,6 +490,8 @@ hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream) {
   a.flags = L.flags;
   a.y_dtype = (uint32_t)L.y_dtype;
   a.mul = (uint32_t)L.mul;
+  a.conv_width = L.conv_width;
+  a.conv_cin = L.conv_cin;
   const uint32_t splits = L.splits < 1 ? 1 : L.splits;
   a.kc = splits > 1 ? L.kc : L.k;
   const int xb = L.x_dtype == F32 ? 4 : 2;

@@ -762,6 +762,7 @@ namespace {
 // Do the operands qualify for the fast path? (16-bit activations, fp8 or matching 16-bit weights, 16-byte
 // aligned rows, K a multiple of 16, operand extents under the 32-bit buffer offsets.)
 bool fast_supported(const GemmLaunch& L, uint32_t kc) {
+  if (L.conv_width) return false;  // the 3x3 convolution input gathers x in the general kernel
   const bool f16 = L.x_dtype == F16;
   if (!(L.x_dtype == BF16 || L.x_dtype == F16)) return false;
   if (!(L.w_dtype == FP8 || (f16 ? L.w_dtype == F16 : L.w_dtype == BF16))) return false;

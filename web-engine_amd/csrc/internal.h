@@ -44,6 +44,9 @@ struct GemmLaunch {
   const float* qk_norm_k;
   const float* qk_cos;
   const float* qk_sin;
+  // 3x3 convolution input (conv_width > 0, the general kernel only): x is a channel-last image
+  // [m / conv_width, conv_width, conv_cin] and k runs over (tap, channel), K = 9 * conv_cin
+  uint32_t conv_width, conv_cin;
   int x_dtype, w_dtype, y_dtype;
   uint32_t m, n, k;
   float scale;

@@ -687,6 +687,15 @@ int we_matmul_params_make(we_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, float
   return WE_OK;
 }
 
+int we_conv3x3_params(we_ctx* ctx, uint32_t height, uint32_t width, uint32_t cin, uint32_t cout,
+                      we_matmul_params* out) {
+  if (!out) return fail(ctx, WE_EINVAL, "params output is null");
+  if (cin % 4) return fail(ctx, WE_EINVAL, "cin must be a multiple of 4, got %u", cin);
+  const uint32_t m = height * width, k = 9 * cin;
+  *out = we_matmul_params{m, cout, k, 1.0f, k, k, cout, 0, 0, 0, width, cin, 1};
+  return WE_OK;
+}
+
 uint32_t we_ksplit_for(uint32_t m, uint32_t n, uint32_t k) {
   const uint32_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
   const uint32_t want = (256 + tiles - 1) / tiles, cap = k / 256;
@@ -777,7 +786,17 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
                 const float* gate, const void* res, bool noalloc, int mul, const QkFuse* qk) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
-  if (p->width || p->cin) return fail(ctx, WE_EUNSUPPORTED, "conv3x3 input mode is not part of this path");
+  const bool conv = p->width || p->cin;
+  if (conv) {
+    // the 3x3 convolution input (src/kernels/matmul.ts:74-83, conv3x3Params :268-272)
+    if (!p->width || !p->cin || p->cin % 4) return fail(ctx, WE_EINVAL, "cin must be a multiple of 4, got %u", p->cin);
+    if (p->k != 9 * p->cin) return fail(ctx, WE_EINVAL, "a 3x3 convolution has K = 9 * cin (K %u, cin %u)", p->k, p->cin);
+    if (p->m % p->width) return fail(ctx, WE_EINVAL, "M (%u pixels) is not a whole number of rows of width %u", p->m,
+                                    p->width);
+    if (w_dtype == WE_INT4) return fail(ctx, WE_EUNSUPPORTED, "int4 weights have no 3x3 convolution input");
+    if (gate || res || mul || qk) return fail(ctx, WE_EUNSUPPORTED, "the 3x3 convolution input takes plain epilogues");
+    if ((uintptr_t)x % 16) return fail(ctx, WE_EINVAL, "the convolution's image must be 16-byte aligned");
+  }
   {
     const char* names[5] = {"K", "xStride", "wStride", "xOffset", "wOffset"};
     const uint32_t vals[5] = {p->k, p->x_stride, p->w_stride, p->x_offset, p->w_offset};
@@ -797,7 +816,8 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
 
   // extents of every operand (in bytes), so that no launch can read or write outside its buffers
   const uint64_t xb = elem_bytes(x_dtype), yb = elem_bytes(y_dtype);
-  const uint64_t x_need = p->k ? ((uint64_t)p->x_offset + (uint64_t)(p->m - 1) * p->x_stride + p->k) * xb : 0;
+  const uint64_t x_need = conv ? (uint64_t)p->m * p->cin * xb
+                               : p->k ? ((uint64_t)p->x_offset + (uint64_t)(p->m - 1) * p->x_stride + p->k) * xb : 0;
   const uint64_t y_rows = (uint64_t)p->m * splits;
   const uint64_t y_need = ((uint64_t)p->y_offset + (y_rows - 1) * p->y_stride + p->n) * yb;
   int rc = check_span(ctx, x, x_need, "x");
@@ -859,6 +879,8 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   L.gate = gate;
   L.res = res;
   L.mul = mul;
+  L.conv_width = conv ? p->width : 0;
+  L.conv_cin = conv ? p->cin : 0;
   L.x_dtype = x_dtype;
   L.w_dtype = w_dtype;
   L.y_dtype = y_dtype;

@@ -51,6 +51,7 @@ export interface ReferenceKernels {
   matmulFp8Wgsl?: string;
   matmulBf16Wgsl?: string;
   matmulF32Wgsl?: string;
+  conv3x3Wgsl?: string;
   rmsnormWgsl?: string;
   ropeKernel?: (pairing: "interleaved" | "half") => string;
   ropeWgsl?: string;
@@ -165,6 +166,9 @@ export function matmulParams(shape: { m: number; n: number; k: number }, scale: 
                              layout?: { xStride?: number; wStride?: number; yStride?: number; xOffset?: number;
                                         wOffset?: number; yOffset?: number; kSplit?: number },
                              graph?: Graph | null): Uint32Array;
+/** src/kernels/matmul.ts:268-272 */
+export function conv3x3Params(height: number, width: number, cin: number, cout: number, graph?: Graph | null):
+  { shape: { m: number; n: number; k: number }; params: Uint32Array };
 /** src/model/ops.ts:42 */
 export function kSplitFor(m: number, n: number, k: number): number;
 /** src/model/ops.ts:61 */

@@ -34,9 +34,9 @@ const SHADOW_MAX = 256; // buffers made from data up to this size keep a host co
  * Fills Graph.run's table from the reference's kernel exports, given by their reference names (e.g. the modules
  * src/kernels/matmul.ts, rmsnorm.ts, rope.ts, elementwise.ts and text.ts spread into one object):
  *   matmulWgsl (the function, src/kernels/matmul.ts:118: fp8 / bf16 / f32 weights x plain, splitK, accumulate),
- *   matmulFp8Wgsl / matmulBf16Wgsl / matmulF32Wgsl, rmsnormWgsl, ropeKernel or ropeWgsl / ropeHalfWgsl,
+ *   matmulFp8Wgsl / matmulBf16Wgsl / matmulF32Wgsl, conv3x3Wgsl, rmsnormWgsl, ropeKernel or ropeWgsl / ropeHalfWgsl,
  *   layerSumWgsl, and swigluWgsl, sigmoidGateWgsl, gatedAddWgsl, addBiasWgsl, geluTanhWgsl, addWgsl, siluWgsl.
- * Returns how many sources the table maps. Shaders outside this list (conv3x3, attention parts, the VAE's) have
+ * Returns how many sources the table maps. Shaders outside this list (attention parts, the VAE's others) have
  * no MI355X kernel here, and Graph.run throws for them.
  */
 function registerKernels(ref) {
@@ -53,7 +53,8 @@ function registerKernels(ref) {
           { op: "matmul", weights: DTYPES[w], flags: EPI.ACCUMULATE });
     }
   }
-  for (const [name, w] of [["matmulFp8Wgsl", FP8], ["matmulBf16Wgsl", BF16], ["matmulF32Wgsl", F32]])
+  // conv3x3Wgsl (src/kernels/matmul.ts:183) is the f32 matmul with the conv input; its Params say so
+  for (const [name, w] of [["matmulFp8Wgsl", FP8], ["matmulBf16Wgsl", BF16], ["matmulF32Wgsl", F32], ["conv3x3Wgsl", F32]])
     if (ref[name] !== undefined) put(name, ref[name], { op: "matmul", weights: w, flags: 0 });
   if (ref.rmsnormWgsl !== undefined) put("rmsnormWgsl", ref.rmsnormWgsl, { op: "rmsnorm" });
   if (ref.ropeKernel !== undefined) {
@@ -404,6 +405,12 @@ function matmulParams({ m, n, k }, scale, layout = {}, graph = null) {
                             l.wOffset, l.yOffset, l.kSplit == null ? 1 : l.kSplit);
 }
 
+/** src/kernels/matmul.ts:268-272: { shape, params } of a 3x3 convolution as a GEMM, with the same error. */
+function conv3x3Params(height, width, cin, cout, graph = null) {
+  const params = addon.conv3x3Params(graph ? graph.ctx : null, height, width, cin, cout);
+  return { shape: { m: height * width, n: cout, k: 9 * cin }, params };
+}
+
 /** src/model/ops.ts:42-45 */
 const kSplitFor = (m, n, k) => addon.kSplitFor(m, n, k);
 
@@ -556,7 +563,7 @@ function readTensor(st, tensor, limit, dst, threads, offset = 0) {
 
 module.exports = {
   addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP, MUL,
-  matmulParams, kSplitFor, linear, norm, noMod, rotate, attention,
+  matmulParams, conv3x3Params, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
   SafetensorsError, readHeader, readTensor, registerKernels,
   lastError: (graph) => addon.lastError(graph ? graph.ctx : null),

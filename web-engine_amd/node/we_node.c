@@ -593,6 +593,24 @@ static napi_value MatmulParams(napi_env env, napi_callback_info info) {
   return arr;
 }
 
+/* conv3x3Params(ctx, height, width, cin, cout) -> the 13 x u32 Params image (src/kernels/matmul.ts:268-272) */
+static napi_value Conv3x3Params(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 5)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t h = u32_arg(&a, 1), w = u32_arg(&a, 2), cin = u32_arg(&a, 3), cout = u32_arg(&a, 4);
+  if (a.bad) return NULL;
+  we_matmul_params p;
+  int rc = we_conv3x3_params(ctx, h, w, cin, cout, &p);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  void* data;
+  napi_value ab, arr;
+  napi_create_arraybuffer(env, sizeof p, &data, &ab);
+  memcpy(data, &p, sizeof p);
+  napi_create_typedarray(env, napi_uint32_array, sizeof p / 4, ab, 0, &arr);
+  return arr;
+}
+
 static napi_value KSplitFor(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 3)) return NULL;
@@ -1147,7 +1165,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},
-      {"matmulParams", MatmulParams}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul}, {"matmulQkNormRope", MatmulQkNormRope},
+      {"matmulParams", MatmulParams}, {"conv3x3Params", Conv3x3Params}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul}, {"matmulQkNormRope", MatmulQkNormRope},
       {"rmsnorm", RmsNorm},       {"rmsnormMod", RmsNormMod},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},

@@ -94,6 +94,7 @@ SIGNATURES = {
     "we_timer_stop": (_I, [_P, _P]),
     "we_matmul_params_make": (_I, [_P, _U32, _U32, _U32, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "we_ksplit_for": (_U32, [_U32, _U32, _U32]),
+    "we_conv3x3_params": (_I, [_P, _U32, _U32, _U32, _U32, _P]),
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
     "we_matmul_mul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _I, _P]),
@@ -440,6 +441,27 @@ def matmul_params(m, n, k, scale, x_stride=None, w_stride=None, y_stride=None, x
     if rc:
         raise WeError(rc, lib.we_last_error(ctx).decode())  # ctx None: this thread's context-free message
     return p
+
+
+def conv3x3_params(height, width, cin, cout, graph=None):
+    """conv3x3Params (src/kernels/matmul.ts:268-272): Params under which matmul is a 3x3 convolution (padding 1)
+    of a channel-last image [height, width, cin] with W [cout, (ky, kx, cin)]."""
+    lib = load_library()
+    p = MatmulParams()
+    ctx = graph.ctx if graph is not None else None
+    rc = lib.we_conv3x3_params(ctx, height, width, cin, cout, ctypes.byref(p))
+    if rc:
+        raise WeError(rc, lib.we_last_error(ctx).decode())
+    return p
+
+
+def conv3x3(graph, x, w, height, width, cin, cout, x_dtype=F32, w_dtype=F32, y_dtype=F32, scale=1.0):
+    """The one-shot conv3x3 of src/kernels/matmul.ts:275-279 on device buffers: y [height * width, cout]."""
+    p = conv3x3_params(height, width, cin, cout, graph=graph)
+    p.scale = scale
+    y = graph.buffer(height * width * cout * ELEM_BYTES[y_dtype])
+    graph.matmul(p, x_dtype, x, w_dtype, w, y_dtype, y)
+    return y
 
 
 def k_split_for(m, n, k):
