@@ -286,12 +286,29 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     };
+    // fp8 with 4 x 2 MFMAs per step (the 128 x 64 wave tile): the weight fragments of the block are unpacked at
+    // the end of the memory phase, which is shorter than the compute phase, so the compute phase issues its 32
+    // MFMAs back to back (2-3% off the 4096 x 12288 x 3072 and 4096 x 3072 x 12288 projections). The 64 x 96
+    // wave tile (2 x 3 MFMAs per step, 24 unpacks) keeps them between its MFMAs: moved, they made its memory
+    // phase the longer one (4% slower).
+    constexpr bool PRE_CVT = B8 && TM >= 4;
+    u32x4 wcv[PRE_CVT ? 4 : 1][TN];
     auto memory_block = [&](uint32_t st_off) {
 #pragma unroll
       for (int q = 0; q < 4; q++) read_x(st_off, q, xb[q]);
 #pragma unroll
       for (int q = 0; q < (B8 ? 2 : 4); q++) read_w(st_off, q, wb[q]);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if constexpr (PRE_CVT) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            const u32x4 r = wb[q >> 1][j];
+            const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
+            wcv[q][j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          }
+      }
     };
     auto compute_block = [&]() {
       static_for<0, 4>([&](auto Q) {
@@ -299,7 +316,9 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         u32x4 w[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-          if constexpr (B8) {
+          if constexpr (PRE_CVT) {
+            w[j] = wcv[q][j];
+          } else if constexpr (B8) {
             const u32x4 r = wb[q >> 1][j];
             const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
             w[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
@@ -807,16 +826,17 @@ bool fast_supported(const GemmLaunch& L, uint32_t kc) {
 
 constexpr uint32_t kCUs = 256;
 
-// Tile shape by predicted speed. score = the tile shape's own speed relative to 256 x 256 (one per CU, the
-// fastest per FLOP) times util^0.3, util being the fraction of workgroup slots busy over the launch's rounds (the
-// last round of tiles is partly empty). The weak exponent is measured: the chip runs at its power limit, so a
-// partly empty last round runs at higher clocks and costs far less than a full one. Both factors come from the
-// tile sweep (bench.py --sweep; bf16 activations, fp8 weights, M = 4096 and 8740): 256 x 192 does 0.93 of
-// 256 x 256's work per unit time at equal occupancy, 128 x 128 (two per CU) 0.86, 256 x 128 0.83; 8740 x 6144 x
-// 6144 at util 0.82 still runs fastest in 256 x 256 tiles (1110 TFLOP/s against 1044 for 128 x 128 at 0.92),
-// while 4096 x 3072 x 12288 (256 x 256: one round at 0.75) goes to 256 x 192 (1191 against 1163).
-// With 16-bit weights 128 x 128 tiles fit one per CU only and lose to the ping-pong tiles
-// (4096 x 9216 x 3072 bf16: 780 against 1011 TFLOP/s), so only the two 256-row shapes compete there.
+// Tile shape by predicted speed: score = base x (tiles / slots) / (time in rounds). base is the tile shape's own
+// speed relative to 256 x 256 (one per CU, the fastest per FLOP) at full occupancy; a full round of tiles costs 1,
+// the last, partly filled round 0.6 + 0.3 f (f = the fraction of slots it fills). The chip runs at its power
+// limit, so tiles run faster when fewer CUs are busy, and a partial round costs far more than its share but less
+// than a full one. Fitted to the tile sweep (bench.py --sweep: bf16 activations and output, fp8 weights unless
+// named, M = 4096 and 8740). With fp8 weights 256 x 192 runs at 0.90 of 256 x 256's speed, 128 x 128 (two per CU)
+// at 0.81, 256 x 128 at 0.77. The tail term decides two shapes: 4096 x 3072 x 12288 (256 x 256: one round at
+// f = 0.75) stays with 256 x 256 (1288 against 1254 TFLOP/s for 256 x 192), while 4096 x 9216 x 3072 (256 x 256:
+// two full rounds and one at f = 0.25) goes to 256 x 192 (three full rounds; 7% faster). With 16-bit weights
+// 128 x 128 tiles fit one per CU only and lose to the ping-pong tiles (4096 x 9216 x 3072 bf16: 801 against 1085
+// TFLOP/s), so only the two 256-row shapes compete there, 256 x 192 at 0.95.
 int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
   if (m <= 32) return GEMM_CFG_32x64;
   if (m <= 64) return GEMM_CFG_64x64;
@@ -825,8 +845,8 @@ int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
     uint32_t bm, bn, per_cu;
     double base;
   };
-  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, 0.93},
-                        {GEMM_CFG_128x128, 128, 128, 2, 0.86}, {GEMM_CFG_256x128, 256, 128, 1, 0.83}};
+  const Cand cands[] = {{GEMM_CFG_256x256, 256, 256, 1, 1.00}, {GEMM_CFG_256x192, 256, 192, 1, w8 ? 0.90 : 0.95},
+                        {GEMM_CFG_128x128, 128, 128, 2, 0.81}, {GEMM_CFG_256x128, 256, 128, 1, 0.77}};
   int best = GEMM_CFG_128x128;
   double best_score = -1.0;
   for (const Cand& c : cands) {
@@ -834,8 +854,9 @@ int pick_fast_cfg(uint32_t m, uint32_t n, uint32_t splits, bool w8) {
     if (!w8 && c.cfg != GEMM_CFG_256x256 && c.cfg != GEMM_CFG_256x192) continue;
     const uint64_t tiles = (uint64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * splits;
     const uint64_t slots = (uint64_t)kCUs * c.per_cu;
-    const uint64_t waves = (tiles + slots - 1) / slots;
-    const double score = c.base * pow((double)tiles / (double)(waves * slots), 0.3);
+    const uint64_t full = tiles / slots, rest = tiles % slots;
+    const double rounds = (double)full + (rest ? 0.6 + 0.3 * (double)rest / (double)slots : 0.0);
+    const double score = c.base * ((double)tiles / (double)slots) / rounds;
     if (score > best_score + 1e-9) {
       best_score = score;
       best = c.cfg;
