@@ -224,6 +224,27 @@ int we_matmul_qk_norm_rope(we_ctx* ctx, const we_matmul_params* p, int x_dtype, 
                            uint32_t k_heads, float eps, float offset, const float* norm_q, const float* norm_k,
                            uint32_t rope_from, const float* cos_t, const float* sin_t);
 
+/* Two GEMMs of one N, K, dtypes and flags as one launch. No counterpart in the reference, which dispatches every
+ * linear() on its own (src/model/ops.ts:61-73): for callers with independent GEMMs of one shape, like a double-stream
+ * block whose text and image streams project with their own weights. Each item holds the arguments of one
+ * we_matmul_gated call (gate and residual NULL: a plain epilogue; bias with WE_EPI_BIAS). With 16-bit x, fp8 or
+ * matching 16-bit weights and 16-byte aligned rows, the tiles of both run in one launch with all of K per tile (no
+ * split-K), in the tile shape picked for the two row counts together: a small GEMM beside a large one then adds no
+ * launch and no partly empty round of tiles of its own. Each result equals a separate we_matmul_gated call made
+ * with that tile shape (WE_GEMM_CFG) and no split-K plan. Any other pair, and count 1, runs as separate calls in
+ * order. Every item is checked before anything is launched; count must be 1 or 2. */
+typedef struct we_matmul_item {
+  const we_matmul_params* p;
+  const void* x;
+  const void* w;
+  void* y;
+  const float* bias;
+  const float* gate;
+  const void* residual;
+} we_matmul_item;
+int we_matmul_group(we_ctx* ctx, uint32_t count, const we_matmul_item* items, int x_dtype, int w_dtype, int y_dtype,
+                    uint32_t flags);
+
 /* ---- norms and rotary: rmsnormWgsl (src/kernels/rmsnorm.ts:13-48) / norm() (src/model/ops.ts:78-82),
  * ropeKernel (src/kernels/rope.ts:59-77) / rotate() (src/model/ops.ts:89-93) ---- */
 /* out = x / sqrt(mean(x^2) + eps) * (offset + weight) * (1 + scale) + shift; scale/shift may be NULL */

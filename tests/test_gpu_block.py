@@ -281,10 +281,17 @@ def test_double_block_full_shape_sampled_rows_match_the_oracle(graph):
             rt if name == "text" else ri])).max() > 0.1
 
 
-def test_double_block_overlapped_streams_equal_serial(graph):
-    """The text stream on the second compute stream beside the image stream (the default) gives the serial
-    block's outputs bit for bit at the full shape (512 + 4096 tokens, hidden 3072, bf16), forward after
-    forward (the text GEMMs' split-K slices use that stream's own scratch)."""
+@pytest.mark.parametrize("grouped", [False, True])
+def test_double_block_overlapped_streams_equal_serial(graph, monkeypatch, grouped):
+    """The text stream on the second compute stream beside the image stream gives the serial block's outputs bit
+    for bit at the full shape (512 + 4096 tokens, hidden 3072, bf16), forward after forward (the text GEMMs'
+    split-K slices use that stream's own scratch). With the output and down projections of the two streams
+    grouped into one launch each (the default), the text tiles run in the image's tile shape with all of K, so
+    the serial block is run with that tile shape and no split-K (WE_GEMM_CFG, WE_GEMM_SPLITK) for the
+    comparison."""
+    if grouped:
+        monkeypatch.setenv("WE_GEMM_CFG", "0")
+        monkeypatch.setenv("WE_GEMM_SPLITK", "off")
     cfg, tt, rows, cols = B.DIT_DOUBLE_BLOCK, 512, 64, 64
     ti, H = rows * cols, cfg.hidden
     rng = np.random.default_rng(9)
@@ -299,7 +306,8 @@ def test_double_block_overlapped_streams_equal_serial(graph):
     w_t, w_i = layout.weights(slot, scales)
     outs = {}
     for overlap in (False, True):
-        blk = B.DoubleBlock(graph, cfg, tt, ti, we.BF16, overlap=overlap)
+        blk = B.DoubleBlock(graph, cfg, tt, ti, we.BF16, overlap=overlap, grouped=grouped)
+        assert blk.grouped == (grouped and overlap)
         out_t, out_i = graph.buffer(tt * H * 2), graph.buffer(ti * H * 2)
         for _ in range(2):
             blk.forward(w_t, w_i, bx_t, bx_i, tv, rope, out_t, out_i)

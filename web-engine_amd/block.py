@@ -150,9 +150,11 @@ class DoubleBlock:
     """The double-stream block at fixed token counts, with its workspace allocated once. With overlap (the
     default) the text stream's steps run on the context's second compute stream, beside the image stream's:
     the two streams meet only in the joint attention, and the text stream's small GEMMs fill workgroup slots
-    the image stream leaves free. The result is the same bit for bit."""
+    the image stream leaves free. With grouped (the default, with overlap) the output and down projections of
+    the two streams run as one launch each (we_matmul_group). The result is the same bit for bit as serial
+    calls that use the same tile shapes."""
 
-    def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16, overlap=True):
+    def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16, overlap=True, grouped=True):
         if cfg.heads != cfg.kv_heads or cfg.heads * cfg.head_dim != cfg.hidden:
             raise ValueError("the double-stream block needs heads == kvHeads and heads * headDim == hidden")
         self.graph, self.cfg, self.dtype = graph, cfg, dtype
@@ -164,6 +166,7 @@ class DoubleBlock:
         self.qkv = graph.buffer(self.tokens * 3 * H * e)
         self.o = graph.buffer(self.tokens * H * e)
         self.overlap = overlap
+        self.grouped = grouped and overlap  # the grouped projections use each stream's own buffers
         if overlap:  # each stream its own norm output and MLP hidden
             self.h = [graph.buffer(r * H * e) for r in self.rows]
             self.u = [graph.buffer(r * cfg.mlp * e) for r in self.rows]
@@ -235,10 +238,31 @@ class DoubleBlock:
             g.matmul(we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, u, we.FP8, w.down.buffer, dt,
                      outs[s], gate=sl(mod, 5 * H * 4, H * 4), residual=self.x1[s])
 
+        def out_grouped():
+            # the output and down projections of the two streams share N and K: each pair runs as one launch
+            # (we_matmul_group), the text tiles beside the image tiles in one round, with the gated residuals
+            # x1 = x + gate1 * proj(o) and out = x1 + gate2 * down(u) in the epilogues
+            g.matmul_group([dict(params=we.matmul_params(self.rows[s], H, H, ws[s].proj.scale, x_offset=self.row0[s] * H,
+                                                         graph=g),
+                                 x=self.o, w=ws[s].proj.buffer, y=self.x1[s], gate=sl(self.mod[s], 2 * H * 4, H * 4),
+                                 residual=xs[s]) for s in (0, 1)], dt, we.FP8, dt)
+            for s in (0, 1):
+                g.rmsnorm(self.rows[s], H, cfg.eps, 1.0, dt, self.x1[s], ws[s].norm2, sl(self.mod[s], 3 * H * 4, H * 4),
+                          sl(self.mod[s], 4 * H * 4, H * 4), self.h[s])
+            # the up projections differ in tile shape (128 x 128 text tiles fill the slots the image's leave)
+            self._streams(lambda s: g.matmul(we.matmul_params(self.rows[s], cfg.mlp, H, ws[s].up.scale, graph=g), dt,
+                                             self.h[s], we.FP8, ws[s].up.buffer, dt, self.u[s], flags=we.EPI_GELU))
+            g.matmul_group([dict(params=we.matmul_params(self.rows[s], H, cfg.mlp, ws[s].down.scale, graph=g),
+                                 x=self.u[s], w=ws[s].down.buffer, y=outs[s], gate=sl(self.mod[s], 5 * H * 4, H * 4),
+                                 residual=self.x1[s]) for s in (0, 1)], dt, we.FP8, dt)
+
         self._streams(qkv_step)
         g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
                     sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
-        self._streams(out_step)
+        if self.grouped:
+            out_grouped()
+        else:
+            self._streams(out_step)
 
 
 # ------------------------------------------------------------------------------------------ weight streaming

@@ -65,6 +65,19 @@ struct FastArgs {
   const float* qk_norm_k;
   const float* qk_cos;
   const float* qk_sin;
+  // A second GEMM in the same launch (gemm_fast_launch_pair): the same N, K, types, flags and product epilogue,
+  // operands of its own. Tiles from grp_first on (after the XCD renumbering) compute it; grp_first 0: none.
+  struct Second {
+    const void* x;
+    const void* w;
+    void* y;
+    const float* bias;
+    const float* gate;
+    const void* res;
+    uint32_t x_bytes, w_bytes, m, x_stride, w_stride, y_stride, y_offset, tiles_m, vec_store, store16;
+    float scale;
+  } g;
+  uint32_t grp, grp_first;
 };
 
 __device__ __forceinline__ uint32_t xcd_remap_f(uint32_t pid, uint32_t total) {
@@ -172,7 +185,27 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int h = lane >> 5, l32 = lane & 31;
 
-  const uint32_t pid = xcd_remap_f(blockIdx.x, gridDim.x);
+  uint32_t pid = xcd_remap_f(blockIdx.x, gridDim.x);
+  if (a.grp_first && pid >= a.grp_first) {  // a tile of the second GEMM of a paired launch
+    pid -= a.grp_first;
+    a.x = a.g.x;
+    a.w = a.g.w;
+    a.y = a.g.y;
+    a.bias = a.g.bias;
+    a.gate = a.g.gate;
+    a.res = a.g.res;
+    a.x_bytes = a.g.x_bytes;
+    a.w_bytes = a.g.w_bytes;
+    a.m = a.g.m;
+    a.x_stride = a.g.x_stride;
+    a.w_stride = a.g.w_stride;
+    a.y_stride = a.g.y_stride;
+    a.y_offset = a.g.y_offset;
+    a.tiles_m = a.g.tiles_m;
+    a.vec_store = a.g.vec_store;
+    a.store16 = a.g.store16;
+    a.scale = a.g.scale;
+  }
   constexpr uint32_t GROUP_M = 4;
   const uint32_t per_group = GROUP_M * a.tiles_n;
   const uint32_t first_m = (pid / per_group) * GROUP_M;
@@ -766,7 +799,13 @@ template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S, bool PP = 
 static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
   a.tiles_n = (a.n + BN - 1) / BN;
-  const dim3 grid(a.tiles_m * a.tiles_n, splits), block(WM * WN * 64);
+  uint32_t tiles = a.tiles_m * a.tiles_n;
+  if (a.grp) {  // the second GEMM's tiles follow the first's
+    a.g.tiles_m = (a.g.m + BM - 1) / BM;
+    a.grp_first = tiles;
+    tiles += a.g.tiles_m * a.tiles_n;
+  }
+  const dim3 grid(tiles, splits), block(WM * WN * 64);
   if (a.rsplits > 1) {
     // slices store raw f32 sums (the output type does not matter to them), then one reduce pass
     hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32, PP>), grid, block, 0, s, a);
@@ -921,13 +960,10 @@ bool gemm_qk_fusable(const GemmLaunch& L) {
          (!L.bias || ((uintptr_t)L.bias % 4) == 0);
 }
 
-// Returns hipErrorNotSupported when the shape / dtypes / alignment are not for this path.
-hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
-  const bool reduce = L.rsplits > 1;
-  const uint32_t splits = reduce ? L.rsplits : (L.splits < 1 ? 1 : L.splits);
-  const uint32_t kc = reduce ? L.rkc : (splits > 1 ? L.kc : L.k);
-  if (!fast_supported(L, kc)) return hipErrorNotSupported;
-  const bool f16 = L.x_dtype == F16;
+namespace {
+
+// The kernel arguments of one GEMM (no split-K slices, no tile pick yet).
+FastArgs fast_args(const GemmLaunch& L, uint32_t kc) {
   const int wb = L.w_dtype == FP8 ? 1 : 2;
   const int yb = L.y_dtype == F32 ? 4 : 2;
   FastArgs a{};
@@ -968,6 +1004,19 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   a.store16 = ((uintptr_t)L.y % 16 == 0 && ((uint64_t)L.y_offset * yb) % 16 == 0 && ((uint64_t)L.y_stride * yb) % 16 == 0)
                   ? 1u
                   : 0u;
+  return a;
+}
+
+}  // namespace
+
+// Returns hipErrorNotSupported when the shape / dtypes / alignment are not for this path.
+hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
+  const bool reduce = L.rsplits > 1;
+  const uint32_t splits = reduce ? L.rsplits : (L.splits < 1 ? 1 : L.splits);
+  const uint32_t kc = reduce ? L.rkc : (splits > 1 ? L.kc : L.k);
+  if (!fast_supported(L, kc)) return hipErrorNotSupported;
+  const bool f16 = L.x_dtype == F16;
+  FastArgs a = fast_args(L, kc);
   if (reduce) {
     if (!L.scratch) return hipErrorInvalidValue;
     a.part = (float*)L.scratch;
@@ -980,6 +1029,36 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   }
   if (L.w_dtype == FP8) return launch_fast_types<false, FP8>(a, splits, cfg, stream);
   return launch_fast_types<false, BF16>(a, splits, cfg, stream);
+}
+
+bool gemm_pair_ok(const GemmLaunch& A, const GemmLaunch& B) {
+  for (const GemmLaunch* L : {&A, &B})
+    if (L->generic || L->conv_width || L->splits > 1 || L->qk_cols || (L->flags & WE_EPI_SPLIT_K_BIT) ||
+        !fast_supported(*L, L->k))
+      return false;
+  return A.n == B.n && A.k == B.k && A.x_dtype == B.x_dtype && A.w_dtype == B.w_dtype && A.y_dtype == B.y_dtype &&
+         A.flags == B.flags && A.mul == B.mul && A.cfg == B.cfg;
+}
+
+// Two GEMMs (gemm_pair_ok) as one launch: the tiles of both share the round(s) of workgroups, so a small GEMM
+// beside a large one costs no launch and no partly empty round of its own. Full K per tile (no split-K), the
+// tile shape picked for the two row counts together; each GEMM's tiles compute exactly as in a launch of its own
+// with the same tile shape.
+hipError_t gemm_fast_launch_pair(const GemmLaunch& A, const GemmLaunch& B, hipStream_t stream) {
+  if (!gemm_pair_ok(A, B)) return hipErrorNotSupported;
+  FastArgs a = fast_args(A, A.k);
+  const FastArgs b = fast_args(B, B.k);
+  a.g = FastArgs::Second{b.x,        b.w,        b.y,        b.bias,     b.gate,      b.res,
+                         b.x_bytes,  b.w_bytes,  b.m,        b.x_stride, b.w_stride,  b.y_stride,
+                         b.y_offset, 0u,         b.vec_store, b.store16, b.scale};
+  a.grp = 1;
+  const int cfg = A.cfg >= 0 ? A.cfg : pick_fast_cfg(A.m + B.m, A.n, 1, A.w_dtype == FP8);
+  if (A.x_dtype == F16) {
+    if (A.w_dtype == FP8) return launch_fast_types<true, FP8>(a, 1, cfg, stream);
+    return launch_fast_types<true, F16>(a, 1, cfg, stream);
+  }
+  if (A.w_dtype == FP8) return launch_fast_types<false, FP8>(a, 1, cfg, stream);
+  return launch_fast_types<false, BF16>(a, 1, cfg, stream);
 }
 
 }  // namespace we

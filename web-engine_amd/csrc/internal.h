@@ -61,6 +61,10 @@ struct GemmLaunch {
   void* scratch;
 };
 hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream);
+// Two GEMMs of one N, K, types and epilogue as one launch of the fast kernels (both through the fast path, full K);
+// gemm_pair_ok says whether a pair qualifies, gemm_fast_launch_pair refuses others with hipErrorNotSupported.
+bool gemm_pair_ok(const GemmLaunch& A, const GemmLaunch& B);
+hipError_t gemm_fast_launch_pair(const GemmLaunch& A, const GemmLaunch& B, hipStream_t stream);
 
 // The split-K plan of a launch on the fast path: rsplits > 1 when the output tiles alone would leave most
 // CUs idle (small M); the scratch it needs, in bytes.

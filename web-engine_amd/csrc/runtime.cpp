@@ -781,9 +781,13 @@ int we_matmul_qk_norm_rope(we_ctx* ctx, const we_matmul_params* p, int x_dtype, 
 }
 
 namespace {
-int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
-                const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
-                const float* gate, const void* res, bool noalloc, int mul, const QkFuse* qk) {
+// The checks every matmul entry point makes: the 3x3 convolution input's parameters, multiples of 4, dtypes,
+// flags, and the extents of x, y, bias, gate and the residual / aux operand, so that no launch can read or write
+// outside its buffers. Sets the split-K slice count and slice length; *empty when M or N is 0 (nothing to launch).
+int check_gemm(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, int y_dtype,
+               const void* y, const float* bias, uint32_t flags, const float* gate, const void* res, int mul,
+               const QkFuse* qk, uint32_t* splits_out, uint32_t* kc_out, bool* empty) {
+  *empty = true;
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (!p) return fail(ctx, WE_EINVAL, "params is null");
   const bool conv = p->width || p->cin;
@@ -811,7 +815,8 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     return fail(ctx, WE_EINVAL, "unknown epilogue flags 0x%x", flags);
   const bool split = (flags & WE_EPI_SPLIT_K) != 0;
   const uint32_t splits = split ? (p->k_split < 1 ? 1 : p->k_split) : 1;
-  if (p->m == 0 || p->n == 0) return WE_OK;
+  *empty = p->m == 0 || p->n == 0;
+  if (*empty) return WE_OK;
   const uint32_t kc = split ? ((p->k + splits - 1) / splits + 15) / 16 * 16 : p->k;
 
   // extents of every operand (in bytes), so that no launch can read or write outside its buffers
@@ -826,6 +831,61 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   if (!rc && gate) rc = check_span(ctx, gate, (uint64_t)p->n * 4, "gate");
   if (!rc && res) rc = check_span(ctx, res, y_need, mul ? "aux" : "residual");
   if (rc) return rc;
+  *splits_out = splits;
+  *kc_out = kc;
+  return WE_OK;
+}
+
+// The GemmLaunch of a checked matmul with 16-bit / fp8 / f32 weights: operands, shape, epilogue, and the
+// WE_GEMM_CFG / WE_GEMM_PATH overrides of sweeps and tests.
+void fill_gemm(we::GemmLaunch& L, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+               int y_dtype, void* y, const float* bias, uint32_t flags, const float* gate, const void* res, int mul,
+               uint32_t splits, uint32_t kc) {
+  const bool conv = p->width || p->cin;
+  L = we::GemmLaunch{};
+  L.x = x;
+  L.w = w;
+  L.y = y;
+  L.bias = bias;
+  L.gate = gate;
+  L.res = res;
+  L.mul = mul;
+  L.conv_width = conv ? p->width : 0;
+  L.conv_cin = conv ? p->cin : 0;
+  L.x_dtype = x_dtype;
+  L.w_dtype = w_dtype;
+  L.y_dtype = y_dtype;
+  L.m = p->m;
+  L.n = p->n;
+  L.k = p->k;
+  L.scale = p->scale;
+  L.x_stride = p->x_stride;
+  L.w_stride = p->w_stride;
+  L.y_stride = p->y_stride;
+  L.x_offset = p->x_offset;
+  L.w_offset = p->w_offset;
+  L.y_offset = p->y_offset;
+  L.splits = splits;
+  L.kc = kc;
+  L.flags = flags;
+  L.cfg = -1;
+  const char* force = getenv("WE_GEMM_CFG");
+  if (force && *force) L.cfg = atoi(force);
+  const char* path = getenv("WE_GEMM_PATH");
+  L.generic = (path && strcmp(path, "generic") == 0) ? 1 : 0;
+  L.rsplits = 1;
+  L.rkc = L.k;
+  L.scratch = nullptr;
+}
+
+int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
+                const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags,
+                const float* gate, const void* res, bool noalloc, int mul, const QkFuse* qk) {
+  uint32_t splits = 1, kc = 0;
+  bool empty = true;
+  int rc = check_gemm(ctx, p, x_dtype, x, w_dtype, y_dtype, y, bias, flags, gate, res, mul, qk, &splits, &kc, &empty);
+  if (rc || empty) return rc;
+  const bool split = (flags & WE_EPI_SPLIT_K) != 0;
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
 
   if (w_dtype == WE_INT4) {
@@ -871,40 +931,8 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   const uint64_t w_need = p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0;
   rc = check_span(ctx, w, w_need, "w");
   if (rc) return rc;
-  we::GemmLaunch L{};
-  L.x = x;
-  L.w = w;
-  L.y = y;
-  L.bias = bias;
-  L.gate = gate;
-  L.res = res;
-  L.mul = mul;
-  L.conv_width = conv ? p->width : 0;
-  L.conv_cin = conv ? p->cin : 0;
-  L.x_dtype = x_dtype;
-  L.w_dtype = w_dtype;
-  L.y_dtype = y_dtype;
-  L.m = p->m;
-  L.n = p->n;
-  L.k = p->k;
-  L.scale = p->scale;
-  L.x_stride = p->x_stride;
-  L.w_stride = p->w_stride;
-  L.y_stride = p->y_stride;
-  L.x_offset = p->x_offset;
-  L.w_offset = p->w_offset;
-  L.y_offset = p->y_offset;
-  L.splits = splits;
-  L.kc = kc;
-  L.flags = flags;
-  L.cfg = -1;
-  const char* force = getenv("WE_GEMM_CFG");
-  if (force && *force) L.cfg = atoi(force);
-  const char* path = getenv("WE_GEMM_PATH");
-  L.generic = (path && strcmp(path, "generic") == 0) ? 1 : 0;
-  L.rsplits = 1;
-  L.rkc = L.k;
-  L.scratch = nullptr;
+  we::GemmLaunch L;
+  fill_gemm(L, p, x_dtype, x, w_dtype, w, y_dtype, y, bias, flags, gate, res, mul, splits, kc);
   bool qk_fused = false;
   if (qk && qk->q_heads + qk->k_heads) {
     L.qk_cols = (qk->q_heads + qk->k_heads) * 128;
@@ -961,6 +989,48 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   return WE_OK;
 }
 }  // namespace
+
+int we_matmul_group(we_ctx* ctx, uint32_t count, const we_matmul_item* items, int x_dtype, int w_dtype, int y_dtype,
+                    uint32_t flags) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (count < 1 || count > 2) return fail(ctx, WE_EINVAL, "a matmul group holds 1 or 2 GEMMs, got %u", count);
+  if (!items) return fail(ctx, WE_EINVAL, "items is null");
+  // every item as we_matmul_gated would check it, before anything is launched
+  we::GemmLaunch L[2];
+  bool empty[2] = {true, true};
+  for (uint32_t i = 0; i < count; i++) {
+    const we_matmul_item& it = items[i];
+    if (it.gate && (flags & WE_EPI_SPLIT_K))
+      return fail(ctx, WE_EINVAL, "a gated residual does not combine with split-K partials");
+    if (it.residual && !it.gate) return fail(ctx, WE_EINVAL, "item %u: a residual needs a gate", i);
+    if (it.residual && (flags & WE_EPI_ACCUMULATE))
+      return fail(ctx, WE_EINVAL, "a residual replaces accumulate: pass y as the residual to add to y");
+    uint32_t splits = 1, kc = 0;
+    int rc = check_gemm(ctx, it.p, x_dtype, it.x, w_dtype, y_dtype, it.y, it.bias, flags, it.gate, it.residual, 0,
+                        nullptr, &splits, &kc, &empty[i]);
+    if (rc) return rc;
+    if (empty[i] || w_dtype == WE_INT4) continue;
+    const uint64_t wb = elem_bytes(w_dtype);
+    const we_matmul_params* p = it.p;
+    const uint64_t w_need = p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0;
+    rc = check_span(ctx, it.w, w_need, "w");
+    if (rc) return rc;
+    fill_gemm(L[i], p, x_dtype, it.x, w_dtype, it.w, y_dtype, it.y, it.bias, flags, it.gate, it.residual, 0, splits,
+              kc);
+  }
+  if (count == 2 && !empty[0] && !empty[1] && w_dtype != WE_INT4 && we::gemm_pair_ok(L[0], L[1])) {
+    HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    const hipError_t e = we::gemm_fast_launch_pair(L[0], L[1], ctx->compute);
+    return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "gemm pair launch");
+  }
+  for (uint32_t i = 0; i < count; i++) {
+    const we_matmul_item& it = items[i];
+    const int rc = matmul_impl(ctx, it.p, x_dtype, it.x, w_dtype, it.w, nullptr, 0, y_dtype, it.y, it.bias, flags,
+                               it.gate, it.residual);
+    if (rc) return rc;
+  }
+  return WE_OK;
+}
 
 // ------------------------------------------------------------------------------------------ peak probes
 

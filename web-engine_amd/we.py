@@ -59,6 +59,13 @@ class MatmulParams(ctypes.Structure):
                 ("width", ctypes.c_uint32), ("cin", ctypes.c_uint32), ("k_split", ctypes.c_uint32)]
 
 
+class MatmulItem(ctypes.Structure):
+    """we_matmul_item: the arguments of one GEMM of a we_matmul_group call."""
+    _fields_ = [("p", ctypes.POINTER(MatmulParams)), ("x", ctypes.c_void_p), ("w", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("residual", ctypes.c_void_p)]
+
+
 _P, _I, _U32, _U64, _SZ, _F, _I64 = (ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t,
                                      ctypes.c_float, ctypes.c_int64)
 SIGNATURES = {
@@ -98,6 +105,7 @@ SIGNATURES = {
     "we_matmul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
     "we_matmul_gated": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _P, _P]),
     "we_matmul_mul": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32, _I, _P]),
+    "we_matmul_group": (_I, [_P, _U32, _P, _I, _I, _I, _U32]),
     "we_matmul_qk_norm_rope": (_I, [_P, _P, _I, _P, _I, _P, _I, _P, _P, _U32, _U32, _U32, _F, _F, _P, _P, _U32, _P,
                                     _P]),
     "we_matmul_noalloc": (_I, [_P, _P, _I, _P, _I, _P, _P, _U32, _I, _P, _P, _U32]),
@@ -366,6 +374,20 @@ class Graph:
             self.check(self.lib.we_matmul_gated(self.ctx, ctypes.byref(params), x_dtype, _addr(x), w_dtype, _addr(w),
                                                 _addr(scales), group, y_dtype, _addr(y), _addr(bias), flags,
                                                 _addr(gate), _addr(residual)))
+
+    def matmul_group(self, items, x_dtype, w_dtype, y_dtype, flags=0):
+        """we_matmul_group: one or two GEMMs of one N, K, dtypes and flags; items are dicts with params, x, w, y and
+        optionally bias, gate, residual (the arguments of matmul). Two qualifying GEMMs run as one launch."""
+        arr = (MatmulItem * len(items))()
+        keep = []
+        for i, it in enumerate(items):
+            p = it["params"]
+            keep.append(p)
+            arr[i].p = ctypes.pointer(p)
+            for f in ("x", "w", "y", "bias", "gate", "residual"):
+                a = _addr(it.get(f))
+                setattr(arr[i], f, a.value if a is not None else None)
+        self.check(self.lib.we_matmul_group(self.ctx, len(items), arr, x_dtype, w_dtype, y_dtype, flags))
 
     def matmul_qk_norm_rope(self, params, x_dtype, x, w_dtype, w, y_dtype, y, q_heads, k_heads, eps, offset, norm_q,
                             norm_k, rope_from=0, cos=None, sin=None, bias=None, flags=0):
