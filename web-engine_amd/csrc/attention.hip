@@ -472,7 +472,7 @@ constexpr int PP_NS = 4;
 // the MFMAs. A scheduling barrier after every step keeps that order: left to itself the compiler issues all
 // 32 reads first, runs out of registers and moves O between register ranges on every tile. Each
 // accumulator sees its MFMAs in the order of attn_pv16 / attn_scores16, so the results are the same.
-constexpr int PP_LA = 3;
+constexpr int PP_LA = 5;
 typedef short attn_v4s __attribute__((ext_vector_type(4)));
 
 // Per-lane constants of the transposing V read (VTR): the V tile sits in LDS key-major like the K tile (rows of
