@@ -322,10 +322,11 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     // fp8 with 4 x 2 MFMAs per step (the 128 x 64 wave tile): the weight fragments of the block are unpacked at
     // the end of the memory phase, which is shorter than the compute phase, so the compute phase issues its 32
     // MFMAs back to back (2-3% off the 4096 x 12288 x 3072 and 4096 x 3072 x 12288 projections). The 64 x 96
-    // wave tile (2 x 3 MFMAs per step, 24 unpacks) keeps them between its MFMAs: moved, they made its memory
-    // phase the longer one (4% slower).
-    constexpr bool PRE_CVT = B8 && TM >= 4;
-    u32x4 wcv[PRE_CVT ? 4 : 1][TN];
+    // wave tile (2 x 3 MFMAs per step, 24 unpacks) unpacks only its first step there (1.7% off 4096 x 9216 x
+    // 3072) and the other three between its MFMAs: moving two or all four made its memory phase the longer one.
+    constexpr int PRE = !B8 ? 0 : TM >= 4 ? 4 : 1;  // steps unpacked in the memory phase
+    constexpr bool PRE_CVT = PRE > 0;
+    u32x4 wcv[PRE_CVT ? PRE : 1][TN];
     auto memory_block = [&](uint32_t st_off) {
 #pragma unroll
       for (int q = 0; q < 4; q++) read_x(st_off, q, xb[q]);
@@ -334,7 +335,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if constexpr (PRE_CVT) {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+        for (int q = 0; q < PRE; q++)
 #pragma unroll
           for (int j = 0; j < TN; j++) {
             const u32x4 r = wb[q >> 1][j];
@@ -349,8 +350,8 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         u32x4 w[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-          if constexpr (PRE_CVT) {
-            w[j] = wcv[q][j];
+          if constexpr (PRE_CVT && q < PRE) {
+            w[j] = wcv[q < PRE ? q : 0][j];
           } else if constexpr (B8) {
             const u32x4 r = wb[q >> 1][j];
             const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
