@@ -143,6 +143,17 @@ async function runCase(graph, c) {
       graph.run(REF.conv3x3Wgsl, [graph.buffer(params), load(graph, c.x), load(graph, c.weight), y], [1, 1]);
       return y;
     }
+    case "group": {  // two GEMMs as one launch (matmulGroup): item 0 plain, item 1 with a gated residual, one y
+      const y = graph.buffer((c.m0 + c.m1) * c.n * 4);
+      const res = load(graph, c.res);
+      graph.matmulGroup([
+        { params: we.matmulParams({ m: c.m0, n: c.n, k: c.k }, c.scale0, {}, graph), x: load(graph, c.x0),
+          w: load(graph, c.w0), y },
+        { params: we.matmulParams({ m: c.m1, n: c.n, k: c.k }, c.scale1, { yOffset: c.m0 * c.n }, graph),
+          x: load(graph, c.x1), w: load(graph, c.w1), y, gate: load(graph, c.gate), residual: res },
+      ], we.BF16, we.FP8, we.F32);
+      return y;
+    }
     case "runUnknown":
       graph.run("// a shader with no MI355X kernel", [graph.buffer(new Uint32Array(2))], [1]);
       return null;

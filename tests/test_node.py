@@ -38,7 +38,7 @@ EXPORTS = {
     "we_host_alloc": "hostAlloc", "we_host_free": "hostFree", "we_host_span": "hostSpan", "we_stream_copy": "streamCopy",
     "we_wait_ticket": "waitTicket", "we_ticket_done": "ticketDone", "we_record_compute": "recordCompute",
     "we_timer_start": "timerStart", "we_timer_stop": "timerStop", "we_matmul_params_make": "matmulParams",
-    "we_ksplit_for": "kSplitFor", "we_conv3x3_params": "conv3x3Params", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_mul": "matmulMul", "we_matmul_qk_norm_rope": "matmulQkNormRope", "we_rmsnorm": "rmsnorm", "we_rmsnorm_mod": "rmsnormMod",
+    "we_ksplit_for": "kSplitFor", "we_conv3x3_params": "conv3x3Params", "we_matmul": "matmul", "we_matmul_noalloc": "matmulNoalloc", "we_matmul_gated": "matmulGated", "we_matmul_group": "matmulGroup", "we_matmul_mul": "matmulMul", "we_matmul_qk_norm_rope": "matmulQkNormRope", "we_rmsnorm": "rmsnorm", "we_rmsnorm_mod": "rmsnormMod",
     "we_rope": "rope",
     "we_qk_norm_rope": "qkNormRope", "we_attention": "attention", "we_elementwise": "elementwise", "we_layer_sum": "layerSum",
     "we_unpack_fp8": "unpackFp8", "we_dequant_int4": "dequantInt4", "we_last_error": "lastError",
@@ -330,6 +330,24 @@ def test_graph_steps_through_the_addon(tmp_path):
                       weight=_write(tmp_path, "wc", wcv)))
     checks["run_conv"] = (np.float32, lambda g: np.abs(g - conv_want).max() < 1e-5)
     cases.append(dict(name="run_unknown", op="runUnknown", expectError=True))
+
+    # two GEMMs as one launch (matmulGroup, we_matmul_group): bf16 x, fp8 weights, f32 y; the second with the gated
+    # residual, written after the first in one y
+    mg0, mg1, ng, kg = 64, 300, 256, 256
+    rng = np.random.default_rng(11)
+    xg0, xg1 = (O.bf16_rne(rng.standard_normal(mm * kg).astype(np.float32)) for mm in (mg0, mg1))
+    wg0, wg1 = ((lambda v: (v + (v >= 0x7F)).astype(np.uint8))(rng.integers(0, 254, ng * kg)) for _ in range(2))
+    gg = rng.uniform(-1, 1, ng).astype(np.float32)
+    resg = np.zeros((mg0 + mg1) * ng, np.float32)
+    resg[mg0 * ng:] = rng.standard_normal(mg1 * ng).astype(np.float32)
+    v0 = O.matmul(O.matmul_params(mg0, ng, kg, 0.05), O.BF16, xg0, O.FP8, wg0)
+    v1 = O.matmul(O.matmul_params(mg1, ng, kg, 0.03), O.BF16, xg1, O.FP8, wg1).reshape(mg1, ng)
+    group_want = np.concatenate([v0, (resg[mg0 * ng:].reshape(mg1, ng) + gg.astype(np.float64) * v1).ravel()])
+    cases.append(dict(name="group", op="group", m0=mg0, m1=mg1, n=ng, k=kg, scale0=0.05, scale1=0.03,
+                      x0=_write(tmp_path, "xg0", xg0.view(np.uint16)), x1=_write(tmp_path, "xg1", xg1.view(np.uint16)),
+                      w0=_write(tmp_path, "wg0", wg0), w1=_write(tmp_path, "wg1", wg1), gate=_write(tmp_path, "gg", gg),
+                      res=_write(tmp_path, "resg", resg)))
+    checks["group"] = (np.float32, lambda g: O.rel_error(g, group_want) < 1e-5)
 
     (tmp_path / "spec.json").write_text(json.dumps(dict(cases=cases)))
     print(f"[node] {len(cases)} cases in {tmp_path}", flush=True)

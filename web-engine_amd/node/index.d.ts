@@ -110,6 +110,10 @@ export class Graph {
   matmul(params: Uint32Array, xDtype: DType, x: Binding, wDtype: DType, w: Binding, yDtype: DType, y: Binding,
          opts?: { scales?: Binding | null; group?: number; bias?: Binding | null; flags?: number; gate?: Binding | null;
                   residual?: Binding | null; mul?: 0 | 1 | 2; aux?: Binding | null }): void;
+  /** One or two GEMMs of one N, K, dtypes and flags as one launch (we_matmul_group). */
+  matmulGroup(items: Array<{ params: Uint32Array; x: Binding; w: Binding; y: Binding; bias?: Binding | null;
+                             gate?: Binding | null; residual?: Binding | null }>,
+              xDtype: DType, wDtype: DType, yDtype: DType, flags?: number): void;
   /** A QKV projection with the per-head RMSNorm + RoPE of its q / k heads (128 wide) fused in. */
   matmulQkNormRope(params: Uint32Array, xDtype: DType, x: Binding, wDtype: DType, w: Binding, yDtype: DType, y: Binding,
                    qHeads: number, kHeads: number, eps: number, offset: number, normQ: Binding, normK: Binding,

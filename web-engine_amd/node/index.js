@@ -303,6 +303,17 @@ class Graph {
     }
   }
 
+  /** One or two GEMMs of one N, K, dtypes and flags as one launch (matmulGroup): items are
+   * { params, x, w, y, bias, gate, residual } (bias, gate and residual optional, as in matmul). */
+  matmulGroup(items, xDtype, wDtype, yDtype, flags = 0) {
+    const args = [];
+    for (const it of items) {
+      args.push(it.params, ptrOf(it.x), ptrOf(it.w), ptrOf(it.y), ptrOf(it.bias), ptrOf(it.gate),
+                ptrOf(it.residual));
+    }
+    addon.matmulGroup(this.ctx, items.length, xDtype, wDtype, yDtype, flags, ...args);
+  }
+
   /** A QKV projection with the per-head RMSNorm + RoPE of its q / k heads (128 wide) fused in (the q/k path of
    * attend(), src/model/block.ts:53-56). */
   matmulQkNormRope(params, xDtype, x, wDtype, w, yDtype, y, qHeads, kHeads, eps, offset, normQ, normK,

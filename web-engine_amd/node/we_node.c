@@ -682,6 +682,43 @@ static napi_value MatmulGated(napi_env env, napi_callback_info info) {
                                           (const float*)bias, flags, (const float*)gate, res));
 }
 
+/* matmulGroup(ctx, count, xDtype, wDtype, yDtype, flags, then per item params, x, w, y, bias, gate, residual):
+ * we_matmul_group, one or two GEMMs of one N, K, dtypes and flags as one launch */
+static napi_value MatmulGroup(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 6)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t count = u32_arg(&a, 1);
+  int32_t xdt = i32_arg(&a, 2), wdt = i32_arg(&a, 3), ydt = i32_arg(&a, 4);
+  uint32_t flags = u32_arg(&a, 5);
+  if (a.bad) return NULL;
+  if (count < 1 || count > 2 || a.argc < 6 + 7 * (size_t)count) {
+    napi_throw_type_error(env, NULL, "matmulGroup takes 1 or 2 items of 7 arguments each");
+    return NULL;
+  }
+  we_matmul_item items[2];
+  memset(items, 0, sizeof(items));
+  for (uint32_t i = 0; i < count; i++) {
+    const size_t b = 6 + 7 * (size_t)i;
+    void* pdata = NULL;
+    size_t plen = 0;
+    bytes_of(&a, b, &pdata, &plen);
+    items[i].x = ptr_arg(&a, b + 1);
+    items[i].w = ptr_arg(&a, b + 2);
+    items[i].y = ptr_arg(&a, b + 3);
+    items[i].bias = (const float*)ptr_arg(&a, b + 4);
+    items[i].gate = (const float*)ptr_arg(&a, b + 5);
+    items[i].residual = ptr_arg(&a, b + 6);
+    if (a.bad) return NULL;
+    if (plen != sizeof(we_matmul_params)) {
+      napi_throw_type_error(env, NULL, "params must be the 13 x u32 image from matmulParams");
+      return NULL;
+    }
+    items[i].p = (const we_matmul_params*)pdata;
+  }
+  return status(env, ctx, we_matmul_group(ctx, count, items, xdt, wdt, ydt, flags));
+}
+
 /* matmulMul(ctx, params, xDtype, x, wDtype, w, scales, group, yDtype, y, bias, flags, mul, aux): we_matmul_mul */
 static napi_value MatmulMul(napi_env env, napi_callback_info info) {
   args_t a;
@@ -1165,7 +1202,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},
-      {"matmulParams", MatmulParams}, {"conv3x3Params", Conv3x3Params}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulMul", MatmulMul}, {"matmulQkNormRope", MatmulQkNormRope},
+      {"matmulParams", MatmulParams}, {"conv3x3Params", Conv3x3Params}, {"kSplitFor", KSplitFor}, {"matmul", Matmul}, {"matmulNoalloc", MatmulNoalloc}, {"matmulGated", MatmulGated}, {"matmulGroup", MatmulGroup}, {"matmulMul", MatmulMul}, {"matmulQkNormRope", MatmulQkNormRope},
       {"rmsnorm", RmsNorm},       {"rmsnormMod", RmsNormMod},       {"rope", Rope},             {"elementwise", Elementwise},
       {"layerSum", LayerSum},     {"lastError", LastError},   {"qkNormRope", QkNormRope}, {"attention", Attention},
       {"unpackFp8", UnpackFp8},   {"dequantInt4", DequantInt4}, {"ticketDone", TicketDone},
