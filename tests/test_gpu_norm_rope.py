@@ -57,10 +57,11 @@ def test_rmsnorm_bf16_storage(graph, rows, d):
     assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 1e-6)
 
 
-@pytest.mark.parametrize("dtype,d", [(we.BF16, 3072), (we.F16, 2048), (we.BF16, 6144)])
+@pytest.mark.parametrize("dtype,d", [(we.BF16, 3072), (we.F16, 2048), (we.BF16, 4096), (we.F16, 4104), (we.BF16, 6144)])
 def test_rmsnorm_16bit_modulated_rows(graph, dtype, d):
     """The double-stream block's modulated norm on 16-bit rows (one wave per row, 16-byte accesses): weight,
-    scale and shift per column, against the f64 oracle at one rounding of the output type."""
+    scale and shift per column, against the f64 oracle at one rounding of the output type. d <= 4096 stages the
+    per-column factors in LDS; 4104 and 6144 take the kernel that loads them per row."""
     rows = 37
     rng = np.random.default_rng(d + dtype)
     x32 = rng.standard_normal(rows * d).astype(np.float32) * 3
