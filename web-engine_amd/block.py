@@ -249,9 +249,10 @@ class DoubleBlock:
             for s in (0, 1):
                 g.rmsnorm(self.rows[s], H, cfg.eps, 1.0, dt, self.x1[s], ws[s].norm2, sl(self.mod[s], 3 * H * 4, H * 4),
                           sl(self.mod[s], 4 * H * 4, H * 4), self.h[s])
-            # the up projections differ in tile shape (128 x 128 text tiles fill the slots the image's leave)
-            self._streams(lambda s: g.matmul(we.matmul_params(self.rows[s], cfg.mlp, H, ws[s].up.scale, graph=g), dt,
-                                             self.h[s], we.FP8, ws[s].up.buffer, dt, self.u[s], flags=we.EPI_GELU))
+            # the up projections share N and K too: one launch with GELU in its epilogue
+            g.matmul_group([dict(params=we.matmul_params(self.rows[s], cfg.mlp, H, ws[s].up.scale, graph=g),
+                                 x=self.h[s], w=ws[s].up.buffer, y=self.u[s]) for s in (0, 1)], dt, we.FP8, dt,
+                           we.EPI_GELU)
             g.matmul_group([dict(params=we.matmul_params(self.rows[s], H, cfg.mlp, ws[s].down.scale, graph=g),
                                  x=self.u[s], w=ws[s].down.buffer, y=outs[s], gate=sl(self.mod[s], 5 * H * 4, H * 4),
                                  residual=self.x1[s]) for s in (0, 1)], dt, we.FP8, dt)
