@@ -116,8 +116,9 @@ def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
     (16, 33, 192, 64, we.BF16), (5, 70, 3072, 256, we.F16), (16, 130, 3584, 64, we.BF16), (1, 96, 1024, 64, we.F16),
     (4, 64, 18944, 512, we.F16), (9, 190, 64, 64, we.F16)])
 def test_shared_x_kernel_matches_general_kernel(graph, m, n, k, group, x_dt, monkeypatch):
-    """2 <= M <= 16 with 16-bit x runs the shared-x kernel (64 columns per workgroup, x rows and weights
-    through one LDS ring, 16 waves); forced at M = 1 as well here, with ragged N, K of one block up to
+    """2 <= M <= 16 with 16-bit x runs the shared-x kernel (x rows and weights through one LDS ring; 32 columns,
+    8 x rows and 8 waves per workgroup for M <= 8, 64 columns, 16 rows and 16 waves above); forced at M = 1 as
+    well here, with ragged N, K of one block up to
     18944 and scale groups of 64-512. It must match the oracle and the general kernel (same exact products,
     1e-6 for the summation order)."""
     rng = np.random.default_rng(m * 100 + k)

@@ -436,43 +436,50 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
 }
 
 // ------------------------------------------------------------------------------------------------------
-// Shared-x kernel (2 <= M <= 16, 16-bit x, K / group <= 64): a workgroup of 8 waves owns 64 columns over
-// ALL of K. The waves walk K in lock step through an NBUF-slot LDS ring; a slot holds one chunk of 4
-// blocks (256 k): the 16 x rows (16 x 512 B, rows >= M read as zeros) and the 64 x 4 weight blocks (four
-// 2 KB images of the decode kernel's layout). x thus crosses L2 -> LDS once per 64 columns.
-// Wave w multiplies column tile w % 4 with the blocks i = w / 4 (mod WPT) of every chunk; the WPT partial
-// tiles of a column tile are summed through LDS at the end. Several waves per tile keep several waves on
-// each SIMD at the decode shapes' 296 workgroups: with one wave per SIMD the dependent LDS read ->
+// Shared-x kernel (2 <= M <= 16, 16-bit x, K / group <= 64): a workgroup of TILES x WPT waves owns 16 TILES
+// columns over ALL of K. The waves walk K in lock step through an NBUF-slot LDS ring; a slot holds one chunk
+// of 4 blocks (256 k): XR x rows (XR x 512 B, rows >= M read as zeros; XR = 8 when M <= 8) and the TILES column
+// tiles' 16 x 4 weight blocks (2 KB images of the decode kernel's layout). x thus crosses L2 -> LDS once per
+// 16 TILES columns.
+// Wave w multiplies column tile w % TILES with the blocks i = w / TILES (mod WPT) of every chunk; the WPT
+// partial tiles of a column tile are summed through LDS at the end, in the same order for every TILES.
+// Several waves per tile keep several waves on each SIMD: with one wave per SIMD the dependent LDS read ->
 // unpack -> MFMA chain of every block was exposed.
-// Per chunk the workgroup issues 1024 16-byte loads, 1024 / threads per lane, all direct-to-LDS (out-of-
-// range ones read zeros), so the waits are constants. No load in the loop targets a register (the compiler would
-// add its own, stricter waits for those). The scale tile (64 rows x K / group halves) is staged once.
+// Per chunk every lane issues LPC 16-byte direct-to-LDS loads (out-of-range ones read zeros); where the slot
+// has fewer pieces than LPC x threads, the spare loads of whole waves read nothing into a pad, so the waits
+// stay constants. No load in the loop targets a register (the compiler would add its own, stricter waits for
+// those). The scale tile (16 TILES rows x K / group halves) is staged once.
 // Step ci: wait for chunk ci (own loads), barrier (everyone's loads landed, everyone is done with the slot
 // of chunk ci - 1), issue chunk ci + NBUF - 1 into that slot, then unpack and multiply chunk ci.
 // x rows in a slot: row m at m * 512, 16-byte piece p at position p ^ (m & 15) (conflict-free b128 reads).
-constexpr int SK_XB = 16 * 512;            // x rows of one chunk: 8 KB
-constexpr int SK_WB = 16 * PIPE_CB * 32;   // one column tile's weights per chunk: 2 KB
-constexpr int SK_SMAX = 64 * 64 * 2;       // scale tile: 64 rows x at most 64 groups
+// Workgroup size: at N = 18944, 64 columns make 296 workgroups, so 40 CUs run two while the others run one
+// and set the time (M = 8: 14.0 us, against 10.4 us for the 256 workgroups of N = 16384). For M <= 8, 32
+// columns and 8 x rows make 592 smaller workgroups (28 KB of LDS, 8 waves), two or three on every CU: 12.5 us.
+constexpr int SK_WB = 16 * PIPE_CB * 32;  // one column tile's weights per chunk: 2 KB
+constexpr int SK_WPT = 4;                 // waves per column tile
+constexpr int SK_NBUF = 3;                // ring slots (4 measured no faster for either shape)
 
-constexpr int SK_NBUF = 3;  // ring slots (56 KB of LDS with the scale tile: two workgroups per CU)
-constexpr int SK_WPT = 4;   // waves per column tile (16 per workgroup)
-
-template <int XT>
-__global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args a) {
+template <int XT, int TILES, int XR>
+__global__ void __launch_bounds__(64 * TILES * SK_WPT) int4_gemv_shared_kernel(Int4Args a) {
   constexpr int WPT = SK_WPT;
   constexpr bool IS_F16 = XT == F16;
-  constexpr int NT = 256 * WPT;           // threads
-  constexpr int SLOT = SK_XB + 4 * SK_WB;  // 1024 pieces of 16 B
-  constexpr int LPC = SLOT / 16 / NT;      // loads per lane per chunk
-  constexpr int BPW = PIPE_CB / WPT;       // blocks per wave per chunk
-  __shared__ __attribute__((aligned(1024))) char ring[SK_NBUF * SLOT];
-  __shared__ __attribute__((aligned(16))) char ss[SK_SMAX];
-  static_assert(SK_NBUF * SLOT >= 4 * WPT * 64 * 16, "reduction area");
+  constexpr int NW = TILES * WPT, NT = 64 * NW;  // waves, threads
+  constexpr int XB = XR * 512;                    // x rows of one chunk
+  constexpr int SLOT = XB + TILES * SK_WB;
+  constexpr int XP = XB / 16, PIECES = SLOT / 16;  // 16-byte pieces: x, then weights
+  constexpr int LPC = (PIECES + NT - 1) / NT;      // loads per lane per chunk
+  constexpr bool PAD = LPC * NT > PIECES;          // spare loads (whole waves) land in a pad
+  constexpr int BPW = PIPE_CB / WPT;               // blocks per wave per chunk
+  constexpr int SROWS = 16 * TILES, SMAX = SROWS * 64 * 2;  // scale tile: rows x at most 64 groups
+  static_assert(XP % 64 == 0 && PIECES % 64 == 0, "x / weight loads are whole waves");
+  __shared__ __attribute__((aligned(1024))) char ring[SK_NBUF * SLOT + (PAD ? 1024 : 0)];
+  __shared__ __attribute__((aligned(16))) char ss[SMAX];
+  static_assert(SK_NBUF * SLOT >= NW * 64 * 16, "reduction area");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
-  const int tile = wave & 3, phase = wave >> 2;
-  const uint32_t n0 = blockIdx.x * 64, nw = n0 + 16 * tile;
+  const int tile = wave % TILES, phase = wave / TILES;
+  const uint32_t n0 = blockIdx.x * SROWS, nw = n0 + 16 * tile;
   const uint32_t nblk = a.k / 64;
   const int nch = (int)((nblk + PIPE_CB - 1) / PIPE_CB);
   const uint32_t gshift = a.gshift;
@@ -482,22 +489,25 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, (int)a.s_bytes, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kRsrcWord3);
 
-  // piece P = j NT + tid of a slot: P < 512 are x rows (row P / 32, position P % 32), the rest the four
-  // weight images (tile (P - 512) / 128, rows nw .. nw + 16); whether a load is x or W is wave-uniform
+  // piece P = j NT + tid of a slot: P < XP are x rows (row P / 32, position P % 32), then the TILES weight
+  // images (tile (P - XP) / 128, rows nw .. nw + 16), then spares; which kind a load is, is wave-uniform
   uint32_t src[LPC];
   int blk[LPC];
 #pragma unroll
   for (int j = 0; j < LPC; j++) {
     const int P = j * NT + tid;
-    if (P < 512) {
+    if (P < XP) {
       const int m = P >> 5, p = (P & 31) ^ (m & 15);
       src[j] = (uint32_t)m < a.m ? (a.x_offset + m * a.x_stride) * 2 + p * 16 : kInvalid;
       blk[j] = p >> 3;
-    } else {
-      const int T = (P - 512) >> 7, p = (P - 512) & 127, r = p >> 3, q = (p & 7) ^ (r & 7);
+    } else if (P < PIECES) {
+      const int T = (P - XP) >> 7, p = (P - XP) & 127, r = p >> 3, q = (p & 7) ^ (r & 7);
       const uint32_t row = n0 + 16 * T + r;
       src[j] = row < a.n ? row * row_bytes + q * 16 : kInvalid;
       blk[j] = q >> 1;
+    } else {
+      src[j] = kInvalid;
+      blk[j] = 0;
     }
   }
 
@@ -507,25 +517,27 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
     char* slot = ring + s * SLOT;
 #pragma unroll
     for (int j = 0; j < LPC; j++) {
-      char* dst = slot + (j * NT + wave * 64) * 16;
-      if (j * NT + wave * 64 < 512) dma16(rx, dst, c + blk[j] < nblk ? src[j] + c * 128 : kInvalid);
-      else dma16(rw, dst, c + blk[j] < nblk ? src[j] + c * 32 : kInvalid);
+      const int first = j * NT + wave * 64;
+      if (first < XP) dma16(rx, slot + first * 16, c + blk[j] < nblk ? src[j] + c * 128 : kInvalid);
+      else if (first < PIECES) dma16(rw, slot + first * 16, c + blk[j] < nblk ? src[j] + c * 32 : kInvalid);
+      else dma16(rw, ring + SK_NBUF * SLOT, kInvalid);  // a spare: zeros into the pad, counted like the others
     }
   };
 
-  // scale tile s[n0 .. n0 + 64, :] (contiguous): 16-byte pieces straight to LDS, or halves through
+  // scale tile s[n0 .. n0 + SROWS, :] (contiguous): 16-byte pieces straight to LDS, or halves through
   // registers on the last column tile (a 16-byte load that straddles the end of the buffer reads nothing)
   const uint32_t ng = a.k / a.group;
-  const bool s_whole = n0 + 64 <= a.n;
-  constexpr int SH = SK_SMAX / 2 / NT;
+  const bool s_whole = n0 + SROWS <= a.n;
+  constexpr int SH = SMAX / 2 / NT;
   uint16_t sh[SH];
   if (s_whole) {
-    if (wave < 8) dma16(rs, ss + wave * 1024, (uint32_t)tid < ng * 8 ? n0 * ng * 2 + tid * 16 : kInvalid);
+    if (wave < SMAX / 1024)
+      dma16(rs, ss + wave * 1024, (uint32_t)tid < (uint32_t)(SROWS / 8) * ng ? n0 * ng * 2 + tid * 16 : kInvalid);
   } else {
 #pragma unroll
     for (int j = 0; j < SH; j++) {
       const uint32_t i = tid + NT * j;
-      sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < 64 * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
+      sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < SROWS * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
     }
   }
   static_for<0, SK_NBUF - 1>([&](auto CI) { issue(decltype(CI)::value, CI); });
@@ -533,7 +545,7 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
 #pragma unroll
     for (int j = 0; j < SH; j++) {
       const uint32_t i = tid + NT * j;
-      if (i < 64 * ng) *(uint16_t*)(ss + i * 2) = sh[j];
+      if (i < SROWS * ng) *(uint16_t*)(ss + i * 2) = sh[j];
     }
   }
   const char* srow = ss + (16 * tile + l16) * ng * 2;  // visible after the first step's barrier
@@ -546,7 +558,7 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
     issue(ci + SK_NBUF - 1, std::integral_constant<int, (s + SK_NBUF - 1) % SK_NBUF>{});
     const uint32_t c = (uint32_t)ci * PIPE_CB;
     const char* slot = ring + s * SLOT;
-    const char* wsl = slot + SK_XB + tile * SK_WB;
+    const char* wsl = slot + XB + tile * SK_WB;
 #pragma unroll
     for (int ii = 0; ii < BPW; ii++) {
       const int i = WPT * ii + phase;
@@ -555,7 +567,9 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
         f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-          const u32x4 xa = *(const u32x4*)(slot + x_rd + (((8 * i + 2 * g + e) ^ x_sw) * 16));
+          // with 8 staged rows, lanes of rows 8-15 feed zeros (those rows are past M)
+          u32x4 xa = *(const u32x4*)(slot + x_rd + (((8 * i + 2 * g + e) ^ x_sw) * 16));
+          if constexpr (XR < 16) xa = l16 < XR ? xa : u32x4{0, 0, 0, 0};
           const u32x4 wf = IS_F16 ? int4x8_to_f16(wq2[e], 0x00f0000fu) : int4x8_to_bf16(wq2[e]);
           part = mfma16<IS_F16>(xa, wf, part);
         }
@@ -574,7 +588,7 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
 
   // lane l of wave (tile, phase) holds column nw + l % 16, rows 4 (l / 16) + (0..3), summed over the
   // blocks of its phase; it stores rows 4 (l / 16) + (4 / WPT) phase + .. of the sum over all phases
-  f32x4_t* red = (f32x4_t*)ring;  // [4 WPT waves][64 lanes]
+  f32x4_t* red = (f32x4_t*)ring;  // [NW waves][64 lanes]
   red[wave * 64 + lane] = acc;
   __syncthreads();
   const uint32_t col = nw + l16;
@@ -584,7 +598,7 @@ __global__ void __launch_bounds__(256 * SK_WPT) int4_gemv_shared_kernel(Int4Args
     const uint32_t row = 4 * g + r;
     float sum = 0.0f;
 #pragma unroll
-    for (int p = 0; p < WPT; p++) sum += red[(tile + 4 * p) * 64 + lane][r];
+    for (int p = 0; p < WPT; p++) sum += red[(tile + TILES * p) * 64 + lane][r];
     if (row < a.m && col < a.n) int4_store(a, row, col, sum);
   }
 }
@@ -760,9 +774,16 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   }
   const bool force_pipe = path && !strcmp(path, "pipe");
   if (ring && !pipe && !force_pipe && L.k / L.group <= 64) {
-    dim3 gs((L.n + 63) / 64);
-    if (L.x_dtype == F16) hipLaunchKernelGGL(int4_gemv_shared_kernel<F16>, gs, dim3(256 * SK_WPT), 0, stream, a);
-    else hipLaunchKernelGGL(int4_gemv_shared_kernel<BF16>, gs, dim3(256 * SK_WPT), 0, stream, a);
+    // M <= 8: 32 columns and 8 staged x rows per workgroup; larger M: 64 columns, 16 rows (32 columns there
+    // double the x traffic and leave a third of each chunk's loads spare: slower)
+    const bool x8 = L.m <= 8;
+    const int tiles = x8 ? 2 : 4;
+    const dim3 gs((L.n + 16 * tiles - 1) / (16 * tiles)), bs(64 * tiles * SK_WPT);
+    const bool f16 = L.x_dtype == F16;
+    void (*kern)(Int4Args);
+    if (x8) kern = f16 ? int4_gemv_shared_kernel<F16, 2, 8> : int4_gemv_shared_kernel<BF16, 2, 8>;
+    else kern = f16 ? int4_gemv_shared_kernel<F16, 4, 16> : int4_gemv_shared_kernel<BF16, 4, 16>;
+    hipLaunchKernelGGL(kern, gs, bs, 0, stream, a);
     return hipGetLastError();
   }
   if (pipe || (force_pipe && ring && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.k / 64 <= 4 * (uint32_t)PIPE_MAXB)) {
