@@ -101,8 +101,8 @@ def test_capture_refuses_allocation_and_host_traffic(graph):
 
 def test_graph_keeps_its_scratch_when_an_eager_call_outgrows_it():
     """A graph captured with a split-K GEMM (partial sums in the context scratch) still replays correctly after an
-    eager 4608-token attention grew the scratch past the 16 MiB first allocation: the graph holds its scratch
-    block until it is destroyed. A graph captured on compute stream 1 is refused on stream 0."""
+    eager split-K GEMM with more slices and rows grew the scratch past the 16 MiB first allocation: the graph holds
+    its scratch block until it is destroyed. A graph captured on compute stream 1 is refused on stream 0."""
     g = we.Graph(0)  # a fresh context: its scratch starts at the minimum size
     try:
         rng = np.random.default_rng(3)
@@ -117,12 +117,12 @@ def test_graph_keeps_its_scratch_when_an_eager_call_outgrows_it():
         g.graph_begin()
         g.matmul(p, we.F16, x, we.FP8, w, we.F16, y_graph)
         gr = g.graph_end()
-        t, heads, hd = 4608, 24, 128  # V^T of 4608 x 24 x 128 bf16 is 28 MB of scratch
-        qkv = g.buffer(O.bf16_rne(rng.standard_normal(t * 3 * heads * hd).astype(np.float32)))
-        o = g.buffer(t * heads * hd * 2)
-        H = heads * hd
-        g.attention(t, heads, heads, hd, False, we.BF16, qkv, we.Graph.slice(qkv, H * 2, 0),
-                    we.Graph.slice(qkv, 2 * H * 2, 0), o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
+        # M = 512, N = 3072, K = 12288 splits K into several slices of 512 x 3072 f32 partial sums (over 16 MiB)
+        m2, k2 = 512, 12288
+        w2 = rng.integers(0, 254, n * k2).astype(np.uint8)
+        g.matmul(we.matmul_params(m2, n, k2, 0.02, graph=g), we.F16,
+                 g.buffer(rng.standard_normal(m2 * k2).astype(np.float16)), we.FP8,
+                 g.buffer((w2 + (w2 >= 0x7F)).astype(np.uint8)), we.F16, g.buffer(m2 * n * 2))
         g.sync()
         want = g.read(y_eager).copy()
         for _ in range(2):
