@@ -333,10 +333,12 @@ def file_read_rate(layout, host, scales, pinned, threads=8, reps=3):
 
 def measured_peaks(g, warmup_ms=500, rounds=3, runs=5, read_bytes=2 << 30):
     """The build's own ceilings, timePeak style (src/bench/peak.ts:69-109: warm up, then the fastest of `rounds`
-    rounds of `runs` dispatches): dense bf16 MFMA, scalar f32 FMA, packed f16 FMA, int8 dot4, and a streaming
-    read of `read_bytes` (beyond the 256 MB Infinity Cache)."""
+    rounds of `runs` dispatches): dense bf16 MFMA on constant operands and on operands with the fp8-weight GEMM's
+    bit statistics (the chip is power-bound under the GEMM, and toggling operand bits cost power), scalar f32 FMA,
+    packed f16 FMA, int8 dot4, and a streaming read of `read_bytes` (beyond the 256 MB Infinity Cache)."""
     out = g.buffer(max(16384 * 256, we.read_peak_out_words(read_bytes)) * 4)
-    kinds = {"mfma_bf16_tflops": (we.PEAK_MFMA_BF16, 2048, 2048), "f32_fma_tflops": (we.PEAK_F32, 16384, 4096),
+    kinds = {"mfma_bf16_tflops": (we.PEAK_MFMA_BF16, 2048, 2048),
+             "mfma_bf16_data_tflops": (we.PEAK_MFMA_BF16_DATA, 2048, 2048), "f32_fma_tflops": (we.PEAK_F32, 16384, 4096),
              "f16_fma_tflops": (we.PEAK_F16, 16384, 4096), "i8_dot4_tops": (we.PEAK_I8, 16384, 4096)}
     res = {}
     for name, (kind, wg, iters) in kinds.items():
@@ -562,6 +564,7 @@ def main():
                             "algorithmic": f"{up['flop']:.0f} FLOP per launch / {up['ms'] * 1e3:.1f} us"}
         if peaks:
             line["roofline"]["frac_of_measured_peak"] = up["tflops"] / peaks["mfma_bf16_tflops"]
+            line["roofline"]["frac_of_data_peak"] = up["tflops"] / peaks["mfma_bf16_data_tflops"]
         line["up_proj_tflops"] = up["tflops"]
         line["down_proj_tflops"] = mlp["down"]["tflops"]
     if int4:

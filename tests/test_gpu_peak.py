@@ -52,6 +52,19 @@ def test_mfma_chains_are_linear_in_the_iterations(graph):
     assert np.array_equal(2 * a, b)
 
 
+def test_mfma_on_gemm_like_operands_is_deterministic_and_finite(graph):
+    """The MFMA probe on the fp8-weight GEMM's operand statistics: same operation count as the constant-operand
+    probe, finite results (random signs keep the sums small), different per thread, the same on a second run, and
+    different from the constant-operand probe's."""
+    out1, out2, out3 = graph.buffer(256 * 4 * 4), graph.buffer(256 * 4 * 4), graph.buffer(256 * 4 * 4)
+    assert graph.peak(we.PEAK_MFMA_BF16_DATA, 4, 19, out1) == 4 * 256 * 19 * 4096  # two groups of 8 and a rest of 3
+    graph.peak(we.PEAK_MFMA_BF16_DATA, 4, 19, out2)
+    graph.peak(we.PEAK_MFMA_BF16, 4, 19, out3)
+    a, b, c = (graph.read(o).view(np.float32) for o in (out1, out2, out3))
+    assert np.all(np.isfinite(a)) and np.array_equal(a, b)
+    assert len(np.unique(a)) > 900 and not np.array_equal(a, c)
+
+
 def test_streaming_read_sums_every_word(graph):
     # 64 MB plus a ragged tail (not a whole number of waves' worth)
     words = np.random.default_rng(0).integers(0, 2 ** 32, (64 << 20) // 4 + 4 * 333, dtype=np.uint64).astype(np.uint32)

@@ -94,7 +94,7 @@ struct Int4Launch {
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream);
 
 // peak probes (peak.hip): kinds as WE_PEAK_* of we.h
-enum PeakKind { PEAK_F32 = 0, PEAK_F16 = 1, PEAK_I8 = 2, PEAK_MFMA_BF16 = 3 };
+enum PeakKind { PEAK_F32 = 0, PEAK_F16 = 1, PEAK_I8 = 2, PEAK_MFMA_BF16 = 3, PEAK_MFMA_BF16_DATA = 4 };
 constexpr int READ_PEAK_U = 8;  // 16-byte chunks per thread of the streaming read: one u32 out per 32 KB / 4 waves
 inline uint64_t read_peak_out_words(uint64_t bytes) { return 4 * ((bytes / 16 + 256 * READ_PEAK_U - 1) / (256 * READ_PEAK_U)); }
 hipError_t peak_launch(int kind, uint32_t workgroups, uint32_t iters, uint32_t* out, hipStream_t stream);

@@ -8,7 +8,13 @@
 //   F16: 8 chains x 2 packed fma (v_pk_fma_f16, 4 ops each);
 //   I8:  8 chains x dot4 of int8 (v_dot4_i32_i8, 4 multiply-adds = 8 ops);
 //   MFMA_BF16: per wave 8 chains of v_mfma_f32_32x32x16_bf16 (32768 FLOP each) per iteration, i.e. 4096 FLOP
-//        per thread per iteration.
+//        per thread per iteration, on small constant operands;
+//   MFMA_BF16_DATA: the same loop on operands with the fp8-weight GEMM's bit statistics: A as its activations
+//        (bf16 of N(0,1)-like magnitude, every mantissa bit random), B as its weights (the bf16 images of random
+//        finite e4m3fn codes, decoded by the hardware converter), 8 operand pairs per lane rotated so that
+//        consecutive MFMAs of a chain see different data. The chip runs at its power limit under the GEMM, and
+//        the power of an MFMA grows with the bits that toggle in its operands: this is the ceiling of the
+//        matmul's MFMA loop on the data it is measured with.
 // The chains start from the thread id so no value is a compile-time constant, and every result is folded
 // into out[thread] so nothing is removed. b = 0.5 and c = 0.25 keep the float chains exact (and finite).
 #include "common.h"
@@ -95,6 +101,67 @@ __global__ void __launch_bounds__(256) peak_mfma_bf16(uint32_t iters, uint32_t* 
   out[id] = __float_as_uint(s);
 }
 
+__device__ __forceinline__ uint32_t peak_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  return x ^ (x >> 16);
+}
+
+__global__ void __launch_bounds__(256) peak_mfma_bf16_data(uint32_t iters, uint32_t* out) {
+  const uint32_t id = blockIdx.x * 256 + threadIdx.x;
+  u32x4 ra[PEAK_CHAINS], rb[PEAK_CHAINS];
+#pragma unroll
+  for (int j = 0; j < PEAK_CHAINS; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t h = peak_hash(id * 64u + (uint32_t)(j * 4 + e) * 2u);
+      // two bf16: random sign and 7 mantissa bits, exponents 124 .. 127 (|v| in [0.125, 2))
+      const uint32_t lo = (h & 0x807fu) | ((124u + ((h >> 7) & 3u)) << 7);
+      const uint32_t hi = ((h >> 16) & 0x807fu) | ((124u + ((h >> 23) & 3u)) << 7);
+      ra[j][e] = lo | (hi << 16);
+    }
+#pragma unroll
+  for (int j = 0; j < PEAK_CHAINS; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      // four random finite e4m3fn codes (0x7f / 0xff, the NaN codes, become 0x7e / 0xfe) -> four bf16
+      uint32_t w = peak_hash(id * 64u + (uint32_t)(j * 4 + e) * 2u + 1u);
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+        if (((w >> (8 * b)) & 0x7fu) == 0x7fu) w -= 1u << (8 * b);
+      const auto lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+      const auto hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+      rb[j][e] = __builtin_bit_cast(uint32_t, lo);
+      rb[j][e + 1] = __builtin_bit_cast(uint32_t, hi);
+    }
+  f32x16_p acc[PEAK_CHAINS];
+#pragma unroll
+  for (int j = 0; j < PEAK_CHAINS; j++) acc[j] = f32x16_p{};
+  uint32_t i = 0;
+  // groups of 8 iterations: in sub-iteration s chain j multiplies A[j] with B[(j + s) % 8]
+  for (; i + PEAK_CHAINS <= iters; i += PEAK_CHAINS)
+#pragma unroll
+    for (int s8 = 0; s8 < PEAK_CHAINS; s8++)
+#pragma unroll
+      for (int j = 0; j < PEAK_CHAINS; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ra[j]),
+                                                         __builtin_bit_cast(bf16x8, rb[(j + s8) % PEAK_CHAINS]), acc[j],
+                                                         0, 0, 0);
+  for (; i < iters; i++)
+#pragma unroll
+    for (int j = 0; j < PEAK_CHAINS; j++)
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ra[j]), __builtin_bit_cast(bf16x8, rb[j]),
+                                                       acc[j], 0, 0, 0);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PEAK_CHAINS; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) s += acc[j][v];
+  out[id] = __float_as_uint(s);
+}
+
 // Streaming read of n16 16-byte chunks in one shot: each thread loads READ_PEAK_U chunks spaced by the grid
 // (all in flight at once, no loop; the grid covers the buffer), sums their words, and each wave writes one sum.
 __global__ void __launch_bounds__(256) read_peak(const u32x4* __restrict__ p, uint64_t n16, uint32_t* out) {
@@ -121,6 +188,9 @@ hipError_t peak_launch(int kind, uint32_t workgroups, uint32_t iters, uint32_t* 
     case PEAK_F32: hipLaunchKernelGGL(peak_f32, dim3(workgroups), dim3(64), 0, stream, iters, 0.5f, 0.25f, out); break;
     case PEAK_F16: hipLaunchKernelGGL(peak_f16, dim3(workgroups), dim3(64), 0, stream, iters, 0.5f, 0.25f, out); break;
     case PEAK_I8: hipLaunchKernelGGL(peak_i8, dim3(workgroups), dim3(64), 0, stream, iters, 0x0302ff01u, out); break;
+    case PEAK_MFMA_BF16_DATA:
+      hipLaunchKernelGGL(peak_mfma_bf16_data, dim3(workgroups), dim3(256), 0, stream, iters, out);
+      break;
     default: hipLaunchKernelGGL(peak_mfma_bf16, dim3(workgroups), dim3(256), 0, stream, iters, out); break;
   }
   return hipGetLastError();

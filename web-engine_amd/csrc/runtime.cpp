@@ -1036,12 +1036,13 @@ int we_matmul_group(we_ctx* ctx, uint32_t count, const we_matmul_item* items, in
 
 int we_peak(we_ctx* ctx, int kind, uint32_t workgroups, uint32_t iters, uint32_t* out, double* ops) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
-  if (kind < WE_PEAK_F32 || kind > WE_PEAK_MFMA_BF16) return fail(ctx, WE_EINVAL, "unknown peak kind %d", kind);
+  if (kind < WE_PEAK_F32 || kind > WE_PEAK_MFMA_BF16_DATA) return fail(ctx, WE_EINVAL, "unknown peak kind %d", kind);
   if (workgroups == 0 || workgroups > (1u << 24)) return fail(ctx, WE_EINVAL, "workgroups must be in [1, 2^24], got %u", workgroups);
-  const uint64_t threads = (uint64_t)workgroups * (kind == WE_PEAK_MFMA_BF16 ? 256 : 64);
+  const bool mfma = kind == WE_PEAK_MFMA_BF16 || kind == WE_PEAK_MFMA_BF16_DATA;
+  const uint64_t threads = (uint64_t)workgroups * (mfma ? 256 : 64);
   int rc = check_span(ctx, out, threads * 4, "out");
   if (rc) return rc;
-  if (ops) *ops = (double)threads * iters * (kind == WE_PEAK_MFMA_BF16 ? 4096.0 : 64.0);
+  if (ops) *ops = (double)threads * iters * (mfma ? 4096.0 : 64.0);
   HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
   hipError_t e = we::peak_launch(kind, workgroups, iters, out, ctx->compute);
   return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "peak launch");

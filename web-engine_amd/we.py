@@ -32,7 +32,7 @@ ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
 MUL_SWIGLU, MUL_SIGMOID_GATE = 1, 2
 OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
-PEAK_F32, PEAK_F16, PEAK_I8, PEAK_MFMA_BF16 = range(4)
+PEAK_F32, PEAK_F16, PEAK_I8, PEAK_MFMA_BF16, PEAK_MFMA_BF16_DATA = range(5)
 
 
 def read_peak_out_words(nbytes):
