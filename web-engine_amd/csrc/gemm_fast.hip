@@ -24,6 +24,9 @@
 //    that wave through an exact recompute that decodes every byte with the shader's formula.
 // Requirements (checked on the host): x / W rows 16-byte aligned, K and the split-K slice multiples of
 // 16, operand extents below 2^31 bytes.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "internal.h"
 
@@ -743,12 +746,30 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
 
 // Sum of the split-K partial planes, then the epilogue of the GEMM (scale, bias, GELU, accumulate, output
 // type): one thread per 4 consecutive outputs of a row, slices added in slice order.
-template <int YT>
+// XCD (BM, BN > 0): the slices of a tile ran on one XCD (workgroups go round-robin over the 8 XCDs, and the slice
+// index adds a multiple of 8 tiles to the workgroup id), so each reduce workgroup takes a part of a tile of its own
+// XCD and reads the slices there. Otherwise one thread per 4 consecutive outputs in row-major order.
+template <int YT, int BM = 0, int BN = 0>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
-  const uint32_t groups = (a.n + 3) / 4;
-  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (size_t)a.m * groups) return;
-  const uint32_t row = (uint32_t)(idx / groups), c0 = (uint32_t)(idx % groups) * 4;
+  uint32_t row, c0;
+  if constexpr (BM > 0) {
+    constexpr uint32_t ITEMS = BM * BN / 4, Q = ITEMS / 256;  // reduce workgroups per tile
+    const uint32_t b = blockIdx.x, j = b >> 3;
+    const uint32_t pid = (b & 7u) * (a.tiles_m * a.tiles_n / 8) + j / Q;  // a tile the GEMM ran on this XCD
+    const uint32_t i = (j % Q) * 256 + threadIdx.x;
+    constexpr uint32_t GROUP_M = 4;
+    const uint32_t per_group = GROUP_M * a.tiles_n, first_m = (pid / per_group) * GROUP_M;
+    const uint32_t gsize = min(a.tiles_m - first_m, GROUP_M), in_group = pid % per_group;
+    row = (first_m + in_group % gsize) * BM + i / (BN / 4);
+    c0 = (in_group / gsize) * BN + (i % (BN / 4)) * 4;
+    if (row >= a.m || c0 >= a.n) return;
+  } else {
+    const uint32_t groups = (a.n + 3) / 4;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)a.m * groups) return;
+    row = (uint32_t)(idx / groups);
+    c0 = (uint32_t)(idx % groups) * 4;
+  }
   const size_t plane = (size_t)a.m * a.n;
   const float* p = a.part + (size_t)row * a.n + c0;
   const bool full = c0 + 3 < a.n;
@@ -812,6 +833,23 @@ static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
     hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, IS_F16, BT, S, F32, PP>), grid, block, 0, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // the slices' placement: the GEMM's tile id comes from xcd_remap_f, so with T tiles, T a multiple of 8, XCD x
+    // ran tiles [x T / 8, (x + 1) T / 8) of every slice (slice z adds z T, a multiple of 8, to the linear id). The
+    // partial sums are still in that XCD's L2 when the reduce pass reads them there unless the GEMM's weight stream
+    // pushed them out: measured on MI355X, 64 x 3072 x 3072 fp8 10.9 -> 9.2 us per call and 16 x 3072 x 3072 8.5 ->
+    // 8.1 us, but 64 x 3072 x 12288 (37.7 MB of weights) 19.5 -> 20.2 us, so only up to 16 MB of weights (2 MB per
+    // XCD). WE_GEMM_REDUCE_XCD=off: the row-major mapping (measurements)
+    static_assert((BM * BN / 4) % 256 == 0, "whole reduce workgroups per tile");
+    const char* xm = getenv("WE_GEMM_REDUCE_XCD");
+    if (tiles % 8 == 0 && a.w_bytes <= (16u << 20) && !(xm && strcmp(xm, "off") == 0)) {
+      const dim3 rg(tiles * (BM * BN / 4 / 256));
+      switch (a.y_dtype) {
+        case F32: hipLaunchKernelGGL((splitk_reduce_kernel<F32, BM, BN>), rg, dim3(256), 0, s, a); break;
+        case F16: hipLaunchKernelGGL((splitk_reduce_kernel<F16, BM, BN>), rg, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((splitk_reduce_kernel<BF16, BM, BN>), rg, dim3(256), 0, s, a); break;
+      }
+      return hipGetLastError();
+    }
     const size_t threads = (size_t)a.m * ((a.n + 3) / 4);
     const dim3 rg((unsigned)((threads + 255) / 256));
     switch (a.y_dtype) {
