@@ -835,10 +835,12 @@ static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
     if (e != hipSuccess) return e;
     // the slices' placement: the GEMM's tile id comes from xcd_remap_f, so with T tiles, T a multiple of 8, XCD x
     // ran tiles [x T / 8, (x + 1) T / 8) of every slice (slice z adds z T, a multiple of 8, to the linear id). The
-    // partial sums are still in that XCD's L2 when the reduce pass reads them there unless the GEMM's weight stream
-    // pushed them out: measured on MI355X, 64 x 3072 x 3072 fp8 10.9 -> 9.2 us per call and 16 x 3072 x 3072 8.5 ->
-    // 8.1 us, but 64 x 3072 x 12288 (37.7 MB of weights) 19.5 -> 20.2 us, so only up to 16 MB of weights (2 MB per
-    // XCD). WE_GEMM_REDUCE_XCD=off: the row-major mapping (measurements)
+    // reduce pass then reads each tile on its XCD, so every L2 holds only its own tiles' partial sums (the
+    // row-major pass pulled all of them into every L2, evicting the GEMM's own inputs). Each output is the same
+    // sum in slice order either way. Measured on MI355X (graph replays): 64 x 3072 x 3072 fp8 10.9 -> 9.2 us per
+    // call, 12.2 -> 11.2 us with the weights streamed from HBM, 16 x 3072 x 3072 8.5 -> 8.1 us; but 64 x 3072 x
+    // 12288 (37.7 MB of weights) 19.5 -> 20.2 us, so only up to 16 MB of weights (2 MB per XCD).
+    // WE_GEMM_REDUCE_XCD=off: the row-major mapping (measurements)
     static_assert((BM * BN / 4) % 256 == 0, "whole reduce workgroups per tile");
     const char* xm = getenv("WE_GEMM_REDUCE_XCD");
     if (tiles % 8 == 0 && a.w_bytes <= (16u << 20) && !(xm && strcmp(xm, "off") == 0)) {
