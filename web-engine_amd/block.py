@@ -150,8 +150,8 @@ class DoubleBlock:
     """The double-stream block at fixed token counts, with its workspace allocated once. With overlap (the
     default) the text stream's steps run on the context's second compute stream, beside the image stream's:
     the two streams meet only in the joint attention, and the text stream's small GEMMs fill workgroup slots
-    the image stream leaves free. With grouped (the default, with overlap) the output and down projections of
-    the two streams run as one launch each (we_matmul_group). The result is the same bit for bit as serial
+    the image stream leaves free. With grouped (the default, with overlap) the output, up and down projections
+    of the two streams run as one launch each (we_matmul_group). The result is the same bit for bit as serial
     calls that use the same tile shapes."""
 
     def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16, overlap=True, grouped=True):
