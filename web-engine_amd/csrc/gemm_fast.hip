@@ -24,6 +24,7 @@
 //    that wave through an exact recompute that decodes every byte with the shader's formula.
 // Requirements (checked on the host): x / W rows 16-byte aligned, K and the split-K slice multiples of
 // 16, operand extents below 2^31 bytes.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -817,6 +818,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
   }
 }
 
+// Does the split-K reduce pass read each tile's partial sums from the L2 of the XCD that computed them? With a
+// multiple of 8 tiles and at most 16 MiB of weights (2 MiB per XCD, so the weight stream does not push the sums
+// out). WE_GEMM_REDUCE_XCD=off: never (measurements).
+static bool reduce_in_l2(uint64_t tiles, uint64_t weight_bytes) {
+  const char* xm = getenv("WE_GEMM_REDUCE_XCD");
+  if (xm && strcmp(xm, "off") == 0) return false;
+  return tiles % 8 == 0 && weight_bytes <= (16u << 20);
+}
+
 template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S, bool PP = false>
 static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
@@ -842,8 +852,7 @@ static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
     // 12288 (37.7 MB of weights) 19.5 -> 20.2 us, so only up to 16 MB of weights (2 MB per XCD).
     // WE_GEMM_REDUCE_XCD=off: the row-major mapping (measurements)
     static_assert((BM * BN / 4) % 256 == 0, "whole reduce workgroups per tile");
-    const char* xm = getenv("WE_GEMM_REDUCE_XCD");
-    if (tiles % 8 == 0 && a.w_bytes <= (16u << 20) && !(xm && strcmp(xm, "off") == 0)) {
+    if (reduce_in_l2(tiles, a.w_bytes)) {
       const dim3 rg(tiles * (BM * BN / 4 / 256));
       switch (a.y_dtype) {
         case F32: hipLaunchKernelGGL((splitk_reduce_kernel<F32, BM, BN>), rg, dim3(256), 0, s, a); break;
@@ -906,6 +915,12 @@ bool fast_supported(const GemmLaunch& L, uint32_t kc) {
 
 constexpr uint32_t kCUs = 256;
 
+// readable weight bytes of a GEMM (FastArgs::w_bytes)
+uint64_t weight_extent(const GemmLaunch& L) {
+  const int wb = L.w_dtype == FP8 ? 1 : 2;
+  return L.k ? ((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb : 0;
+}
+
 // Tile shape by predicted speed: score = base x (tiles / slots) / (time in rounds). base is the tile shape's own
 // speed relative to 256 x 256 (one per CU, the fastest per FLOP) at full occupancy; a full round of tiles costs 1,
 // the last, partly filled round 0.6 + 0.3 f (f = the fraction of slots it fills). The chip runs at its power
@@ -966,8 +981,14 @@ GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits) {
   uint32_t rs;
   if (L.m <= 64) {
     if (tiles >= kCUs / 2) return p;
-    rs = (uint32_t)((kCUs + tiles - 1) / tiles);  // about one workgroup per CU (measured: 4 .. 12 slices of
-                                                   // M = 64, K = 3072 within 2%)
+    // about one workgroup per CU; where the reduce pass reads the partial sums from L2 (reduce_in_l2), up to two
+    // (at most 8 slices where one per CU needs fewer). Measured, 8 slices against one workgroup per CU, weights
+    // cached / streamed from HBM: 64 x 3072 x 3072 9.24 / 10.22 -> 8.99 / 9.98 us, 16 x 3072 x 3072 8.07 / 9.05 ->
+    // 7.61 / 8.67 us, 64 x 4096 x 4096 10.92 / 12.47 -> 10.23 / 11.78 us (12 slices of 64 x 3072 x 3072: 10.5 us);
+    // without the L2 reduce more slices only add partial-sum traffic (64 x 6144 x 3072: 14.1 -> 15.9 us)
+    const uint64_t one = (kCUs + tiles - 1) / tiles, two = (2 * kCUs + tiles - 1) / tiles;
+    rs = reduce_in_l2(tiles, weight_extent(L)) ? (uint32_t)std::max<uint64_t>(one, std::min<uint64_t>(8, two))
+                                               : (uint32_t)one;
   } else {
     // larger M: split when the tiles fill less than half of the workgroup slots (M = 512, N = 3072:
     // 96 tiles of 128 x 128 for 512 slots), to about one workgroup per slot

@@ -116,7 +116,7 @@ size_t attention_scratch_bytes(const AttnLaunch& L);
 hipError_t attention_launch(const AttnLaunch& L, hipStream_t stream);
 
 // Scratch of the allocation-free entry point (noalloc.hip): a file-scope device array of this many bytes per GPU.
-// It holds the split-K partial sums of we_matmul_noalloc (about 4-6 MB for any M <= 64).
+// It holds the split-K partial sums of we_matmul_noalloc (at most about 10 MB for any M <= 64).
 constexpr size_t kNoallocScratchBytes = 16u << 20;
 // Looks up the array's address on `device`, which must be current; once per device (later calls return at once).
 hipError_t noalloc_scratch_init(int device);
