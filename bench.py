@@ -164,8 +164,8 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20, rotate=0):
     """One GEMM timed over repeated calls on the same operands. rotate > 0 (small M only): also the time per call
     when the calls cycle through `rotate` copies of the weights, so that they stream from HBM rather than from
     the caches (`us_rotating_weights`)."""
-    x = g.buffer(bf16_bits(rng.standard_normal(m * k, dtype=np.float32)) if x_dt == we.BF16 else
-                 rng.standard_normal(m * k).astype(np.float16))
+    xs = rng.standard_normal(m * k, dtype=np.float32)
+    x = g.buffer(bf16_bits(xs) if x_dt == we.BF16 else xs.astype(np.float16) if x_dt == we.F16 else xs)
 
     def weights():
         if w_dt == we.FP8:
@@ -198,7 +198,7 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20, rotate=0):
     return res
 
 
-# Tile configurations of the fast GEMM (WE_GEMM_CFG values) and the shapes the sweep times them on: the
+# Tile configurations of the fast GEMM (gemm_cfg tuning values) and the shapes the sweep times them on: the
 # benchmarked DiT shapes (M = 4096 image tokens, the M = 512 text stream) and the reference tuner's own shapes
 # (src/bench/tune.ts:5-9, 1928x1088 at 8740 tokens), all with fp8 weights unless named.
 SWEEP_CFGS = {0: "256x256", 1: "256x128", 2: "128x128", 3: "64x64", 4: "32x64", 5: "256x192"}
@@ -219,8 +219,7 @@ def sweep_tiles(g, rng, iters=10):
     """The tile sweep behind the fast GEMM's tile pick (the role of tuneMatmul, src/bench/tune.ts:14-30): every
     tile configuration on every sweep shape, bf16 activations and output, TFLOP/s from HIP events. Each shape is
     warmed up first and the configurations are timed twice, in opposite orders, keeping the faster run, so no
-    configuration is measured on cold clocks. "auto" is the library's own pick (WE_GEMM_CFG unset)."""
-    import os
+    configuration is measured on cold clocks. "auto" is the library's own pick (gemm_cfg -1)."""
     rows = []
     for name, m, n, k, w_dt, flags in SWEEP_SHAPES:
         x = g.buffer(bf16_bits(rng.standard_normal(m * k, dtype=np.float32)))
@@ -239,15 +238,12 @@ def sweep_tiles(g, rng, iters=10):
             run()
         for sweep_pass in (order, order[::-1]):
             for cfg in sweep_pass:
-                if cfg == "auto":
-                    os.environ.pop("WE_GEMM_CFG", None)
-                else:
-                    os.environ["WE_GEMM_CFG"] = str(cfg)
+                g.set_tuning("gemm_cfg", -1 if cfg == "auto" else cfg)
                 run()
                 reps = iters if m <= 512 or cfg not in (3, 4) else 2
                 ms = time_graph(g, run, 10, 1) if m <= 64 else time_launches(g, run, reps)
                 best[cfg] = min(best.get(cfg, float("inf")), ms)
-        os.environ.pop("WE_GEMM_CFG", None)
+        g.set_tuning("gemm_cfg", -1)
         tflops = {("auto" if c == "auto" else SWEEP_CFGS[c]): flop / ms / 1e9 for c, ms in best.items()}
         top = max(v for c, v in tflops.items() if c != "auto")
         rows.append({"shape": name, "m": m, "n": n, "k": k, "weights": "fp8" if w_dt == we.FP8 else "bf16",
@@ -288,6 +284,9 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
     for i in range(8):  # the first forwards run below steady clocks (measured: the first 10 ~12% slower)
         forward(i, w_res)
     t_comp = time_launches(g, lambda i: forward(i, w_res), iters)
+    # profileBlock (src/bench/block.ts:17-95): every step on its own, serial, after the whole-block timing
+    ops = blk.profile(w_res[0], w_res[1], xs[0][0], xs[0][1], tvec, rope, xs[1][0], xs[1][1])
+    op_sum = {kind: sum(o["us"] for o in ops if o["kind"] == kind) for kind in ("linear", "attention", "other")}
     attn_ms = time_launches(g, lambda i: g.attention(tt + ti, 24, 24, 128, False, we.BF16, blk.qkv,
                                                      we.Graph.slice(blk.qkv, H * 2, 0),
                                                      we.Graph.slice(blk.qkv, 2 * H * 2, 0), blk.o, q_stride=3 * H,
@@ -326,7 +325,12 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
             "attention_us": attn_ms * 1e3, "attention_tflops": attn_flop / attn_ms / 1e9,
             "weight_bytes_per_block": layout.nbytes, "copy_ms_per_block": t_copy,
             "h2d_gbs": layout.nbytes / t_copy / 1e6, "streamed_ms_per_block": t_stream,
-            "overlap_efficiency": (t_copy + t_comp - t_stream) / min(t_copy, t_comp), "file_read": file_read}
+            "overlap_efficiency": (t_copy + t_comp - t_stream) / min(t_copy, t_comp), "file_read": file_read,
+            "profile": {"ops": ops, "linear_us": op_sum["linear"], "attention_us": op_sum["attention"],
+                        "other_us": op_sum["other"], "sum_of_ops_us": sum(op_sum.values()),
+                        "whole_block_us": t_comp * 1e3,
+                        "note": "each step alone on one stream (profileBlock); the whole block overlaps the text "
+                                "stream with the image stream and groups their projections"}}
 
 
 def file_read_rate(layout, host, scales, pinned, threads=8, reps=3):
@@ -513,12 +517,16 @@ def cpu_baseline(budget_s):
 
 
 def measured_traffic(name):
-    """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs, or None."""
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter runs, or None; with where they were
+    measured (the commit and box recorded in profiles/traffic.json)."""
     try:
-        entry = json.loads(TRAFFIC.read_text())["kernels"][name]
-        return float(entry["fetch_bytes"]) + float(entry["write_bytes"])
+        data = json.loads(TRAFFIC.read_text())
+        entry = data["kernels"][name]
+        source = {k: data[k] for k in ("commit", "box", "command") if k in data}
+        source["measured"] = "an earlier rocprofv3 --pmc run of this script (not this run)"
+        return float(entry["fetch_bytes"]) + float(entry["write_bytes"]), source
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 def main():
@@ -556,6 +564,11 @@ def main():
     if args.only in ("gemm", "all"):
         extra["c2_bf16_qkv_4096x9216x3072"] = bench_gemm(g, rng, 4096, 9216, 3072, we.BF16, we.BF16, we.BF16)
         extra["c1_fp8_64x3072x3072"] = bench_gemm(g, rng, 64, 3072, 3072, we.F16, we.FP8, we.F16, rotate=32)
+        # the drop-in caller's own dtypes: an unchanged src/model/ops.ts reaches we_matmul through
+        # Graph.run(matmulFp8Wgsl, ...) with f32 x and f32 y (src/kernels/matmul.ts:129-131)
+        extra["c3_up_f32_activations"] = dict(
+            bench_gemm(g, rng, 4096, 12288, 3072, we.F32, we.FP8, we.F32, iters=10),
+            note="up-projection shape with f32 x and f32 y, as Graph.run(matmulFp8Wgsl) issues it")
     extra["calibration"] = calibration_copy(g)
     peaks = measured_peaks(g) if args.only == "all" else None
     if peaks:
@@ -573,8 +586,9 @@ def main():
     if mlp:
         line.update({"value": mlp["step_tflops"], "ms_per_step": mlp["ms_per_step"]})
         up = mlp["up"]
+        traffic, source = measured_traffic("gemm_fp8_up")
         line["roofline"] = {"bound": "mfma", "achieved": up["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                            "frac": up["tflops"] / PEAK_BF16_TFLOPS, "traffic": measured_traffic("gemm_fp8_up"),
+                            "frac": up["tflops"] / PEAK_BF16_TFLOPS, "traffic": traffic, "traffic_source": source,
                             "kernel": "gemm_lds_kernel<256,256,2,4,bf16,fp8, ping-pong> up-projection "
                                       "4096x12288x3072 (+ fused GELU)",
                             "algorithmic": f"{up['flop']:.0f} FLOP per launch / {up['ms'] * 1e3:.1f} us"}
@@ -586,8 +600,9 @@ def main():
     if int4:
         line["int4_gemv"] = int4
         m1 = int4["M1"]
+        traffic, source = measured_traffic("int4_decode_m1")
         line["roofline_int4"] = {"bound": "hbm", "achieved": m1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": m1["gbs"] / PEAK_HBM_GBS, "traffic": measured_traffic("int4_decode_m1"),
+                                 "frac": m1["gbs"] / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": source,
                                  "kernel": "int4_gemv_direct_kernel<7> M=1 K=3584 N=18944 group 64 (f16 x)",
                                  "algorithmic": f"{m1['bytes']} B per launch / {m1['us']:.2f} us",
                                  "frac_of_same_size_read_probe": m1["gbs"] / int4["read_probe_same_size"]["gbs"]}

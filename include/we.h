@@ -60,7 +60,7 @@ typedef struct we_matmul_params {
   float scale;
   uint32_t x_stride, w_stride, y_stride;
   uint32_t x_offset, w_offset, y_offset;
-  uint32_t width, cin; /* conv3x3 only in the reference; must be 0 here */
+  uint32_t width, cin; /* 3x3 convolution input (we_conv3x3_params, src/kernels/matmul.ts:74-83); 0 for a GEMM */
   uint32_t k_split;
 } we_matmul_params;
 
@@ -95,6 +95,22 @@ int we_stats(we_ctx* ctx, uint64_t* created, uint64_t* reused, uint64_t* created
  *    buffer reads NaN instead of stale plausible values. Reused buffers are still zeroed by we_buf_alloc. */
 int we_set_alloc_cap(we_ctx* ctx, uint64_t bytes, uint64_t* held);
 int we_set_poison(we_ctx* ctx, int on);
+
+/* Kernel-choice switches, per context. Additive: the reference's tuner (src/bench/tune.ts:5-30) compiles shader
+ * variants from TUNE_CONFIGS (src/kernels/matmul-tuned.ts:13-125); here the variants are built in and a switch pins
+ * one, for tile sweeps, measurements and tests. A context starts from the environment as it is at we_ctx_create
+ * (WE_GEMM_CFG=<id>, WE_GEMM_PATH=generic, WE_GEMM_SPLITK=off|<slices>, WE_GEMM_REDUCE_XCD=off,
+ * WE_ATTN_PATH=registers|ring, WE_INT4_PATH=generic|shared|pipe); launches read the context, never the environment.
+ * we_set_tuning sets one key (WE_EINVAL for an unknown key or a value out of range) and returns the old value in
+ * `previous` (may be NULL). */
+#define WE_TUNE_GEMM_CFG 0        /* fast-GEMM tile: 0 256x256, 1 256x128, 2 128x128, 3 64x64, 4 32x64, 5 256x192; -1 by shape */
+#define WE_TUNE_GEMM_GENERIC 1    /* 1: the general GEMM kernel only */
+#define WE_TUNE_GEMM_SPLITK 2     /* -1: split-K plan by shape, 0: off, n > 0: n slices */
+#define WE_TUNE_GEMM_REDUCE_XCD 3 /* 1: the split-K reduce reads each tile on its XCD where that pays, 0: never */
+#define WE_TUNE_ATTN_PATH 4       /* 0: default, 1: register-staged kernel, 2: DMA ring with a V^T pre-pass */
+#define WE_TUNE_INT4_PATH 5       /* 0: by shape, 1: general kernel, 2: shared-x kernel, 3: LDS-ring decode kernel */
+int we_set_tuning(we_ctx* ctx, int key, int value, int* previous);
+
 int we_sync(we_ctx* ctx); /* device.queue.onSubmittedWorkDone(), called from src/model/weights.ts:128 */
 
 /* Two compute streams. No counterpart in the reference, whose WebGPU queue is one ordered stream: for
@@ -182,7 +198,11 @@ int we_matmul(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x
  * output tiles) keep in scratch go to a fixed per-GPU device array of 16 MiB instead of the context's scratch,
  * which holds every M <= 64 shape. A GEMM whose split plan needs more fails with WE_EINVAL, "... needs <n> bytes of
  * split-K scratch; the allocation-free entry point has 16777216 (use we_matmul)". Every call on one GPU shares that
- * GPU's array: calls that overlap on one GPU (the two compute streams, or two contexts) race. */
+ * GPU's array, so calls that could overlap are refused rather than raced: the array belongs to the first live
+ * context that calls this on the GPU until that context is destroyed (another context's call fails with WE_EINVAL),
+ * and a call while compute stream 1 is selected fails with WE_EINVAL. Calls of the owning context on stream 0 run
+ * in stream order; each call's split-K slices write every partial sum before its reduce pass reads them, so what a
+ * previous call left in the array is never read. */
 int we_matmul_noalloc(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
                       const void* w_scales, uint32_t group, int y_dtype, void* y, const float* bias, uint32_t flags);
 /* we_matmul with the gated residual of the reference's gatedAdd (src/kernels/elementwise.ts:52-58, used after the
@@ -231,8 +251,9 @@ int we_matmul_qk_norm_rope(we_ctx* ctx, const we_matmul_params* p, int x_dtype, 
  * matching 16-bit weights and 16-byte aligned rows, the tiles of both run in one launch with all of K per tile (no
  * split-K), in the tile shape picked for the two row counts together: a small GEMM beside a large one then adds no
  * launch and no partly empty round of tiles of its own. Each result equals a separate we_matmul_gated call made
- * with that tile shape (WE_GEMM_CFG) and no split-K plan. Any other pair, and count 1, runs as separate calls in
- * order. Every item is checked before anything is launched; count must be 1 or 2. */
+ * with that tile shape (WE_TUNE_GEMM_CFG) and no split-K plan. A pair whose items depend on each other (one item's
+ * y overlaps the other's y, x, w, bias, gate or residual bytes), any other pair, and count 1 run as separate calls
+ * in order, item 0 first. Every item is checked before anything is launched; count must be 1 or 2. */
 typedef struct we_matmul_item {
   const we_matmul_params* p;
   const void* x;

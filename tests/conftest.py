@@ -26,6 +26,22 @@ def graph():
     g.destroy()
 
 
+@pytest.fixture
+def tune(graph):
+    """Pins kernel choices of the session's context for one test (graph.set_tuning: tune(gemm_cfg=0, ...)); the
+    previous values come back when the test ends."""
+    saved = {}
+
+    def set_(**switches):
+        for key, value in switches.items():
+            prev = graph.set_tuning(key, value)
+            saved.setdefault(key, prev)
+
+    yield set_
+    for key, value in saved.items():
+        graph.set_tuning(key, value)
+
+
 @pytest.fixture(autouse=True)
 def _announce(request):
     """Names each GPU test before it runs, so a run that dies still shows which case it was on."""

@@ -147,9 +147,9 @@ def test_double_stream_block_shape_sampled_rows(graph):
 @pytest.mark.parametrize("tokens,heads,kv_heads,causal,dtype", [
     (4608, 24, 24, False, we.BF16), (300, 4, 2, True, we.F16), (65, 3, 1, False, we.BF16), (1000, 8, 8, True, we.BF16),
     (257, 2, 2, False, we.F16), (64, 1, 1, False, we.BF16), (200, 2, 1, True, we.BF16), (2048, 4, 2, True, we.F16)])
-def test_dma_ring_path_equals_register_path(graph, monkeypatch, tokens, heads, kv_heads, causal, dtype):
+def test_dma_ring_path_equals_register_path(graph, tune, tokens, heads, kv_heads, causal, dtype):
     """Head dim 128 with 16-bit operands runs the V^T pre-pass and the ping-pong DMA kernel (or, with
-    WE_ATTN_PATH=ring, the single-phase DMA-ring kernel); their per-tile arithmetic is the register-staged
+    attn_path 2, the single-phase DMA-ring kernel); their per-tile arithmetic is the register-staged
     kernel's, so all three outputs are identical bit for bit."""
     rng = np.random.default_rng(tokens + heads)
     q, _ = to16(rng.standard_normal(tokens * heads * 128).astype(np.float32) * 2, dtype)
@@ -157,9 +157,9 @@ def test_dma_ring_path_equals_register_path(graph, monkeypatch, tokens, heads, k
     v, _ = to16(rng.standard_normal(tokens * kv_heads * 128).astype(np.float32), dtype)
     shape = we.AttentionShape(tokens, heads, kv_heads, 128, causal=causal)
     dma = run(graph, q, k, v, shape, dtype)
-    monkeypatch.setenv("WE_ATTN_PATH", "ring")
+    tune(attn_path=2)
     ring = run(graph, q, k, v, shape, dtype)
-    monkeypatch.setenv("WE_ATTN_PATH", "registers")
+    tune(attn_path=1)
     reg = run(graph, q, k, v, shape, dtype)
     assert np.array_equal(ring, reg)
     assert np.array_equal(dma, reg)

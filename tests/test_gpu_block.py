@@ -282,16 +282,15 @@ def test_double_block_full_shape_sampled_rows_match_the_oracle(graph):
 
 
 @pytest.mark.parametrize("grouped", [False, True])
-def test_double_block_overlapped_streams_equal_serial(graph, monkeypatch, grouped):
+def test_double_block_overlapped_streams_equal_serial(graph, tune, grouped):
     """The text stream on the second compute stream beside the image stream gives the serial block's outputs bit
     for bit at the full shape (512 + 4096 tokens, hidden 3072, bf16), forward after forward (the text GEMMs'
     split-K slices use that stream's own scratch). With the output, up and down projections of the two streams
     grouped into one launch each (the default), the text tiles run in the image's tile shape with all of K, so
-    the serial block is run with that tile shape and no split-K (WE_GEMM_CFG, WE_GEMM_SPLITK) for the
+    the serial block is run with that tile shape and no split-K (gemm_cfg, gemm_splitk) for the
     comparison."""
     if grouped:
-        monkeypatch.setenv("WE_GEMM_CFG", "0")
-        monkeypatch.setenv("WE_GEMM_SPLITK", "off")
+        tune(gemm_cfg=0, gemm_splitk=0)
     cfg, tt, rows, cols = B.DIT_DOUBLE_BLOCK, 512, 64, 64
     ti, H = rows * cols, cfg.hidden
     rng = np.random.default_rng(9)
@@ -318,10 +317,16 @@ def test_double_block_overlapped_streams_equal_serial(graph, monkeypatch, groupe
     graph.release(mark)
 
 
-def test_streamed_weights_give_the_resident_result(graph):
+@pytest.mark.parametrize("shape", ["small", "full"])
+def test_streamed_weights_give_the_resident_result(graph, shape):
     """Three blocks whose weights stream through two device slots from pinned host memory equal the same blocks
-    run from resident copies of their weights, bit for bit."""
-    cfg, tt, rows, cols = B.BlockConfig(256, 512, 2, 2, 128, 1e-6), 16, 4, 8
+    run from resident copies of their weights, bit for bit: at hidden 256 with 48 tokens, and at the benchmarked
+    shape (512 text + 4096 image tokens, hidden 3072, 226.7 MB of weights per block), where the copy of block
+    i + 1 runs on the copy stream while block i computes."""
+    if shape == "small":
+        cfg, tt, rows, cols = B.BlockConfig(256, 512, 2, 2, 128, 1e-6), 16, 4, 8
+    else:
+        cfg, tt, rows, cols = B.DIT_DOUBLE_BLOCK, 512, 64, 64
     ti, H = rows * cols, cfg.hidden
     rng = np.random.default_rng(6)
     tvec = graph.buffer(rng.uniform(-.2, .2, 6 * H).astype(np.float32))

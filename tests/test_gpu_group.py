@@ -3,7 +3,7 @@
 The double-stream block's text and image streams project with their own weights but the same N and K; grouped,
 the tiles of both run in one launch (full K per tile). Checks:
   * a qualifying pair (16-bit x, fp8 / 16-bit weights, aligned rows) equals two separate calls that use the same
-    tile shape (WE_GEMM_CFG) with split-K off (WE_GEMM_SPLITK=off), bit for bit, on every epilogue the block uses
+    tile shape (gemm_cfg) with split-K off (gemm_splitk 0), bit for bit, on every epilogue the block uses
     (plain, GELU, bias, gated residual with the residual in place or separate) and on ragged row counts, and is
     within the GEMM's own bar of the f64 oracle (gatedAdd of src/kernels/elementwise.ts:52-58 after the product);
   * the default tile pick for the pair gives the oracle's result too (the block's shapes: 512 + 4096 rows);
@@ -71,12 +71,11 @@ CASES = {
 
 
 @pytest.mark.parametrize("case", list(CASES))
-def test_pair_equals_separate_calls_and_the_oracle(graph, monkeypatch, case):
+def test_pair_equals_separate_calls_and_the_oracle(graph, tune, case):
     m0, m1, n, k, x_dt, w_dt, y_dt, flags, gated, bias, in_place, cfg = CASES[case]
     rng = np.random.default_rng(len(case))
     scale = 0.05 if w_dt == we.FP8 else 1.0
-    monkeypatch.setenv("WE_GEMM_CFG", str(cfg))
-    monkeypatch.setenv("WE_GEMM_SPLITK", "off")
+    tune(gemm_cfg=cfg, gemm_splitk=0)
     mark = graph.mark()
     probs = [_problem(graph, rng, m, n, k, x_dt, w_dt, y_dt, gated, bias, in_place, scale) for m in (m0, m1)]
     sep = [_buffers(graph, d, y_dt, n) for d in probs]
@@ -154,4 +153,60 @@ def test_group_refusals_launch_nothing(graph):
     with pytest.raises(we.WeError, match="split-K"):
         graph.matmul_group([dict(items[0], gate=graph.buffer(np.ones(256, np.float32)))], we.BF16, we.FP8, we.BF16,
                            we.EPI_SPLIT_K)
+    graph.release(mark)
+
+
+def test_dependent_pair_runs_in_order(graph):
+    """Item 1 reads item 0's output as its x (a chained pair): the paired launch would run both GEMMs' tiles at
+    once, so the call runs them in order instead. The result equals two separate calls, and item 1's output is
+    the oracle's product of item 0's output (rounded to bf16 as stored) with its own weights."""
+    m, n, k = 256, 512, 512  # n == k: item 0's output [m, n] is item 1's x [m, k]
+    rng = np.random.default_rng(77)
+    x0 = O.bf16_rne(rng.standard_normal(m * k).astype(np.float32))
+    w0, w1 = (make_weights(rng, n, k, we.FP8)[0] for _ in range(2))
+    p = we.matmul_params(m, n, k, 0.05, graph=graph)
+    mark = graph.mark()
+    xb, w0b, w1b = graph.buffer(x0), graph.buffer(w0), graph.buffer(w1)
+    outs = []
+    for grouped in (False, True):
+        mid, out = graph.buffer(m * n * 2), graph.buffer(m * n * 2)
+        items = [{"params": p, "x": xb, "w": w0b, "y": mid}, {"params": p, "x": mid, "w": w1b, "y": out}]
+        if grouped:
+            graph.matmul_group(items, we.BF16, we.FP8, we.BF16)
+        else:
+            for it in items:
+                graph.matmul(it["params"], we.BF16, it["x"], we.FP8, it["w"], we.BF16, it["y"])
+        outs.append((graph.read(mid), graph.read(out)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    h = outs[1][0].view(np.uint16)
+    want = O.matmul(O.matmul_params(m, n, k, 0.05), O.BF16, h, O.FP8, w1)
+    assert O.rel_error(decode(outs[1][1], we.BF16), want) < TOL[we.BF16]
+    graph.release(mark)
+
+
+def test_pair_writing_the_other_items_residual_runs_in_order(graph):
+    """Item 0's output is item 1's residual (bytes item 1 reads): ordered calls, item 0 first."""
+    m, n, k = 256, 512, 256
+    rng = np.random.default_rng(78)
+    xs = [O.bf16_rne(rng.standard_normal(m * k).astype(np.float32)) for _ in range(2)]
+    ws = [make_weights(rng, n, k, we.FP8)[0] for _ in range(2)]
+    gate = rng.uniform(-1, 1, n).astype(np.float32)
+    p = we.matmul_params(m, n, k, 0.05, graph=graph)
+    mark = graph.mark()
+    xb = [graph.buffer(x) for x in xs]
+    wb = [graph.buffer(w) for w in ws]
+    gb = graph.buffer(gate)
+    got = []
+    for grouped in (False, True):
+        y0, y1 = graph.buffer(m * n * 2), graph.buffer(m * n * 2)
+        items = [{"params": p, "x": xb[0], "w": wb[0], "y": y0},
+                 {"params": p, "x": xb[1], "w": wb[1], "y": y1, "gate": gb, "residual": y0}]
+        if grouped:
+            graph.matmul_group(items, we.BF16, we.FP8, we.BF16)
+        else:
+            graph.matmul(p, we.BF16, xb[0], we.FP8, wb[0], we.BF16, y0)
+            graph.matmul(p, we.BF16, xb[1], we.FP8, wb[1], we.BF16, y1, gate=gb, residual=y0)
+        got.append(graph.read(y1))
+    assert np.array_equal(got[0], got[1])
+    assert np.abs(decode(got[1], we.BF16)).max() > 0
     graph.release(mark)

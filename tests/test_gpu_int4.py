@@ -97,7 +97,7 @@ def test_refuses_unsupported_layouts(graph):
 
 
 @pytest.mark.parametrize("k", [256, 2048, 2304, 3072, 3584])
-def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
+def test_decode_kernel_matches_general_kernel(graph, k, tune):
     """M = 1 runs the pipelined decode kernel (x staged in LDS, weights through an LDS ring); it must give
     the general kernel's results at every K, including K whose x staging spans several passes per thread
     and whose blocks span several ring chunks (both sum exact f32 products; only the order inside an MFMA
@@ -106,7 +106,7 @@ def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
     rng = np.random.default_rng(k)
     words, scales, x, _ = make(rng, 1, n, k, 64)
     fast = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
-    monkeypatch.setenv("WE_INT4_PATH", "generic")
+    tune(int4_path=1)
     general = run(graph, 1, n, k, 64, words, scales, x, we.F16, we.F32)
     assert O.rel_error(fast, general) < 1e-6
 
@@ -115,7 +115,7 @@ def test_decode_kernel_matches_general_kernel(graph, k, monkeypatch):
     (2, 80, 256, 64, we.F16), (8, 100, 2304, 64, we.F16), (16, 64, 3584, 64, we.F16), (13, 200, 4096, 128, we.F16),
     (16, 33, 192, 64, we.BF16), (5, 70, 3072, 256, we.F16), (16, 130, 3584, 64, we.BF16), (1, 96, 1024, 64, we.F16),
     (4, 64, 18944, 512, we.F16), (9, 190, 64, 64, we.F16)])
-def test_shared_x_kernel_matches_general_kernel(graph, m, n, k, group, x_dt, monkeypatch):
+def test_shared_x_kernel_matches_general_kernel(graph, m, n, k, group, x_dt, tune):
     """2 <= M <= 16 with 16-bit x runs the shared-x kernel (x rows and weights through one LDS ring; 32 columns,
     8 x rows and 8 waves per workgroup for M <= 8, 64 columns, 16 rows and 16 waves above); forced at M = 1 as
     well here, with ragged N, K of one block up to
@@ -124,9 +124,30 @@ def test_shared_x_kernel_matches_general_kernel(graph, m, n, k, group, x_dt, mon
     rng = np.random.default_rng(m * 100 + k)
     words, scales, x, ox = make(rng, m, n, k, group, x_dt)
     want = O.matmul(O.matmul_params(m, n, k, 1.0), ox, x, O.INT4, words, scales=scales, group=group)
-    monkeypatch.setenv("WE_INT4_PATH", "generic")
+    tune(int4_path=1)
     general = run(graph, m, n, k, group, words, scales, x, x_dt, we.F32)
-    monkeypatch.setenv("WE_INT4_PATH", "shared")
+    tune(int4_path=2)
     got = run(graph, m, n, k, group, words, scales, x, x_dt, we.F32)
     assert O.rel_error(got, want) < 1e-5
     assert O.rel_error(got, general) < 1e-6
+
+
+def test_f32_activations_keep_every_mantissa_bit(graph):
+    """f32 x enters the int4 kernel as three bf16 planes whose sum is the f32 value exactly, so each product with a
+    code keeps all 24 bits of x. Every code is +1 (nibbles 1) with scale 1.0, and x alternates
+    1 + 2^-9 + (r + 1) 2^-20 and -1 in row r, so the large parts cancel and y[r, :] = 32 (2^-9 + (r + 1) 2^-20)
+    exactly (every partial sum is exact in f32). The 2^-20 terms lie below the second plane: two planes would give
+    32 * 2^-9 in every row, 2e-3 off."""
+    m, n, k, group = 4, 16, 64, 64
+    words = np.full(n * k // 8, 0x11111111, np.uint32)
+    scales = np.full(n * k // group, 0x3C00, np.uint16)
+    x = np.empty((m, k), np.float32)
+    for r in range(m):
+        x[r, 0::2] = np.float32(1 + 2.0 ** -9 + (r + 1) * 2.0 ** -20)
+        x[r, 1::2] = -1.0
+    assert np.float64(x[0, 0]) == 1 + 2.0 ** -9 + 2.0 ** -20  # exact in f32
+    exact = np.repeat([32 * (2.0 ** -9 + (r + 1) * 2.0 ** -20) for r in range(m)], n)
+    want = O.matmul(O.matmul_params(m, n, k, 1.0), O.F32, x.ravel(), O.INT4, words, scales=scales, group=group)
+    assert np.array_equal(want, exact)
+    got = run(graph, m, n, k, group, words, scales, x.ravel(), we.F32, we.F32)
+    assert np.array_equal(got, exact), np.abs(got - exact).max()

@@ -9,7 +9,6 @@ Tolerances (max|y - ref| / max|ref|, tests/gpu/matmul.test.ts:38-46):
   * f16 output: 2e-3 (one f16 rounding is 2^-11 of the value);  bf16 output: 1e-2 (2^-8 of the value).
 """
 import ctypes
-import os
 
 import numpy as np
 import pytest
@@ -179,13 +178,8 @@ def test_every_tile_config_with_ragged_edges(graph, cfg, x_dt, w_dt, path):
     x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
     w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
     p = we.matmul_params(m, n, k, 0.5, graph=graph)
-    os.environ["WE_GEMM_CFG"] = str(cfg)
-    os.environ["WE_GEMM_PATH"] = path
-    try:
+    with graph.tuned(gemm_cfg=cfg, gemm_generic=int(path == "generic")):
         got = run(graph, p, x_store, x_dt, w_store, w_dt, we.F32)
-    finally:
-        del os.environ["WE_GEMM_CFG"]
-        del os.environ["WE_GEMM_PATH"]
     want = O.matmul(O.matmul_params(m, n, k, 0.5), ox, x_oracle, ow, w_oracle)
     assert O.rel_error(got, want) < TOL_F32_OUT
 
@@ -244,7 +238,7 @@ def test_nan_codes_decode_like_the_shader(graph):
 @pytest.mark.parametrize("y_dt", [we.BF16, we.F32, we.F16])
 @pytest.mark.parametrize("gated", [False, True])
 @pytest.mark.parametrize("cfg", [None, 0])
-def test_fast_epilogue_gelu_without_bias(graph, monkeypatch, y_dt, gated, cfg):
+def test_fast_epilogue_gelu_without_bias(graph, tune, y_dt, gated, cfg):
     """The fast kernel's whole-sub-tile epilogue with GELU and no bias: the up-projection as benchmarked (256 x 256
     ping-pong tiles, bf16 out) and the gated form, against the oracle product followed by or_gelu_tanh (and the
     reference's gatedAdd). 512 x 768 outputs are 2 x 3 whole 256 x 256 tiles; cfg None takes the default pick."""
@@ -256,7 +250,7 @@ def test_fast_epilogue_gelu_without_bias(graph, monkeypatch, y_dt, gated, cfg):
     gate = rng.uniform(-1.5, 1.5, n).astype(np.float32) if gated else None
     res_store, res_vals = _store(rng.standard_normal(m * n), y_dt) if gated else (None, None)
     if cfg is not None:
-        monkeypatch.setenv("WE_GEMM_CFG", str(cfg))
+        tune(gemm_cfg=cfg)
     p = we.matmul_params(m, n, k, 0.02, graph=graph)
     mark = graph.mark()
     yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
@@ -435,7 +429,7 @@ def test_lora_down_split_over_long_k(graph):  # tests/gpu/lora.test.ts:120-146
     (33, 129, 768, we.F16, we.F16, we.EPI_BIAS),
     (256, 384, 2048, we.BF16, we.F32, we.EPI_GELU), (256, 384, 2048, we.BF16, we.BF16, 0),
     (200, 1000, 1024, we.BF16, we.F32, we.EPI_BIAS)])
-def test_small_m_split_k_reduction(graph, monkeypatch, m, n, k, x_dt, y_dt, flags):
+def test_small_m_split_k_reduction(graph, tune, m, n, k, x_dt, y_dt, flags):
     """fp8 GEMMs whose tiles fill few workgroup slots (small M; or M > 64 with few tiles, like the
     double-stream block's 512-token text projections) split K across workgroups and a reduce pass adds the
     slices. The result matches the oracle, repeats bit for bit (slices are summed in slice order), and
@@ -458,7 +452,7 @@ def test_small_m_split_k_reduction(graph, monkeypatch, m, n, k, x_dt, y_dt, flag
         want = want + start
     tol = 1e-4 if flags & we.EPI_GELU else TOL[y_dt]
     assert O.rel_error(runs[0], want) < tol
-    monkeypatch.setenv("WE_GEMM_SPLITK", "off")
+    tune(gemm_splitk=0)
     unsplit = run(graph, p, x_store, x_dt, w, we.FP8, y_dt, flags=flags, bias=bias, y_init=y_init)
     assert O.rel_error(unsplit, want) < tol
 
@@ -472,7 +466,7 @@ def _store(vals, dt):
 
 
 @pytest.mark.parametrize("case", ["fast_full", "fast_ragged", "small_m_split", "generic_f32", "f16_out", "gelu_bias"])
-def test_gated_residual_equals_gemm_then_gated_add(graph, case, monkeypatch):
+def test_gated_residual_equals_gemm_then_gated_add(graph, case, tune):
     """y = residual + gate * v (v: scale, bias, GELU of the product), against the f64 oracle of the product followed
     by the reference's gatedAdd, on every epilogue: the fast kernel's whole-tile and per-value paths, the split-K
     reduce pass (small M), the general kernel (f32 operands) and f16 output."""
@@ -494,7 +488,7 @@ def test_gated_residual_equals_gemm_then_gated_add(graph, case, monkeypatch):
     yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
     bb = graph.buffer(bias) if bias is not None else None
     if case == "generic_f32":
-        monkeypatch.setenv("WE_GEMM_PATH", "generic")
+        tune(gemm_generic=1)
     graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=flags, gate=gb, residual=rb)
     got = decode(graph.read(yb), y_dt)
     graph.release(mark)
@@ -568,7 +562,7 @@ def _sigmoid(v):
 
 @pytest.mark.parametrize("mul", [we.MUL_SWIGLU, we.MUL_SIGMOID_GATE])
 @pytest.mark.parametrize("case", ["fast_full", "fast_ragged", "small_m_split", "generic_f32", "f16_out", "bias"])
-def test_product_epilogue_equals_gemm_then_the_elementwise_step(graph, case, mul, monkeypatch):
+def test_product_epilogue_equals_gemm_then_the_elementwise_step(graph, case, mul, tune):
     """y = silu(aux) * v (swiglu with the GEMM as `up`) or aux * sigmoid(v) (sigmoidGate with the GEMM as `gate`),
     v the scaled (biased) product, against the f64 oracle of the product followed by the reference's formula
     (src/kernels/elementwise.ts:38-50), on every epilogue: the fast kernel's whole-tile and per-value paths, the
@@ -589,7 +583,7 @@ def test_product_epilogue_equals_gemm_then_the_elementwise_step(graph, case, mul
     yb = graph.buffer(m * n * we.ELEM_BYTES[y_dt])
     bb = graph.buffer(bias) if bias is not None else None
     if case == "generic_f32":
-        monkeypatch.setenv("WE_GEMM_PATH", "generic")
+        tune(gemm_generic=1)
     graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=we.EPI_BIAS if bias is not None else 0, mul=mul, aux=ab)
     got = decode(graph.read(yb), y_dt)
     graph.release(mark)

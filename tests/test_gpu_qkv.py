@@ -39,7 +39,7 @@ CASES = {
 
 
 @pytest.mark.parametrize("case", list(CASES))
-def test_fused_qkv_projection(graph, monkeypatch, case):
+def test_fused_qkv_projection(graph, tune, case):
     cfg, m, heads, k, y_dt, rope_from, with_bias = CASES[case]
     hid = heads * 128
     n = 3 * hid
@@ -54,7 +54,7 @@ def test_fused_qkv_projection(graph, monkeypatch, case):
     cos = rng.uniform(-1, 1, max(rot_rows, 1) * 64).astype(np.float32)
     sin = np.sqrt(1 - cos.astype(np.float64) ** 2).astype(np.float32)
     if cfg is not None:
-        monkeypatch.setenv("WE_GEMM_CFG", str(cfg))
+        tune(gemm_cfg=cfg)
     x_dt = we.BF16
     p = we.matmul_params(m, n, k, scale, graph=graph)
     mark = graph.mark()

@@ -103,3 +103,36 @@ def test_noalloc_refuses_a_split_plan_beyond_its_array(graph):
     graph.matmul(p, we.BF16, xb, we.FP8, wb, we.BF16, y)
     graph.sync()
     graph.release(mark)
+
+
+def test_noalloc_refuses_the_second_stream_and_other_contexts(graph):
+    """Every call on a GPU shares its fixed array, so calls that could overlap are refused rather than raced: a call
+    while compute stream 1 is selected fails, and so does a call from a second live context while this one holds
+    the array; we_matmul runs in both places, and this context's calls on stream 0 go on working."""
+    m, n, k = 16, 1024, 2048
+    rng = np.random.default_rng(24)
+    x, _, w = _operands(rng, m, n, k, we.BF16)
+    p = we.matmul_params(m, n, k, 0.02, graph=graph)
+    mark = graph.mark()
+    xb, wb, y, y2 = graph.buffer(x), graph.buffer(w), graph.buffer(m * n * 2), graph.buffer(m * n * 2)
+    graph.matmul_noalloc(p, we.BF16, xb, we.FP8, wb, we.BF16, y)  # this context now holds the device's array
+    graph.stream(1)
+    try:
+        with pytest.raises(we.WeError, match="compute stream 0 only"):
+            graph.matmul_noalloc(p, we.BF16, xb, we.FP8, wb, we.BF16, y2)
+    finally:
+        graph.stream(0)
+    other = we.Graph(0)
+    try:
+        op = we.matmul_params(m, n, k, 0.02, graph=other)
+        ox, ow, oy = other.buffer(x), other.buffer(w), other.buffer(m * n * 2)
+        with pytest.raises(we.WeError, match="belongs to another live context"):
+            other.matmul_noalloc(op, we.BF16, ox, we.FP8, ow, we.BF16, oy)
+        other.matmul(op, we.BF16, ox, we.FP8, ow, we.BF16, oy)
+        other_y = other.read(oy)
+    finally:
+        other.destroy()
+    graph.matmul_noalloc(p, we.BF16, xb, we.FP8, wb, we.BF16, y2)
+    assert np.array_equal(graph.read(y2), graph.read(y))
+    assert np.array_equal(other_y, graph.read(y))
+    graph.release(mark)

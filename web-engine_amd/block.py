@@ -265,6 +265,60 @@ class DoubleBlock:
         else:
             self._streams(out_step)
 
+    def profile(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img, reps=5):
+        """Where the block's time goes (profileBlock, src/bench/block.ts:17-95): the steps of forward() in its
+        order, each run on its own on compute stream 0 (`reps` back-to-back calls between HIP events, after one
+        untimed call), per stream, without the overlap and grouping of forward(). Every step rewrites its outputs
+        from inputs it does not write, so repeating it changes nothing. Returns [{name, kind, us}], kind one of
+        linear / attention / other as in the reference."""
+        g, cfg, dt = self.graph, self.cfg, self.dtype
+        H, hd, heads, e = cfg.hidden, cfg.head_dim, cfg.heads, we.ELEM_BYTES[dt]
+        sl = we.Graph.slice
+        ws, xs, outs, names = (w_txt, w_img), (x_txt, x_img), (out_txt, out_img), ("text", "image")
+        steps = []
+        for s in (0, 1):
+            w, rows, r0, h, u, mod = ws[s], self.rows[s], self.row0[s], self.h[s], self.u[s], self.mod[s]
+            cos, sin = (rope_img.cos, rope_img.sin) if s == 1 else (None, None)
+            steps += [
+                (f"norm 1 + modulation ({names[s]})", "other",
+                 lambda w=w, rows=rows, h=h, mod=mod, s=s: g.rmsnorm_mod(rows, H, cfg.eps, 1.0, dt, xs[s], w.norm1,
+                                                                          tvec, w.table, 6 * H, mod, h)),
+                (f"qkv + q/k norm{' + rope' if s else ''} ({names[s]})", "linear",
+                 lambda w=w, rows=rows, r0=r0, h=h, cos=cos, sin=sin: g.matmul_qk_norm_rope(
+                     we.matmul_params(rows, 3 * H, H, w.qkv.scale, y_offset=r0 * 3 * H, graph=g), dt, h, we.FP8,
+                     w.qkv.buffer, dt, self.qkv, heads, heads, cfg.eps, 1.0, w.norm_q, w.norm_k, 0, cos, sin))]
+        steps.append(("attention (joint)", "attention",
+                      lambda: g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
+                                          sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H,
+                                          v_stride=3 * H, out_stride=H)))
+        for s in (0, 1):
+            w, rows, r0, h, u, mod = ws[s], self.rows[s], self.row0[s], self.h[s], self.u[s], self.mod[s]
+            steps += [
+                (f"out + gated residual ({names[s]})", "linear",
+                 lambda w=w, rows=rows, r0=r0, mod=mod, s=s: g.matmul(
+                     we.matmul_params(rows, H, H, w.proj.scale, x_offset=r0 * H, graph=g), dt, self.o, we.FP8,
+                     w.proj.buffer, dt, self.x1[s], gate=sl(mod, 2 * H * 4, H * 4), residual=xs[s])),
+                (f"norm 2 ({names[s]})", "other",
+                 lambda w=w, rows=rows, h=h, mod=mod, s=s: g.rmsnorm(rows, H, cfg.eps, 1.0, dt, self.x1[s], w.norm2,
+                                                                      sl(mod, 3 * H * 4, H * 4),
+                                                                      sl(mod, 4 * H * 4, H * 4), h)),
+                (f"mlp up + gelu ({names[s]})", "linear",
+                 lambda w=w, rows=rows, h=h, u=u: g.matmul(we.matmul_params(rows, cfg.mlp, H, w.up.scale, graph=g), dt,
+                                                           h, we.FP8, w.up.buffer, dt, u, flags=we.EPI_GELU)),
+                (f"mlp down + gated residual ({names[s]})", "linear",
+                 lambda w=w, rows=rows, u=u, mod=mod, s=s: g.matmul(
+                     we.matmul_params(rows, H, cfg.mlp, w.down.scale, graph=g), dt, u, we.FP8, w.down.buffer, dt,
+                     outs[s], gate=sl(mod, 5 * H * 4, H * 4), residual=self.x1[s]))]
+        out = []
+        for name, kind, fn in steps:
+            fn()
+            g.sync()
+            g.timer_start()
+            for _ in range(reps):
+                fn()
+            out.append({"name": name, "kind": kind, "us": g.timer_stop() / reps * 1e3})
+        return out
+
 
 # ------------------------------------------------------------------------------------------ weight streaming
 

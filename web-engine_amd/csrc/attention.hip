@@ -817,21 +817,17 @@ namespace {
 // head dim 128, 16-bit, operand extents within the 32-bit buffer offsets: the DMA kernels
 bool attn_dma_ok(const AttnLaunch& L) {
   if (L.dtype == F32 || L.dim != 128 || L.tokens == 0 || L.heads == 0) return false;
-  const char* path = getenv("WE_ATTN_PATH");
-  if (path && strcmp(path, "registers") == 0) return false;
+  if (L.path == 1) return false;  // Tuning::attn_path: the register-staged kernel
   const uint64_t kb = ((uint64_t)(L.tokens - 1) * L.k_stride + (uint64_t)L.kv_heads * 128) * 2;
   const uint64_t vb = ((uint64_t)(L.tokens - 1) * L.v_stride + (uint64_t)L.kv_heads * 128) * 2;
   return kb < kAttInvalid && vb < kAttInvalid;
 }
-bool attn_ring_path() {
-  const char* path = getenv("WE_ATTN_PATH");
-  return path && strcmp(path, "ring") == 0;
-}
+bool attn_ring_path(const AttnLaunch& L) { return L.path == 2; }
 }  // namespace
 
 // Only the ring kernel (WE_ATTN_PATH=ring) stages V^T through scratch; the default kernel reads V as it is.
 size_t attention_scratch_bytes(const AttnLaunch& L) {
-  if (!attn_dma_ok(L) || !attn_ring_path()) return 0;
+  if (!attn_dma_ok(L) || !attn_ring_path(L)) return 0;
   const size_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;
   return (size_t)L.kv_heads * 128 * tp * 2;
 }
@@ -856,7 +852,7 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
   if (attn_dma_ok(L)) {
     a.nqb = (L.tokens + DMA_BM - 1) / DMA_BM;
     const dim3 grid(a.nqb * L.heads);
-    if (attn_ring_path()) {
+    if (attn_ring_path(L)) {
       // the ring kernel: V^T pre-pass into scratch, then the one-phase DMA ring
       if (!L.scratch) return hipErrorInvalidValue;
       const uint32_t tp = (L.tokens + ATT_BN - 1) / ATT_BN * ATT_BN;

@@ -36,6 +36,9 @@ namespace we {
 namespace {
 
 constexpr int BK = 64;
+#ifndef WE_GEMM_LIC
+#define WE_GEMM_LIC 0
+#endif
 constexpr uint32_t kInvalid = 0x80000000u;  // a byte offset past every extent: the load returns 0
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 family)
 
@@ -180,13 +183,19 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   static_assert(A_INS % NW == 0 && (BN * B_ROW) % 1024 == 0, "stage loads must split evenly over the waves");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && WTM >= 32, "wave tile");
   static_assert(!PP || NW * 32 * (WTN * 2 + 16) <= S * STAGE, "the epilogue's row staging fits the stages");
-  constexpr int A_PW = A_INS / NW, B_PW = B_INS / NW, L = A_PW + B_PW;  // loads per wave per stage
+  // Ping-pong tiles: the ring's loads are issued by the waves of group 1 alone, between the MFMAs of their compute
+  // phase (LIC), so the memory phases of both groups hold only fragment reads. Other tiles: every wave loads.
+  constexpr bool LIC = PP && WE_GEMM_LIC;
+  constexpr int NL = LIC ? NW / 2 : NW;                                   // waves that issue loads
+  static_assert(A_INS % NL == 0 && B_INS % NL == 0, "stage loads split evenly over the loading waves");
+  constexpr int A_PW = A_INS / NL, B_PW = B_INS / NL, L = A_PW + B_PW;  // loads per loading wave per stage
   constexpr int B_RPI = 1024 / B_ROW;                                     // weight rows per load
   constexpr int B_CPR = B_ROW / 16;                                       // 16-B chunks per weight row
   __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int lw = wave % NL;  // this wave's share of the loads (LIC: group 1's waves 0 .. NW / 2 - 1)
   const int h = lane >> 5, l32 = lane & 31;
 
   uint32_t pid = xcd_remap_f(blockIdx.x, gridDim.x);
@@ -226,44 +235,48 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)a.w_bytes, kRsrcWord3);
 
   // ---- per-lane source offsets of the direct-to-LDS loads (k = 0 of the block), invalid past M / N
+  // The rows of a lane's successive loads are 8 NL (x) and B_RPI NL (weights) apart, multiples of 16 (swz128) and of 32
+  // (swz64), so its chunk, and the first k of that chunk inside the 64-k block (ka, kb8), is the same for every load.
+  static_assert((8 * NL) % 16 == 0 && (B_RPI * NL) % (B8 ? 32 : 16) == 0, "one swizzled chunk per lane");
   uint32_t offa[A_PW], offb[B_PW];
-  int ka[A_PW], kb8[B_PW];  // first k of the lane's chunk inside the 64-k block
+  int ka, kb8;
 #pragma unroll
   for (int i = 0; i < A_PW; i++) {
-    const int ins = wave + i * NW;
+    const int ins = lw + i * NL;
     const int r = ins * 8 + (lane >> 3);
     const int c = (lane & 7) ^ swz128(r);
     const uint32_t row = row0 + r;
     offa[i] = row < a.m ? (row * a.x_stride + c * 8) * 2 : kInvalid;
-    ka[i] = c * 8;
+    if (i == 0) ka = c * 8;
   }
 #pragma unroll
   for (int j = 0; j < B_PW; j++) {
-    const int ins = wave + j * NW;
+    const int ins = lw + j * NL;
     const int r = ins * B_RPI + lane / B_CPR;
     const int c = (lane % B_CPR) ^ (B8 ? swz64(r) : swz128(r));
     const uint32_t col = col0 + r;
     offb[j] = r < BN && col < a.n ? (col * a.w_stride * WB + c * 16) : kInvalid;
-    kb8[j] = c * 16 / WB;
+    if (j == 0) kb8 = c * 16 / WB;
   }
 
-  // issue the loads of the 64-k block starting at kb into stage st
-  auto issue = [&](uint32_t kb, int st) {
+  // load q (0 .. L - 1) of this wave's share of the 64-k block starting at kb, into stage st
+  auto issue_one = [&](auto Q, uint32_t kb, int st) {
+    constexpr int q = decltype(Q)::value;
     const bool full = kb + BK <= k_end;  // only the last block of a slice can be partial
     char* base = lds + st * STAGE;
-#pragma unroll
-    for (int i = 0; i < A_PW; i++) {
-      const uint32_t o = (full || kb + ka[i] < k_end) ? offa[i] : kInvalid;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t*)(base + (wave + i * NW) * 1024), 16, o, (int)(kb * 2), 0,
+    if constexpr (q < A_PW) {
+      const uint32_t o = (full || kb + ka < k_end) ? offa[q] : kInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t*)(base + (lw + q * NL) * 1024), 16, o, (int)(kb * 2), 0,
                                                0);
-    }
-#pragma unroll
-    for (int j = 0; j < B_PW; j++) {
-      const uint32_t o = (full || kb + kb8[j] < k_end) ? offb[j] : kInvalid;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(base + A_BYTES + (wave + j * NW) * 1024), 16, o,
+    } else {
+      constexpr int j = q - A_PW;
+      const uint32_t o = (full || kb + kb8 < k_end) ? offb[j] : kInvalid;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(base + A_BYTES + (lw + j * NL) * 1024), 16, o,
                                                (int)(kb * WB), 0, 0);
     }
   };
+  // issue this wave's share of the loads of the 64-k block starting at kb into stage st
+  auto issue = [&](uint32_t kb, int st) { static_for<0, L>([&](auto Q) { issue_one(Q, kb, st); }); };
 
   // ---- per-lane LDS read offsets of the MFMA fragments (within a stage)
   // k order inside a 64-k block: MFMA step s, lane half h uses the 8 k of logical chunk 4h + s for both
@@ -348,9 +361,14 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
           }
       }
     };
-    auto compute_block = [&]() {
+    // LD: issue this wave's L loads of the block at kb into stage st between the MFMAs (L / 4 per step)
+    auto compute_block = [&](bool ld, uint32_t kb, int st) {
       static_for<0, 4>([&](auto Q) {
         constexpr int q = decltype(Q)::value;
+        if (LIC && ld) {  // wave-uniform
+          constexpr int PER = (L + 3) / 4, Q0 = q * PER, Q1 = Q0 + PER < L ? Q0 + PER : L;
+          static_for<Q0, Q1>([&](auto QQ) { issue_one(QQ, kb, st); });
+        }
         u32x4 w[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -376,7 +394,34 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       if (S >= 3 && t + 2 < nk) wait_vmcnt<(S >= 3 ? (S - 2) * L : 0)>();
       else wait_vmcnt<0>();
     };
-    if (nk > 0) {
+    if (nk > 0 && LIC) {
+      // Group 1 issues every load of the ring. Prologue: blocks 0 .. S - 1 into stages 0 .. S - 1. In its compute
+      // phase of block t (interval 2t + 2) a group-1 wave loads block t + S into block t's stage, which both groups
+      // have read by then (group 0 in interval 2t, group 1 in 2t + 1). A group-1 wave's loads of block t + 1 must
+      // land before the barrier that ends interval 2t + 1 (group 0 reads block t + 1 in interval 2t + 2): it waits
+      // for them after its memory phase of block t, when at most the blocks up to t + S - 1 have been issued.
+      if (grp == 1) {
+#pragma unroll
+        for (int p = 0; p < S; p++)
+          if (p < nk) issue(k_begin + (uint32_t)p * BK, p);
+        if (nk >= S) wait_vmcnt<(S - 1) * L>();
+        else wait_vmcnt<0>();
+      }
+      lds_barrier();
+      if (grp == 1) pp_barrier();  // group 1 sits out interval 0
+      int cur = 0;
+      for (int t = 0; t < nk; ++t) {
+        memory_block((uint32_t)(cur * STAGE));
+        if (grp == 1 && t + 1 < nk) {
+          if (S >= 3 && t + S - 1 < nk) wait_vmcnt<(S >= 3 ? (S - 2) * L : 0)>();
+          else wait_vmcnt<0>();
+        }
+        pp_barrier();
+        compute_block(grp == 1 && t + S < nk, k_begin + (uint32_t)(t + S) * BK, cur);
+        if (!(grp == 1 && t + 1 == nk)) pp_barrier();  // both groups pass the same number of barriers
+        cur = cur + 1 == S ? 0 : cur + 1;
+      }
+    } else if (nk > 0) {
 #pragma unroll
       for (int p = 0; p < S - 1; p++)
         if (p < nk) issue(k_begin + (uint32_t)p * BK, p);
@@ -392,7 +437,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         memory_block(cur_off);
         wait_next(t);
         pp_barrier();
-        compute_block();
+        compute_block(false, 0u, 0);
         wait_next(t);
         if (!(grp == 1 && t + 1 == nk)) pp_barrier();  // both groups pass the same number of barriers
         cur = cur + 1 == S ? 0 : cur + 1;
@@ -560,7 +605,9 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         const float tot = red[rloc * WAVES_N + (wn & ~1)] + red[rloc * WAVES_N + (wn | 1)];
         const float inv = 1.0f / sqrtf(tot / 128.0f + a.qk_eps);
         const uint32_t row = row0 + rloc;
-        const bool rot = a.qk_cos && row >= a.qk_rope_from;
+        // padding rows of the last M tile (row >= M) form no table address: the checked span of cos / sin
+        // ends at row M - 1
+        const bool rot = a.qk_cos && row >= a.qk_rope_from && row < a.m;
         const size_t trow = rot ? (size_t)(row - a.qk_rope_from) * 64 : 0;
         const size_t yrow = (size_t)a.y_offset + (size_t)row * a.y_stride + col0 + wn * WTN;
 #pragma unroll
@@ -820,15 +867,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(FastArgs a) {
 
 // Does the split-K reduce pass read each tile's partial sums from the L2 of the XCD that computed them? With a
 // multiple of 8 tiles and at most 16 MiB of weights (2 MiB per XCD, so the weight stream does not push the sums
-// out). WE_GEMM_REDUCE_XCD=off: never (measurements).
-static bool reduce_in_l2(uint64_t tiles, uint64_t weight_bytes) {
-  const char* xm = getenv("WE_GEMM_REDUCE_XCD");
-  if (xm && strcmp(xm, "off") == 0) return false;
-  return tiles % 8 == 0 && weight_bytes <= (16u << 20);
+// out). `on` 0 (Tuning::gemm_reduce_xcd): never (measurements).
+static bool reduce_in_l2(uint64_t tiles, uint64_t weight_bytes, int on) {
+  return on && tiles % 8 == 0 && weight_bytes <= (16u << 20);
 }
 
 template <int BM, int BN, int WM, int WN, bool IS_F16, int BT, int S, bool PP = false>
-static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
+static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, int reduce_xcd, hipStream_t s) {
   a.tiles_m = (a.m + BM - 1) / BM;
   a.tiles_n = (a.n + BN - 1) / BN;
   uint32_t tiles = a.tiles_m * a.tiles_n;
@@ -850,9 +895,9 @@ static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
     // sum in slice order either way. Measured on MI355X (graph replays): 64 x 3072 x 3072 fp8 10.9 -> 9.2 us per
     // call, 12.2 -> 11.2 us with the weights streamed from HBM, 16 x 3072 x 3072 8.5 -> 8.1 us; but 64 x 3072 x
     // 12288 (37.7 MB of weights) 19.5 -> 20.2 us, so only up to 16 MB of weights (2 MB per XCD).
-    // WE_GEMM_REDUCE_XCD=off: the row-major mapping (measurements)
+    // reduce_xcd 0: the row-major mapping (measurements)
     static_assert((BM * BN / 4) % 256 == 0, "whole reduce workgroups per tile");
-    if (reduce_in_l2(tiles, a.w_bytes)) {
+    if (reduce_in_l2(tiles, a.w_bytes, reduce_xcd)) {
       const dim3 rg(tiles * (BM * BN / 4 / 256));
       switch (a.y_dtype) {
         case F32: hipLaunchKernelGGL((splitk_reduce_kernel<F32, BM, BN>), rg, dim3(256), 0, s, a); break;
@@ -879,18 +924,18 @@ static hipError_t launch_fast_cfg(FastArgs a, uint32_t splits, hipStream_t s) {
 }
 
 template <bool IS_F16, int BT>
-static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg, hipStream_t s) {
+static hipError_t launch_fast_types(const FastArgs& a, uint32_t splits, int cfg, int rx, hipStream_t s) {
   constexpr bool B8 = BT == FP8;
   switch (cfg) {
     // ping-pong schedule, 2 x 4 waves (128 x 64 each): measured on MI355X the fastest layout for fp8
     // and 16-bit weights
-    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, s);
-    case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, s);
+    case GEMM_CFG_256x256: return launch_fast_cfg<256, 256, 2, 4, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, rx, s);
+    case GEMM_CFG_256x128: return launch_fast_cfg<256, 128, 4, 2, IS_F16, BT, 3>(a, splits, rx, s);
     // 256 x 192 (4 x 2 waves of 64 x 96, ping-pong): 4096 x 3072 outputs are exactly 256 tiles
-    case GEMM_CFG_256x192: return launch_fast_cfg<256, 192, 4, 2, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, s);
-    case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, s);
-    case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, s);
-    default: return launch_fast_cfg<32, 64, 1, 2, IS_F16, BT, 3>(a, splits, s);
+    case GEMM_CFG_256x192: return launch_fast_cfg<256, 192, 4, 2, IS_F16, BT, B8 ? 3 : 2, true>(a, splits, rx, s);
+    case GEMM_CFG_128x128: return launch_fast_cfg<128, 128, 2, 2, IS_F16, BT, 3>(a, splits, rx, s);
+    case GEMM_CFG_64x64: return launch_fast_cfg<64, 64, 2, 2, IS_F16, BT, 3>(a, splits, rx, s);
+    default: return launch_fast_cfg<32, 64, 1, 2, IS_F16, BT, 3>(a, splits, rx, s);
   }
 }
 
@@ -987,7 +1032,7 @@ GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits) {
     // 7.61 / 8.67 us, 64 x 4096 x 4096 10.92 / 12.47 -> 10.23 / 11.78 us (12 slices of 64 x 3072 x 3072: 10.5 us);
     // without the L2 reduce more slices only add partial-sum traffic (64 x 6144 x 3072: 14.1 -> 15.9 us)
     const uint64_t one = (kCUs + tiles - 1) / tiles, two = (2 * kCUs + tiles - 1) / tiles;
-    rs = reduce_in_l2(tiles, weight_extent(L)) ? (uint32_t)std::max<uint64_t>(one, std::min<uint64_t>(8, two))
+    rs = reduce_in_l2(tiles, weight_extent(L), L.reduce_xcd) ? (uint32_t)std::max<uint64_t>(one, std::min<uint64_t>(8, two))
                                                : (uint32_t)one;
   } else {
     // larger M: split when the tiles fill less than half of the workgroup slots (M = 512, N = 3072:
@@ -1085,12 +1130,13 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
     a.rsplits = splits;
   }
   const int cfg = L.cfg >= 0 ? L.cfg : pick_fast_cfg(L.m, L.n, splits, L.w_dtype == FP8);
+  const int rx = L.reduce_xcd;
   if (f16) {
-    if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, stream);
-    return launch_fast_types<true, F16>(a, splits, cfg, stream);
+    if (L.w_dtype == FP8) return launch_fast_types<true, FP8>(a, splits, cfg, rx, stream);
+    return launch_fast_types<true, F16>(a, splits, cfg, rx, stream);
   }
-  if (L.w_dtype == FP8) return launch_fast_types<false, FP8>(a, splits, cfg, stream);
-  return launch_fast_types<false, BF16>(a, splits, cfg, stream);
+  if (L.w_dtype == FP8) return launch_fast_types<false, FP8>(a, splits, cfg, rx, stream);
+  return launch_fast_types<false, BF16>(a, splits, cfg, rx, stream);
 }
 
 bool gemm_pair_ok(const GemmLaunch& A, const GemmLaunch& B) {
@@ -1116,11 +1162,11 @@ hipError_t gemm_fast_launch_pair(const GemmLaunch& A, const GemmLaunch& B, hipSt
   a.grp = 1;
   const int cfg = A.cfg >= 0 ? A.cfg : pick_fast_cfg(A.m + B.m, A.n, 1, A.w_dtype == FP8);
   if (A.x_dtype == F16) {
-    if (A.w_dtype == FP8) return launch_fast_types<true, FP8>(a, 1, cfg, stream);
-    return launch_fast_types<true, F16>(a, 1, cfg, stream);
+    if (A.w_dtype == FP8) return launch_fast_types<true, FP8>(a, 1, cfg, 0, stream);
+    return launch_fast_types<true, F16>(a, 1, cfg, 0, stream);
   }
-  if (A.w_dtype == FP8) return launch_fast_types<false, FP8>(a, 1, cfg, stream);
-  return launch_fast_types<false, BF16>(a, 1, cfg, stream);
+  if (A.w_dtype == FP8) return launch_fast_types<false, FP8>(a, 1, cfg, 0, stream);
+  return launch_fast_types<false, BF16>(a, 1, cfg, 0, stream);
 }
 
 }  // namespace we

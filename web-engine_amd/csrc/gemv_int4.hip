@@ -104,10 +104,11 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
 }
 
 // x fragments of one 64-k block for lane (m, g): k = 64b + 16g + 8e + (0..7), e = 0, 1. 16-bit x: one
-// 16-B load per e. f32 x: two 16-B loads per e, split into hi + lo bf16 planes.
+// 16-B load per e. f32 x: two 16-B loads per e, split into three bf16 planes hi + mid + lo whose sum is the f32
+// value exactly (8 + 8 + 8 significant bits), so every product with an int4 code keeps all 24 bits.
 template <int XT>
 struct XFrag {
-  static constexpr int NA = XT == F32 ? 2 : 1;
+  static constexpr int NA = XT == F32 ? 3 : 1;
   u32x4 v[2][NA];
 };
 
@@ -120,16 +121,19 @@ __device__ __forceinline__ void load_x(const __amdgpu_buffer_rsrc_t& rx, uint32_
       const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, e * 32 + 16, 0));
       float fl[8] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w),
                      __uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w)};
-      uint32_t hi[8], lo[8];
+      uint32_t hi[8], mid[8], lo[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         hi[i] = f32_to_bf16(fl[i]);
-        lo[i] = f32_to_bf16(fl[i] - bf16_to_f32((uint16_t)hi[i]));
+        const float r1 = fl[i] - bf16_to_f32((uint16_t)hi[i]);  // exact: at most 16 significant bits
+        mid[i] = f32_to_bf16(r1);
+        lo[i] = f32_to_bf16(r1 - bf16_to_f32((uint16_t)mid[i]));  // exact: at most 8 significant bits
       }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         f.v[e][0][i] = hi[2 * i] | (hi[2 * i + 1] << 16);
-        f.v[e][1][i] = lo[2 * i] | (lo[2 * i + 1] << 16);
+        f.v[e][1][i] = mid[2 * i] | (mid[2 * i + 1] << 16);
+        f.v[e][2][i] = lo[2 * i] | (lo[2 * i + 1] << 16);
       }
     }
   } else {
@@ -750,9 +754,9 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
   uint32_t gshift = 0;
   while ((64u << gshift) < L.group) gshift++;
   a.gshift = gshift;
-  // "generic" / "shared" force a kernel (tests, measurements)
-  const char* path = getenv("WE_INT4_PATH");
-  const bool generic = path && !strcmp(path, "generic");
+  // L.path (Tuning::int4_path) 1 / 2 / 3 forces the general / shared-x / LDS-ring kernel (tests, measurements)
+  const int path = L.path;
+  const bool generic = path == 1;
   const bool ring = L.x_dtype != F32 && L.m <= 16 && (64u << gshift) == L.group && !generic;
   const bool pipe = ring && !path && (uint64_t)L.m * L.k * 2 <= (uint64_t)PIPE_XMAX && L.k / 64 <= 4 * (uint32_t)PIPE_MAXB;
   // M = 1, f16 x, K <= 4096: every weight in flight at once (WE_INT4_PATH=pipe selects the ring kernel)
@@ -772,7 +776,7 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
     }
     return hipGetLastError();
   }
-  const bool force_pipe = path && !strcmp(path, "pipe");
+  const bool force_pipe = path == 3;
   if (ring && !pipe && !force_pipe && L.k / L.group <= 64) {
     // M <= 8: 32 columns and 8 staged x rows per workgroup; larger M: 64 columns, 16 rows (32 columns there
     // double the x traffic and leave a third of each chunk's loads spare: slower)

@@ -20,6 +20,18 @@ enum GemmCfgId {
   GEMM_CFG_256x192 = 5
 };
 
+// Kernel-choice switches of a context (we_set_tuning): the context reads the WE_* environment variables once, when
+// it is created, and every launch takes the values from here. Keys and meanings as WE_TUNE_* of we.h.
+struct Tuning {
+  int gemm_cfg = -1;        // GemmCfgId, -1: pick by shape
+  int gemm_generic = 0;     // 1: the general GEMM kernel only
+  int gemm_splitk = -1;     // -1: split-K plan by shape, 0: off, n > 0: n slices
+  int gemm_reduce_xcd = 1;  // 1: the split-K reduce reads each tile on its XCD where that pays, 0: never
+  int attn_path = 0;        // 0: default kernel, 1: register-staged kernel, 2: DMA ring with the V^T pre-pass
+  int int4_path = 0;        // 0: by shape, 1: general kernel, 2: shared-x kernel, 3: LDS-ring decode kernel
+};
+Tuning tuning_from_env();
+
 struct GemmLaunch {
   const void* x;
   const void* w;
@@ -53,8 +65,9 @@ struct GemmLaunch {
   uint32_t x_stride, w_stride, y_stride, x_offset, w_offset, y_offset;
   uint32_t splits, kc;
   uint32_t flags;
-  int cfg;      // -1: pick by shape
-  int generic;  // 1: skip the fast path (tests of the general kernel)
+  int cfg;         // -1: pick by shape
+  int generic;     // 1: skip the fast path (tests of the general kernel)
+  int reduce_xcd;  // Tuning::gemm_reduce_xcd
   // split-K for small M: K in rsplits slices of rkc, partial sums in scratch (rsplits * m * n f32), then a
   // reduce pass that runs the epilogue
   uint32_t rsplits, rkc;
@@ -90,6 +103,7 @@ struct Int4Launch {
   float scale;
   uint32_t x_stride, y_stride, x_offset, y_offset;
   uint32_t flags;
+  int path;  // Tuning::int4_path
 };
 hipError_t int4_launch(const Int4Launch& L, hipStream_t stream);
 
@@ -109,6 +123,7 @@ struct AttnLaunch {
   uint32_t tokens, heads, kv_heads, dim;
   uint32_t q_stride, k_stride, v_stride, out_stride;  // elements between consecutive tokens
   int causal;
+  int path;       // Tuning::attn_path
   void* scratch;  // attention_scratch_bytes(L) bytes, or null (the register-staged kernel)
 };
 // Scratch the fast path needs (V^T of a head dim 128, 16-bit attention), 0 when it does not apply.
@@ -122,6 +137,10 @@ constexpr size_t kNoallocScratchBytes = 16u << 20;
 hipError_t noalloc_scratch_init(int device);
 // The address noalloc_scratch_init found on `device`, or null before it succeeded.
 void* noalloc_scratch(int device);
+// The array of `device` belongs to one context at a time: claim returns true when it was free (it is then
+// `owner`'s) or already `owner`'s; release frees it if `owner` holds it (context destruction).
+bool noalloc_claim(int device, const void* owner);
+void noalloc_release(int device, const void* owner);
 
 // Can gemm_fast_launch run this GEMM with the fused q/k epilogue (fast path, a head-aligned tile chosen, no
 // split-K plan)? qk_cols / q_cols must be set in L.

@@ -62,6 +62,7 @@ struct we_ctx {
   size_t alloc_cap = 0, held_bytes = 0;
   bool poison = false;
   std::map<void*, size_t> scratch_sizes;  // bytes of every scratch block (current, other lane's, retired)
+  we::Tuning tune;  // kernel-choice switches (we_set_tuning), from the environment at creation
 };
 
 namespace {
@@ -193,6 +194,30 @@ int ticket_valid(we_ctx* ctx, uint64_t t) {
 
 }  // namespace
 
+namespace we {
+// The switches as the WE_* environment variables give them (the values of sweeps and tests that pin a kernel):
+// WE_GEMM_CFG=<id>, WE_GEMM_PATH=generic, WE_GEMM_SPLITK=off|<slices>, WE_GEMM_REDUCE_XCD=off,
+// WE_ATTN_PATH=registers|ring, WE_INT4_PATH=generic|shared|pipe. Unset or unknown values keep the defaults.
+Tuning tuning_from_env() {
+  Tuning t;
+  auto env = [](const char* name) -> const char* {
+    const char* v = getenv(name);
+    return v && *v ? v : nullptr;
+  };
+  if (const char* v = env("WE_GEMM_CFG")) t.gemm_cfg = atoi(v);
+  if (const char* v = env("WE_GEMM_PATH")) t.gemm_generic = strcmp(v, "generic") == 0;
+  if (const char* v = env("WE_GEMM_SPLITK")) {
+    const long n = strtol(v, nullptr, 10);
+    t.gemm_splitk = strcmp(v, "off") == 0 ? 0 : n > 0 ? (int)n : -1;
+  }
+  if (const char* v = env("WE_GEMM_REDUCE_XCD")) t.gemm_reduce_xcd = strcmp(v, "off") != 0;
+  if (const char* v = env("WE_ATTN_PATH")) t.attn_path = strcmp(v, "registers") == 0 ? 1 : strcmp(v, "ring") == 0 ? 2 : 0;
+  if (const char* v = env("WE_INT4_PATH"))
+    t.int4_path = strcmp(v, "generic") == 0 ? 1 : strcmp(v, "shared") == 0 ? 2 : strcmp(v, "pipe") == 0 ? 3 : 0;
+  return t;
+}
+}  // namespace we
+
 extern "C" {
 
 int we_host_span(we_ctx* ctx, const void* p, size_t bytes);
@@ -205,6 +230,7 @@ int we_ctx_create(int device, we_ctx** out) {
   if (device < 0 || device >= count) return fail(nullptr, WE_EINVAL, "device %d out of range (%d visible)", device, count);
   we_ctx* ctx = new we_ctx();
   ctx->device = device;
+  ctx->tune = we::tuning_from_env();
   auto cleanup = [&](int code) {
     we_ctx_destroy(ctx);
     return fail(nullptr, code, "HIP set-up of device %d failed", device);
@@ -240,6 +266,7 @@ int we_ctx_destroy(we_ctx* ctx) {
   for (auto st : ctx->lanes)
     if (st) (void)hipStreamSynchronize(st);
   if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+  we::noalloc_release(ctx->device, ctx);  // its calls are done: another context may take the array
   for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->lane_scratch[1 - ctx->lane]) (void)hipFree(ctx->lane_scratch[1 - ctx->lane]);
@@ -259,6 +286,25 @@ int we_ctx_destroy(we_ctx* ctx) {
 }
 
 const char* we_last_error(const we_ctx* ctx) { return ctx ? ctx->err.c_str() : g_no_ctx_err.c_str(); }
+
+int we_set_tuning(we_ctx* ctx, int key, int value, int* previous) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  int* slot = nullptr;
+  int lo = 0, hi = 0;
+  switch (key) {
+    case WE_TUNE_GEMM_CFG: slot = &ctx->tune.gemm_cfg, lo = -1, hi = we::GEMM_CFG_256x192; break;
+    case WE_TUNE_GEMM_GENERIC: slot = &ctx->tune.gemm_generic, lo = 0, hi = 1; break;
+    case WE_TUNE_GEMM_SPLITK: slot = &ctx->tune.gemm_splitk, lo = -1, hi = 1 << 16; break;
+    case WE_TUNE_GEMM_REDUCE_XCD: slot = &ctx->tune.gemm_reduce_xcd, lo = 0, hi = 1; break;
+    case WE_TUNE_ATTN_PATH: slot = &ctx->tune.attn_path, lo = 0, hi = 2; break;
+    case WE_TUNE_INT4_PATH: slot = &ctx->tune.int4_path, lo = 0, hi = 3; break;
+    default: return fail(ctx, WE_EINVAL, "unknown tuning key %d", key);
+  }
+  if (value < lo || value > hi) return fail(ctx, WE_EINVAL, "tuning key %d takes %d .. %d, got %d", key, lo, hi, value);
+  if (previous) *previous = *slot;
+  *slot = value;
+  return WE_OK;
+}
 
 int we_device_info(we_ctx* ctx, char* name, size_t name_len, int* compute_units, int* lds_bytes) {
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
@@ -730,6 +776,13 @@ int we_matmul_noalloc(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const
   if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
   if (ctx->noalloc_status != hipSuccess)
     return hip_fail(ctx, ctx->noalloc_status, "allocation-free scratch of this device");
+  // one fixed array per GPU: a call that could overlap another call's use of it is refused, not raced
+  if (ctx->lane != 0)
+    return fail(ctx, WE_EINVAL, "we_matmul_noalloc runs on compute stream 0 only (select stream 0): the device's fixed "
+                                "scratch array would be shared with the other stream's calls");
+  if (!we::noalloc_claim(ctx->device, ctx))
+    return fail(ctx, WE_EINVAL, "the allocation-free scratch array of device %d belongs to another live context",
+                ctx->device);
   return matmul_impl(ctx, p, x_dtype, x, w_dtype, w, w_scales, group, y_dtype, y, bias, flags, nullptr, nullptr, true);
 }
 
@@ -836,11 +889,11 @@ int check_gemm(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void* 
   return WE_OK;
 }
 
-// The GemmLaunch of a checked matmul with 16-bit / fp8 / f32 weights: operands, shape, epilogue, and the
-// WE_GEMM_CFG / WE_GEMM_PATH overrides of sweeps and tests.
-void fill_gemm(we::GemmLaunch& L, const we_matmul_params* p, int x_dtype, const void* x, int w_dtype, const void* w,
-               int y_dtype, void* y, const float* bias, uint32_t flags, const float* gate, const void* res, int mul,
-               uint32_t splits, uint32_t kc) {
+// The GemmLaunch of a checked matmul with 16-bit / fp8 / f32 weights: operands, shape, epilogue, and the context's
+// kernel-choice switches (tile configuration, general kernel, reduce mapping) of sweeps and tests.
+void fill_gemm(we::GemmLaunch& L, const we::Tuning& t, const we_matmul_params* p, int x_dtype, const void* x,
+               int w_dtype, const void* w, int y_dtype, void* y, const float* bias, uint32_t flags, const float* gate,
+               const void* res, int mul, uint32_t splits, uint32_t kc) {
   const bool conv = p->width || p->cin;
   L = we::GemmLaunch{};
   L.x = x;
@@ -868,11 +921,9 @@ void fill_gemm(we::GemmLaunch& L, const we_matmul_params* p, int x_dtype, const 
   L.splits = splits;
   L.kc = kc;
   L.flags = flags;
-  L.cfg = -1;
-  const char* force = getenv("WE_GEMM_CFG");
-  if (force && *force) L.cfg = atoi(force);
-  const char* path = getenv("WE_GEMM_PATH");
-  L.generic = (path && strcmp(path, "generic") == 0) ? 1 : 0;
+  L.cfg = t.gemm_cfg;
+  L.generic = t.gemm_generic;
+  L.reduce_xcd = t.gemm_reduce_xcd;
   L.rsplits = 1;
   L.rkc = L.k;
   L.scratch = nullptr;
@@ -922,6 +973,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     L.x_offset = p->x_offset;
     L.y_offset = p->y_offset;
     L.flags = flags;
+    L.path = ctx->tune.int4_path;
     hipError_t e = we::int4_launch(L, ctx->compute);
     if (e != hipSuccess) return hip_fail(ctx, e, "int4 launch");
     return WE_OK;
@@ -932,7 +984,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   rc = check_span(ctx, w, w_need, "w");
   if (rc) return rc;
   we::GemmLaunch L;
-  fill_gemm(L, p, x_dtype, x, w_dtype, w, y_dtype, y, bias, flags, gate, res, mul, splits, kc);
+  fill_gemm(L, ctx->tune, p, x_dtype, x, w_dtype, w, y_dtype, y, bias, flags, gate, res, mul, splits, kc);
   bool qk_fused = false;
   if (qk && qk->q_heads + qk->k_heads) {
     L.qk_cols = (qk->q_heads + qk->k_heads) * 128;
@@ -947,9 +999,8 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     qk_fused = we::gemm_qk_fusable(L);
     if (!qk_fused) L.qk_cols = L.q_cols = 0;  // the plain GEMM, then the q/k pass below
   }
-  const char* split_env = getenv("WE_GEMM_SPLITK");  // "off", or a slice count for sweeps
-  if (!(split_env && strcmp(split_env, "off") == 0)) {
-    const uint32_t force = split_env ? (uint32_t)strtoul(split_env, nullptr, 10) : 0u;
+  if (ctx->tune.gemm_splitk != 0) {  // 0: split-K off; n > 0: n slices (sweeps)
+    const uint32_t force = ctx->tune.gemm_splitk > 0 ? (uint32_t)ctx->tune.gemm_splitk : 0u;
     const we::GemmReducePlan rp = we::gemm_reduce_plan(L, force);
     if (rp.rsplits > 1) {
       if (noalloc) {
@@ -1015,10 +1066,38 @@ int we_matmul_group(we_ctx* ctx, uint32_t count, const we_matmul_item* items, in
     const uint64_t w_need = p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0;
     rc = check_span(ctx, it.w, w_need, "w");
     if (rc) return rc;
-    fill_gemm(L[i], p, x_dtype, it.x, w_dtype, it.w, y_dtype, it.y, it.bias, flags, it.gate, it.residual, 0, splits,
+    fill_gemm(L[i], ctx->tune, p, x_dtype, it.x, w_dtype, it.w, y_dtype, it.y, it.bias, flags, it.gate, it.residual, 0,
+              splits,
               kc);
   }
-  if (count == 2 && !empty[0] && !empty[1] && w_dtype != WE_INT4 && we::gemm_pair_ok(L[0], L[1])) {
+  // The paired launch runs the tiles of both GEMMs at once, so it is taken only for independent items: neither item's
+  // output bytes may overlap the other's output or any operand it reads (x, w, bias, gate, residual). A dependent
+  // pair runs as two calls in order, item 0 first.
+  auto independent = [&]() {
+    struct Span {
+      uintptr_t lo, hi;
+    };
+    auto span = [](const void* p, uint64_t bytes) { return Span{(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; };
+    auto hit = [](Span a, Span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; };
+    const uint64_t xb = elem_bytes(x_dtype), wb = elem_bytes(w_dtype), yb = elem_bytes(y_dtype);
+    Span out[2], in[2][5];
+    for (int i = 0; i < 2; i++) {
+      const we_matmul_params* p = items[i].p;
+      const uint64_t y_need = ((uint64_t)p->y_offset + (uint64_t)(p->m - 1) * p->y_stride + p->n) * yb;
+      out[i] = span(items[i].y, y_need);
+      in[i][0] = span(items[i].x, p->k ? ((uint64_t)p->x_offset + (uint64_t)(p->m - 1) * p->x_stride + p->k) * xb : 0);
+      in[i][1] = span(items[i].w, p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0);
+      in[i][2] = span(items[i].bias, (flags & WE_EPI_BIAS) ? (uint64_t)p->n * 4 : 0);
+      in[i][3] = span(items[i].gate, items[i].gate ? (uint64_t)p->n * 4 : 0);
+      in[i][4] = span(items[i].residual, items[i].residual ? y_need : 0);
+    }
+    if (hit(out[0], out[1])) return false;
+    for (int i = 0; i < 2; i++)
+      for (const Span& r : in[1 - i])
+        if (hit(out[i], r)) return false;
+    return true;
+  };
+  if (count == 2 && !empty[0] && !empty[1] && w_dtype != WE_INT4 && we::gemm_pair_ok(L[0], L[1]) && independent()) {
     HIP_OK(ctx, hipSetDevice(ctx->device), "hipSetDevice");
     const hipError_t e = we::gemm_fast_launch_pair(L[0], L[1], ctx->compute);
     return e == hipSuccess ? WE_OK : hip_fail(ctx, e, "gemm pair launch");
@@ -1170,7 +1249,7 @@ int we_attention(we_ctx* ctx, uint32_t tokens, uint32_t heads, uint32_t kv_heads
     if (rc) return rc;
   }
   we::AttnLaunch L{q, k, v, out, dtype, tokens, heads, kv_heads, dim, (uint32_t)qs, (uint32_t)ks, (uint32_t)vs,
-                   (uint32_t)os, causal ? 1 : 0, nullptr};
+                   (uint32_t)os, causal ? 1 : 0, ctx->tune.attn_path, nullptr};
   const size_t need = we::attention_scratch_bytes(L);
   if (need) {
     const int rc = ensure_scratch(ctx, need);

@@ -34,6 +34,7 @@ export const EPI: { ACCUMULATE: 1; SPLIT_K: 2; BIAS: 4; GELU_TANH: 8 };
 export const OP: { SWIGLU: 0; SIGMOID_GATE: 1; GATED_ADD: 2; ADD_BIAS: 3; GELU_TANH: 4; ADD: 5; SILU: 6 };
 /** Product epilogues of Graph.matmul: y = silu(aux) * v, or aux * sigmoid(v). */
 export const MUL: { SWIGLU: 1; SIGMOID_GATE: 2 };
+export const TUNE: { gemmCfg: 0; gemmGeneric: 1; gemmSplitK: 2; gemmReduceXcd: 3; attnPath: 4; int4Path: 5 };
 
 /** The subset of GPUQueue the reference's callers use. */
 export interface Queue {
@@ -99,6 +100,8 @@ export class Graph {
   setAllocCap(bytes: number): number;
   /** Debugging: freed and released buffers are filled with NaN bytes once pooled. */
   setPoison(on: boolean): void;
+  /** Pins a kernel choice (a TUNE key or its name); returns the previous value. */
+  setTuning(key: keyof typeof TUNE | number, value: number): number;
   /** Every read() and onSubmittedWorkDone() promise must have settled first. */
   destroy(): void;
   sync(): void;

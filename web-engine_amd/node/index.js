@@ -12,6 +12,8 @@ const ELEM_BYTES = { [F32]: 4, [F16]: 2, [BF16]: 2, [FP8]: 1 };
 const EPI = { ACCUMULATE: 1, SPLIT_K: 2, BIAS: 4, GELU_TANH: 8 };
 const OP = { SWIGLU: 0, SIGMOID_GATE: 1, GATED_ADD: 2, ADD_BIAS: 3, GELU_TANH: 4, ADD: 5, SILU: 6 };
 const MUL = { SWIGLU: 1, SIGMOID_GATE: 2 };
+// kernel-choice switches (we_set_tuning, WE_TUNE_* of include/we.h)
+const TUNE = { gemmCfg: 0, gemmGeneric: 1, gemmSplitK: 2, gemmReduceXcd: 3, attnPath: 4, int4Path: 5 };
 
 // A binding is a buffer { ptr, size }, a Graph.slice of one, the reference's { buffer, offset, size } form, or a
 // BigInt address.
@@ -248,6 +250,14 @@ class Graph {
   /** Debugging: freed and released buffers are filled with NaN bytes once pooled. */
   setPoison(on) {
     addon.setPoison(this.ctx, on ? 1 : 0);
+  }
+
+  /** Pins a kernel choice (a TUNE key: gemmCfg, gemmGeneric, gemmSplitK, gemmReduceXcd, attnPath, int4Path);
+   *  returns the previous value. */
+  setTuning(key, value) {
+    const k = typeof key === "string" ? TUNE[key] : key;
+    if (k === undefined) throw new Error(`unknown tuning key ${key}`);
+    return addon.setTuning(this.ctx, k, value);
   }
 
   /** src/gpu/graph.ts:32: buffers created vs taken from the pool, and bytes created. */
@@ -573,7 +583,7 @@ function readTensor(st, tensor, limit, dst, threads, offset = 0) {
 }
 
 module.exports = {
-  addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP, MUL,
+  addon, Graph, F32, F16, BF16, FP8, INT4, DTYPES, EPI, OP, MUL, TUNE,
   matmulParams, conv3x3Params, kSplitFor, linear, norm, noMod, rotate, attention,
   swiglu, sigmoidGate, gatedAdd, addBias, add, gelu, silu,
   SafetensorsError, readHeader, readTensor, registerKernels,

@@ -360,6 +360,20 @@ static napi_value SetPoison(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_set_poison(ctx, on));
 }
 
+/* setTuning(ctx, key, value) -> previous value (WE_TUNE_* keys) */
+static napi_value SetTuning(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 3)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  int32_t key = i32_arg(&a, 1);
+  int32_t value = i32_arg(&a, 2);
+  if (a.bad) return NULL;
+  int prev = 0;
+  int rc = we_set_tuning(ctx, key, value, &prev);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)prev);
+}
+
 static napi_value HostAlloc(napi_env env, napi_callback_info info) {
   args_t a;
   if (!get_args(env, info, &a, 2)) return NULL;
@@ -1198,7 +1212,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
-      {"setAllocCap", SetAllocCap}, {"setPoison", SetPoison},
+      {"setAllocCap", SetAllocCap}, {"setPoison", SetPoison}, {"setTuning", SetTuning},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},

@@ -15,6 +15,7 @@ Every op runs the hand-written gfx950 kernels in libwe.so; there is no CPU fallb
 without a GPU (the symbol checks use that); creating a Graph needs the library and a GPU and raises
 otherwise.
 """
+import contextlib
 import ctypes
 import os
 import pathlib
@@ -30,6 +31,8 @@ F32, F16, BF16, FP8, INT4 = 0, 1, 2, 3, 4
 DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
 ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
+# kernel-choice switches (we_set_tuning, WE_TUNE_* of include/we.h)
+TUNE_KEYS = {"gemm_cfg": 0, "gemm_generic": 1, "gemm_splitk": 2, "gemm_reduce_xcd": 3, "attn_path": 4, "int4_path": 5}
 MUL_SWIGLU, MUL_SIGMOID_GATE = 1, 2
 OP_SWIGLU, OP_SIGMOID_GATE, OP_GATED_ADD, OP_ADD_BIAS, OP_GELU_TANH, OP_ADD, OP_SILU = range(7)
 PEAK_F32, PEAK_F16, PEAK_I8, PEAK_MFMA_BF16, PEAK_MFMA_BF16_DATA = range(5)
@@ -93,6 +96,7 @@ SIGNATURES = {
     "we_record_all": (_I, [_P, _P]),
     "we_set_alloc_cap": (_I, [_P, _U64, _P]),
     "we_set_poison": (_I, [_P, ctypes.c_int]),
+    "we_set_tuning": (_I, [_P, ctypes.c_int, ctypes.c_int, _P]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
     "we_wait_ticket": (_I, [_P, _U64]),
     "we_record_compute": (_I, [_P, _P]),
@@ -301,6 +305,27 @@ class Graph:
     def set_poison(self, on):
         """Debugging: freed / released buffers are filled with 0xff bytes (NaN) once pooled."""
         self.check(self.lib.we_set_poison(self.ctx, 1 if on else 0))
+
+    def set_tuning(self, key, value):
+        """Sets one kernel-choice switch of this context (a TUNE_* key or its name, e.g. "gemm_cfg") and returns
+        the previous value. The context starts from the WE_* environment variables as they were when it was made."""
+        k = TUNE_KEYS[key] if isinstance(key, str) else int(key)
+        prev = ctypes.c_int()
+        self.check(self.lib.we_set_tuning(self.ctx, k, int(value), ctypes.byref(prev)))
+        return prev.value
+
+    @contextlib.contextmanager
+    def tuned(self, **switches):
+        """Pins kernel choices for the calls queued inside the block, e.g. graph.tuned(gemm_cfg=0, gemm_splitk=0);
+        the previous values come back on exit."""
+        old = []
+        try:
+            for name, value in switches.items():
+                old.append((name, self.set_tuning(name, value)))
+            yield self
+        finally:
+            for name, value in reversed(old):
+                self.set_tuning(name, value)
 
     def host_alloc(self, nbytes):
         p = ctypes.c_void_p()
