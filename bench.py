@@ -104,11 +104,16 @@ def bench_mlp(g, steps, warmup, rng):
         up()
         down()
 
+    # The GEMMs alone first: measured on MI355X, the first ~10 launches after an idle GPU run below steady clocks,
+    # which a step timed first absorbed (556 us per step against 507 us for up + down timed after it). Then the
+    # step: `warmup` untimed steps and `steps` timed ones.
+    for _ in range(3):
+        step()
+    ms_up = time_launches(g, up, steps)
+    ms_dn = time_launches(g, down, steps)
     for _ in range(warmup):
         step()
     ms_step = time_launches(g, step, steps)
-    ms_up = time_launches(g, up, steps)
-    ms_dn = time_launches(g, down, steps)
     flop = 2.0 * m * f * h
     res = {
         "ms_per_step": ms_step,

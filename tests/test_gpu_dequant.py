@@ -57,9 +57,11 @@ ONE_HOT_K, ONE_HOT_N = 512, 256
 
 def _one_hot_gemm(graph, tune, x_dt, cfg, w, splitk=None):
     k, n = ONE_HOT_K, ONE_HOT_N
-    one = 0x3F80 if x_dt == we.BF16 else 0x3C00  # 1.0 as bf16 / f16
-    x = np.zeros((k, k), np.uint16)
-    x[np.arange(k), np.arange(k)] = one
+    if x_dt == we.F32:  # f32 x runs as three bf16 planes (1.0, 0, 0) over 3K with the weights repeating every K
+        x = np.eye(k, dtype=np.float32)
+    else:
+        x = np.zeros((k, k), np.uint16)
+        x[np.arange(k), np.arange(k)] = 0x3F80 if x_dt == we.BF16 else 0x3C00  # 1.0 as bf16 / f16
     tune(gemm_cfg=cfg)
     if splitk is not None:
         tune(gemm_splitk=splitk)
@@ -81,14 +83,15 @@ def _codes(with_nan):
 
 
 @pytest.mark.parametrize("with_nan", [False, True])
-@pytest.mark.parametrize("x_dt", [we.BF16, we.F16])
+@pytest.mark.parametrize("x_dt", [we.BF16, we.F16, we.F32])
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5])
 def test_gemm_fp8_decode_every_byte_exactly(graph, tune, cfg, x_dt, with_nan):
     """Every byte through the fast GEMM's in-register decode, in every tile configuration (0 256x256 and 5 256x192
     ping-pong, 1 256x128, 2 128x128, 3 64x64, 4 32x64), bit for bit against the shader formula
     (src/kernels/fp8.ts:12-20). Without 0x7f / 0xff the hardware converter decodes all 254 finite codes, the
     subnormals 0x01-0x07 and 0x81-0x87 included; with them, the waves that meet a NaN recompute with the shader's
-    decoding, which must give +-480 and every other code unchanged."""
+    decoding, which must give +-480 and every other code unchanged. f32 x takes the plane path (the weights read
+    at k mod K, in the main loop and in the recompute)."""
     w = _codes(with_nan)
     got = _one_hot_gemm(graph, tune, x_dt, cfg, w)
     want = O.e4m3_gpu_table()[w.T]  # [K, N]: y[r, c] = decode(W[c, r])

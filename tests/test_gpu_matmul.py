@@ -687,3 +687,40 @@ def test_conv3x3_refusals(graph):
     p = we.conv3x3_params(4, 4, 8, 8, graph=graph)
     with pytest.raises(we.WeError, match="int4 weights have no 3x3 convolution input"):
         graph.matmul(p, we.F16, b, we.INT4, b, we.F32, b, scales=b, group=64)
+
+
+F32_FAST_CASES = [
+    # (m, n, k, weights, flags): ragged tiles, the small-M split-K plan over the planes, the reference's Krea layer
+    # shape, bf16 weights, and the fused epilogues
+    (300, 520, 192, we.FP8, 0), (64, 3072, 3072, we.FP8, 0), (8, 1536, 6144, we.FP8, 0), (130, 200, 320, we.BF16, 0),
+    (512, 768, 512, we.FP8, we.EPI_BIAS | we.EPI_GELU), (256, 512, 1024, we.BF16, we.EPI_ACCUMULATE),
+]
+
+
+@pytest.mark.parametrize("m,n,k,w_dt,flags", F32_FAST_CASES)
+def test_f32_activations_on_the_fast_path(graph, tune, m, n, k, w_dt, flags):
+    """f32 x, the reference's own activation dtype (src/kernels/matmul.ts:129-131), with fp8 or bf16 weights and K a
+    multiple of 64: split into three exact bf16 planes and run by the fast kernel over 3K. It matches the float64
+    oracle at the reference's 1e-5 bar, and the general kernel (which splits x into the same planes tile by tile)
+    to 4e-6: every product is exact in both, only the f32 summation order differs (at K = 3072, sums of ~200 move by
+    ~1.5e-6 of max|y| between two orders)."""
+    rng = np.random.default_rng(m + n + k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    scale = 0.02 if w_dt == we.FP8 else 1.0
+    bias = rng.normal(0, 1, n).astype(np.float32) if flags & we.EPI_BIAS else None
+    y0 = rng.standard_normal(m * n).astype(np.float32) if flags & we.EPI_ACCUMULATE else None
+    p = we.matmul_params(m, n, k, scale, graph=graph)
+    got = run(graph, p, x, we.F32, w_store, w_dt, we.F32, flags=flags, bias=bias, y_init=y0)
+    want = O.matmul(O.matmul_params(m, n, k, scale), O.F32, x, ow, w_oracle)
+    if bias is not None:
+        want = want + np.tile(bias.astype(np.float64), m)
+    if flags & we.EPI_GELU:
+        want = O.gelu_tanh(want)
+    if y0 is not None:
+        want = want + y0.astype(np.float64)
+    tol = 1e-4 if flags & we.EPI_GELU else TOL_F32_OUT
+    assert O.rel_error(got, want) < tol
+    tune(gemm_generic=1)
+    general = run(graph, p, x, we.F32, w_store, w_dt, we.F32, flags=flags, bias=bias, y_init=y0)
+    assert O.rel_error(got, general) < 4e-6

@@ -468,7 +468,7 @@ int pick_gemm_cfg(uint32_t m, uint32_t n, uint32_t splits) {
 hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream) {
   if (!L.generic && !L.conv_width) {
     const hipError_t e = gemm_fast_launch(L, stream);
-    if (e != hipErrorNotSupported) return e;
+    if (e != hipErrorNotSupported || L.k_wrap) return e;  // planes of x (k_wrap) exist for the fast path only
   }
   GemmArgs a{};
   a.x = L.x;

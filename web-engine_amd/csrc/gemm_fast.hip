@@ -24,6 +24,9 @@
 //    that wave through an exact recompute that decodes every byte with the shader's formula.
 // Requirements (checked on the host): x / W rows 16-byte aligned, K and the split-K slice multiples of
 // 16, operand extents below 2^31 bytes.
+// f32 activations arrive as three exact bf16 planes along K (x [M, 3K], split by a pass before the GEMM); the kernel
+// walks k over all 3K while the weights are read at k mod K (K a multiple of 64, so no 64-k block spans two
+// planes): one GEMM of exact products, so every epilogue applies to the f32-exact sum.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -36,9 +39,7 @@ namespace we {
 namespace {
 
 constexpr int BK = 64;
-#ifndef WE_GEMM_LIC
-#define WE_GEMM_LIC 0
-#endif
+
 constexpr uint32_t kInvalid = 0x80000000u;  // a byte offset past every extent: the load returns 0
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 family)
 
@@ -53,6 +54,9 @@ struct FastArgs {
   const void* res;
   uint32_t x_bytes, w_bytes;  // readable bytes from x / w (their extents)
   uint32_t m, n, k;
+  // weights read at k - kwrap (k >= kwrap) and k - kwrap2 (k >= kwrap2): x holds k / kwrap planes of kwrap values per
+  // row (GemmLaunch::k_wrap); 0xffffffff: no wrap
+  uint32_t kwrap, kwrap2;
   float scale;
   uint32_t x_stride, w_stride, y_stride, y_offset;  // x / w already point at their offsets
   uint32_t kc;
@@ -183,10 +187,14 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   static_assert(A_INS % NW == 0 && (BN * B_ROW) % 1024 == 0, "stage loads must split evenly over the waves");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && WTM >= 32, "wave tile");
   static_assert(!PP || NW * 32 * (WTN * 2 + 16) <= S * STAGE, "the epilogue's row staging fits the stages");
-  // Ping-pong tiles: the ring's loads are issued by the waves of group 1 alone, between the MFMAs of their compute
-  // phase (LIC), so the memory phases of both groups hold only fragment reads. Other tiles: every wave loads.
-  constexpr bool LIC = PP && WE_GEMM_LIC;
-  constexpr int NL = LIC ? NW / 2 : NW;                                   // waves that issue loads
+  // Load schedule of the ping-pong tiles (LM, details at the loop). 16-bit weights (two ring stages): 1, the waves of
+  // group 1 issue every load, between the MFMAs of their compute phase, one block further ahead than a memory-phase
+  // load could be (4096 x 9216 x 3072 bf16, 256 x 192 tiles: 211 -> 199-205 us, same box). fp8 weights (three
+  // stages): 0, every wave issues its share in its memory phase; loads in the compute phases held the MFMAs back (1:
+  // 243 -> 279 us, 2, each group its own share in its compute phase: 247 -> 291 us, up-projection, same box).
+  // Other tiles: every wave loads its share in the memory phase.
+  constexpr int LM = PP ? (B8 ? 0 : 1) : 0;
+  constexpr int NL = LM == 1 ? NW / 2 : NW;                               // waves that issue loads
   static_assert(A_INS % NL == 0 && B_INS % NL == 0, "stage loads split evenly over the loading waves");
   constexpr int A_PW = A_INS / NL, B_PW = B_INS / NL, L = A_PW + B_PW;  // loads per loading wave per stage
   constexpr int B_RPI = 1024 / B_ROW;                                     // weight rows per load
@@ -195,7 +203,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int lw = wave % NL;  // this wave's share of the loads (LIC: group 1's waves 0 .. NW / 2 - 1)
+  const int lw = wave % NL;  // this wave's share of the loads (LM 1: group 1's waves 0 .. NW / 2 - 1)
   const int h = lane >> 5, l32 = lane & 31;
 
   uint32_t pid = xcd_remap_f(blockIdx.x, gridDim.x);
@@ -271,8 +279,9 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     } else {
       constexpr int j = q - A_PW;
       const uint32_t o = (full || kb + kb8 < k_end) ? offb[j] : kInvalid;
+      const uint32_t kbw = kb >= a.kwrap2 ? kb - a.kwrap2 : kb >= a.kwrap ? kb - a.kwrap : kb;  // weights' k
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(base + A_BYTES + (lw + j * NL) * 1024), 16, o,
-                                               (int)(kb * WB), 0, 0);
+                                               (int)(kbw * WB), 0, 0);
     }
   };
   // issue this wave's share of the loads of the 64-k block starting at kb into stage st
@@ -365,7 +374,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     auto compute_block = [&](bool ld, uint32_t kb, int st) {
       static_for<0, 4>([&](auto Q) {
         constexpr int q = decltype(Q)::value;
-        if (LIC && ld) {  // wave-uniform
+        if (LM && ld) {  // wave-uniform
           constexpr int PER = (L + 3) / 4, Q0 = q * PER, Q1 = Q0 + PER < L ? Q0 + PER : L;
           static_for<Q0, Q1>([&](auto QQ) { issue_one(QQ, kb, st); });
         }
@@ -394,7 +403,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       if (S >= 3 && t + 2 < nk) wait_vmcnt<(S >= 3 ? (S - 2) * L : 0)>();
       else wait_vmcnt<0>();
     };
-    if (nk > 0 && LIC) {
+    if (nk > 0 && LM == 1) {
       // Group 1 issues every load of the ring. Prologue: blocks 0 .. S - 1 into stages 0 .. S - 1. In its compute
       // phase of block t (interval 2t + 2) a group-1 wave loads block t + S into block t's stage, which both groups
       // have read by then (group 0 in interval 2t, group 1 in 2t + 1). A group-1 wave's loads of block t + 1 must
@@ -516,6 +525,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
         for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
       for (uint32_t k0 = k_begin; k0 < k_end; k0 += 16) {
         const uint32_t kk = k0 + 8 * h;  // 8 k per lane half; k_end - k0 >= 16 (multiples of 16)
+        const uint32_t kkw = kk >= a.kwrap2 ? kk - a.kwrap2 : kk >= a.kwrap ? kk - a.kwrap : kk;  // weights' k
         u32x4 xr[TM];
         u32x4 wv[TN];
 #pragma unroll
@@ -527,7 +537,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
 #pragma unroll
         for (int j = 0; j < TN; j++) {
           const uint32_t col = col0 + wn * WTN + j * 32 + l32;
-          const uint32_t o = col < a.n ? col * a.w_stride + kk : kInvalid;
+          const uint32_t o = col < a.n ? col * a.w_stride + kkw : kInvalid;
           const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
           const u32x2 lo = fp8x4_to_16<IS_F16>(raw.x), hi = fp8x4_to_16<IS_F16>(raw.y);
           wv[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
@@ -953,8 +963,9 @@ bool fast_supported(const GemmLaunch& L, uint32_t kc) {
   if (((uintptr_t)L.x + (uint64_t)L.x_offset * 2) % 16 || ((uintptr_t)L.w + (uint64_t)L.w_offset * wb) % 16 ||
       (L.x_stride * 2) % 16 || (L.w_stride * wb) % 16)
     return false;
+  if (L.k_wrap && (L.k_wrap % BK || L.k % L.k_wrap || L.k / L.k_wrap > 3)) return false;
   const uint64_t xb = L.k ? ((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2 : 0;
-  const uint64_t wbytes = L.k ? ((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb : 0;
+  const uint64_t wbytes = L.k ? ((uint64_t)(L.n - 1) * L.w_stride + (L.k_wrap ? L.k_wrap : L.k)) * wb : 0;
   return xb < kInvalid && wbytes < kInvalid;
 }
 
@@ -963,7 +974,7 @@ constexpr uint32_t kCUs = 256;
 // readable weight bytes of a GEMM (FastArgs::w_bytes)
 uint64_t weight_extent(const GemmLaunch& L) {
   const int wb = L.w_dtype == FP8 ? 1 : 2;
-  return L.k ? ((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb : 0;
+  return L.k ? ((uint64_t)(L.n - 1) * L.w_stride + (L.k_wrap ? L.k_wrap : L.k)) * wb : 0;
 }
 
 // Tile shape by predicted speed: score = base x (tiles / slots) / (time in rounds). base is the tile shape's own
@@ -1091,10 +1102,12 @@ FastArgs fast_args(const GemmLaunch& L, uint32_t kc) {
   a.qk_cos = L.qk_cos;
   a.qk_sin = L.qk_sin;
   a.x_bytes = L.k ? (uint32_t)(((uint64_t)(L.m - 1) * L.x_stride + L.k) * 2) : 0;
-  a.w_bytes = L.k ? (uint32_t)(((uint64_t)(L.n - 1) * L.w_stride + L.k) * wb) : 0;
+  a.w_bytes = (uint32_t)weight_extent(L);
   a.m = L.m;
   a.n = L.n;
   a.k = L.k;
+  a.kwrap = L.k_wrap ? L.k_wrap : 0xffffffffu;
+  a.kwrap2 = L.k_wrap ? 2 * L.k_wrap : 0xffffffffu;
   a.scale = L.scale;
   a.x_stride = L.x_stride;
   a.w_stride = L.w_stride;
@@ -1139,9 +1152,13 @@ hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream) {
   return launch_fast_types<false, BF16>(a, splits, cfg, rx, stream);
 }
 
+bool gemm_fast_supported(const GemmLaunch& L) {
+  return L.splits <= 1 && !(L.flags & WE_EPI_SPLIT_K_BIT) && fast_supported(L, L.k);
+}
+
 bool gemm_pair_ok(const GemmLaunch& A, const GemmLaunch& B) {
   for (const GemmLaunch* L : {&A, &B})
-    if (L->generic || L->conv_width || L->splits > 1 || L->qk_cols || (L->flags & WE_EPI_SPLIT_K_BIT) ||
+    if (L->generic || L->conv_width || L->splits > 1 || L->qk_cols || L->k_wrap || (L->flags & WE_EPI_SPLIT_K_BIT) ||
         !fast_supported(*L, L->k))
       return false;
   return A.n == B.n && A.k == B.k && A.x_dtype == B.x_dtype && A.w_dtype == B.w_dtype && A.y_dtype == B.y_dtype &&

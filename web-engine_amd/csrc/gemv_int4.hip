@@ -460,12 +460,11 @@ __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
 // and set the time (M = 8: 14.0 us, against 10.4 us for the 256 workgroups of N = 16384). For M <= 8, 32
 // columns and 8 x rows make 592 smaller workgroups (28 KB of LDS, 8 waves), two or three on every CU: 12.5 us.
 constexpr int SK_WB = 16 * PIPE_CB * 32;  // one column tile's weights per chunk: 2 KB
-constexpr int SK_WPT = 4;                 // waves per column tile
 constexpr int SK_NBUF = 3;                // ring slots (4 measured no faster for either shape)
 
-template <int XT, int TILES, int XR>
-__global__ void __launch_bounds__(64 * TILES * SK_WPT) int4_gemv_shared_kernel(Int4Args a) {
-  constexpr int WPT = SK_WPT;
+// WPT: waves per column tile (each takes PIPE_CB / WPT blocks of every chunk)
+template <int XT, int TILES, int XR, int WPT>
+__global__ void __launch_bounds__(64 * TILES * WPT) int4_gemv_shared_kernel(Int4Args a) {
   constexpr bool IS_F16 = XT == F16;
   constexpr int NW = TILES * WPT, NT = 64 * NW;  // waves, threads
   constexpr int XB = XR * 512;                    // x rows of one chunk
@@ -781,12 +780,14 @@ hipError_t int4_launch(const Int4Launch& L, hipStream_t stream) {
     // M <= 8: 32 columns and 8 staged x rows per workgroup; larger M: 64 columns, 16 rows (32 columns there
     // double the x traffic and leave a third of each chunk's loads spare: slower)
     const bool x8 = L.m <= 8;
-    const int tiles = x8 ? 2 : 4;
-    const dim3 gs((L.n + 16 * tiles - 1) / (16 * tiles)), bs(64 * tiles * SK_WPT);
     const bool f16 = L.x_dtype == F16;
     void (*kern)(Int4Args);
-    if (x8) kern = f16 ? int4_gemv_shared_kernel<F16, 2, 8> : int4_gemv_shared_kernel<BF16, 2, 8>;
-    else kern = f16 ? int4_gemv_shared_kernel<F16, 4, 16> : int4_gemv_shared_kernel<BF16, 4, 16>;
+    // (measured: 80-column workgroups of 5 tiles x 2 waves, one round of 237 on 256 CUs, gave M = 16 no faster and
+    // M = 8 14.7 against 13.0 us: fewer waves in flight per CU cost more than the second round saves)
+    const int tiles = x8 ? 2 : 4, wpt = 4;
+    if (x8) kern = f16 ? int4_gemv_shared_kernel<F16, 2, 8, 4> : int4_gemv_shared_kernel<BF16, 2, 8, 4>;
+    else kern = f16 ? int4_gemv_shared_kernel<F16, 4, 16, 4> : int4_gemv_shared_kernel<BF16, 4, 16, 4>;
+    const dim3 gs((L.n + 16 * tiles - 1) / (16 * tiles)), bs(64 * tiles * wpt);
     hipLaunchKernelGGL(kern, gs, bs, 0, stream, a);
     return hipGetLastError();
   }

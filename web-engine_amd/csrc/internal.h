@@ -68,6 +68,9 @@ struct GemmLaunch {
   int cfg;         // -1: pick by shape
   int generic;     // 1: skip the fast path (tests of the general kernel)
   int reduce_xcd;  // Tuning::gemm_reduce_xcd
+  // 0, or the weights' K when x holds k / k_wrap planes of k_wrap values per row (f32 activations split into bf16
+  // planes): k runs over all planes and the weights are read at k mod k_wrap. Fast path only (k_wrap % 64 == 0).
+  uint32_t k_wrap;
   // split-K for small M: K in rsplits slices of rkc, partial sums in scratch (rsplits * m * n f32), then a
   // reduce pass that runs the epilogue
   uint32_t rsplits, rkc;
@@ -88,6 +91,8 @@ struct GemmReducePlan {
 GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits = 0);  // force_splits: sweeps
 // The straight-line fast path; hipErrorNotSupported when the operands do not qualify.
 hipError_t gemm_fast_launch(const GemmLaunch& L, hipStream_t stream);
+// Would gemm_fast_launch take this launch (types, alignment, extents)? (Not for split-K partial modes.)
+bool gemm_fast_supported(const GemmLaunch& L);
 int pick_gemm_cfg(uint32_t m, uint32_t n, uint32_t splits);
 
 struct Int4Launch {
@@ -149,6 +154,10 @@ bool gemm_qk_fusable(const GemmLaunch& L);
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_fill(void* p, size_t bytes, uint8_t byte, hipStream_t s);
 hipError_t launch_unpack_fp8(const void* packed, size_t n, const float* scale, float* out, hipStream_t s);
+// f32 rows [m, k] (x_stride floats apart, 16-byte aligned, k % 8 == 0) -> bf16 [m, 3k]: planes hi | mid | lo along k,
+// whose sum is each value exactly
+hipError_t launch_split_f32_planes(const float* x, uint32_t m, uint32_t k, uint32_t x_stride, uint16_t* out,
+                                   hipStream_t s);
 hipError_t launch_dequant_int4(const uint32_t* w, const uint16_t* sc, uint32_t rows, uint32_t k, uint32_t group,
                                float* out, hipStream_t s);
 hipError_t launch_elementwise(int op, size_t n, size_t d, int dtype, const void* a, const void* b, const void* c,

@@ -32,6 +32,44 @@ hipError_t launch_fill(void* p, size_t bytes, uint8_t byte, hipStream_t s) {
 
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) { return launch_fill(p, bytes, 0, s); }
 
+// ------------------------------------------------------------------ f32 activations as three bf16 planes
+// out[r, p K + k] = plane p of x[r, k]: hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid). Each remainder is
+// exact in f32 (at most 16, then 8 significant bits), so hi + mid + lo == x for every normal f32 value and a GEMM
+// over the 3K planes against weights that repeat every K sums exact products of all 24 bits of x. One thread per 8
+// consecutive values of a row (two 16-byte loads, three 16-byte stores); x rows 16-byte aligned, K % 8 == 0.
+__global__ void __launch_bounds__(256) split_f32_planes_kernel(const float* __restrict__ x, uint32_t m, uint32_t k,
+                                                              uint32_t xs, uint16_t* __restrict__ out) {
+  const uint32_t groups = k / 8;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)m * groups) return;
+  const uint32_t r = (uint32_t)(idx / groups), g = (uint32_t)(idx % groups);
+  const float* src = x + (size_t)r * xs + (size_t)g * 8;
+  const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
+  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  uint32_t h[3][8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    h[0][i] = f32_to_bf16(v[i]);
+    const float r1 = v[i] - bf16_to_f32((uint16_t)h[0][i]);
+    h[1][i] = f32_to_bf16(r1);
+    h[2][i] = f32_to_bf16(r1 - bf16_to_f32((uint16_t)h[1][i]));
+  }
+  uint16_t* dst = out + (size_t)r * 3 * k + (size_t)g * 8;
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+    *(u32x4*)(dst + (size_t)p * k) = u32x4{h[p][0] | (h[p][1] << 16), h[p][2] | (h[p][3] << 16),
+                                           h[p][4] | (h[p][5] << 16), h[p][6] | (h[p][7] << 16)};
+}
+
+hipError_t launch_split_f32_planes(const float* x, uint32_t m, uint32_t k, uint32_t x_stride, uint16_t* out,
+                                   hipStream_t s) {
+  const size_t n = (size_t)m * (k / 8);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(split_f32_planes_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, m, k, x_stride,
+                     out);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ unpackFp8 (src/kernels/fp8.ts:24-36)
 __global__ void unpack_fp8_kernel(const uint8_t* packed, size_t n, const float* scale, float* out) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;

@@ -162,14 +162,18 @@ __global__ void __launch_bounds__(256) peak_mfma_bf16_data(uint32_t iters, uint3
   out[id] = __float_as_uint(s);
 }
 
-// Streaming read of n16 16-byte chunks in one shot: each thread loads READ_PEAK_U chunks spaced by the grid
-// (all in flight at once, no loop; the grid covers the buffer), sums their words, and each wave writes one sum.
+// Streaming read of n16 16-byte chunks in one shot: workgroup b reads the contiguous 32 KB block of chunks
+// [b 256 U, (b + 1) 256 U), thread t the chunks t, t + 256, ... of it (each load instruction reads 1 KB of consecutive
+// bytes), all in flight at once, no loop; the grid covers the buffer. It sums the words and each wave writes one sum.
+// Measured on MI355X over one 34 MB buffer (graph replays, 10 rotating copies): this form 6.70 us, the same loads
+// spaced by the whole grid 7.15 us, 2 or 4 times larger workgroups 7.9-8.2 us.
 __global__ void __launch_bounds__(256) read_peak(const u32x4* __restrict__ p, uint64_t n16, uint32_t* out) {
-  const uint64_t tid = (uint64_t)blockIdx.x * 256 + threadIdx.x, stride = (uint64_t)gridDim.x * 256;
+  const uint64_t tid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t base = (uint64_t)blockIdx.x * 256 * READ_PEAK_U + threadIdx.x;
   u32x4 v[READ_PEAK_U];
 #pragma unroll
   for (int u = 0; u < READ_PEAK_U; u++) {
-    const uint64_t i = tid + u * stride;
+    const uint64_t i = base + (uint64_t)u * 256;
     v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
   }
   u32x4 t = v[0];

@@ -985,6 +985,28 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
   if (rc) return rc;
   we::GemmLaunch L;
   fill_gemm(L, ctx->tune, p, x_dtype, x, w_dtype, w, y_dtype, y, bias, flags, gate, res, mul, splits, kc);
+  // f32 activations (the reference's own dtype) on the fast path: x is split once into three exact bf16 planes along K
+  // in scratch ([M, 3K]: hi | mid | lo, summing to x exactly) and the fast kernel runs one GEMM over 3K with the
+  // weights read at k mod K, so each product keeps all 24 bits of x. Taken when the fast kernel accepts the planes
+  // (fp8 or bf16 weights, K a multiple of 64, aligned rows); otherwise, for the allocation-free entry point and for
+  // split-K partial modes, the general kernel splits x into the same planes tile by tile.
+  size_t plane_bytes = 0;
+  if (x_dtype == WE_F32 && !noalloc && !split && !L.generic && !L.conv_width && p->k % 64 == 0 &&
+      (w_dtype == WE_FP8_E4M3 || w_dtype == WE_BF16) && (uintptr_t)x % 16 == 0 &&
+      (uint64_t)p->m * p->k * 3 <= (1ull << 30)) {
+    we::GemmLaunch P = L;
+    P.x = (const void*)(uintptr_t)256;  // placeholder with the scratch's alignment, for the check
+    P.x_dtype = WE_BF16;
+    P.k = 3 * p->k;
+    P.kc = P.k;
+    P.k_wrap = p->k;
+    P.x_stride = 3 * p->k;
+    P.x_offset = 0;
+    if (we::gemm_fast_supported(P)) {
+      L = P;
+      plane_bytes = ((uint64_t)p->m * 3 * p->k * 2 + 255) / 256 * 256;
+    }
+  }
   bool qk_fused = false;
   if (qk && qk->q_heads + qk->k_heads) {
     L.qk_cols = (qk->q_heads + qk->k_heads) * 128;
@@ -999,9 +1021,25 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     qk_fused = we::gemm_qk_fusable(L);
     if (!qk_fused) L.qk_cols = L.q_cols = 0;  // the plain GEMM, then the q/k pass below
   }
+  we::GemmReducePlan rp{1, L.k, 0};
   if (ctx->tune.gemm_splitk != 0) {  // 0: split-K off; n > 0: n slices (sweeps)
     const uint32_t force = ctx->tune.gemm_splitk > 0 ? (uint32_t)ctx->tune.gemm_splitk : 0u;
-    const we::GemmReducePlan rp = we::gemm_reduce_plan(L, force);
+    rp = we::gemm_reduce_plan(L, force);
+  }
+  if (plane_bytes) {
+    // scratch: the planes of x, then the split-K partial sums (if any)
+    const int rc = ensure_scratch(ctx, plane_bytes + (rp.rsplits > 1 ? rp.scratch_bytes : 0));
+    if (rc) return rc;
+    L.x = ctx->scratch;
+    const hipError_t e = we::launch_split_f32_planes((const float*)x + p->x_offset, p->m, p->k, p->x_stride,
+                                                     (uint16_t*)ctx->scratch, ctx->compute);
+    if (e != hipSuccess) return hip_fail(ctx, e, "f32 plane split launch");
+    if (rp.rsplits > 1) {
+      L.scratch = (char*)ctx->scratch + plane_bytes;
+      L.rsplits = rp.rsplits;
+      L.rkc = rp.rkc;
+    }
+  } else {
     if (rp.rsplits > 1) {
       if (noalloc) {
         // the device's fixed scratch array: no allocation, a hard size limit
