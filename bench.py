@@ -8,8 +8,8 @@ timed region.
 
 The same run reports, measured with HIP events on the context's compute stream (the stream every kernel
 is launched on):
-  * roofline: the up-projection GEMM (the dominant kernel) alone: 2*M*N*K FLOP per launch over its
-    average launch time, against the bf16 / f16 dense MFMA peak;
+  * roofline: the up-projection GEMM (the dominant kernel): 2*M*N*K FLOP per launch over its average launch
+    time in the timed steps (timestamps between the launches), against the bf16 / f16 dense MFMA peak;
   * roofline_int4: the int4 decode GEMV (M = 1, K = 3584, N = 18944, group 64): algorithmic bytes per
     launch (every tensor read or written once) over its average launch time, against HBM peak; 10
     weight copies rotate (> 256 MB) so no launch reads its weights from the Infinity Cache; M = 8 and 16
@@ -104,22 +104,33 @@ def bench_mlp(g, steps, warmup, rng):
         up()
         down()
 
-    # The GEMMs alone first: measured on MI355X, the first ~10 launches after an idle GPU run below steady clocks,
-    # which a step timed first absorbed (556 us per step against 507 us for up + down timed after it). Then the
-    # step: `warmup` untimed steps and `steps` timed ones.
-    for _ in range(3):
-        step()
-    ms_up = time_launches(g, up, steps)
-    ms_dn = time_launches(g, down, steps)
+    # `warmup` untimed steps, then `steps` timed ones with a timestamp before each GEMM and after the last
+    # (events on the compute stream, no host round trip): the line's value is the whole run (first to last
+    # timestamp), and each GEMM's duration inside it is what the roofline reports, from the same launches. (Timing a
+    # GEMM alone, back to back, measures something else: the power management's response to sustained peak load;
+    # measured on MI355X, the up-projection 260 -> 338 us over 12 launches, settling near 290 us.)
     for _ in range(warmup):
         step()
-    ms_step = time_launches(g, step, steps)
+    n = steps
+    assert 2 * n + 1 <= we.TIMER_MARKS, "at most 127 timed steps"
+    g.sync()
+    for i in range(n):
+        g.timer_mark(2 * i)
+        up()
+        g.timer_mark(2 * i + 1)
+        down()
+    g.timer_mark(2 * n)
+    ms_step = g.timer_between(0, 2 * n) / n
+    ups = [g.timer_between(2 * i, 2 * i + 1) for i in range(n)]
+    dns = [g.timer_between(2 * i + 1, 2 * i + 2) for i in range(n)]
+    ms_up, ms_dn = float(np.mean(ups)), float(np.mean(dns))
     flop = 2.0 * m * f * h
     res = {
         "ms_per_step": ms_step,
         "step_tflops": 2 * flop / ms_step / 1e9,
-        "up": {"ms": ms_up, "tflops": flop / ms_up / 1e9, "flop": flop},
-        "down": {"ms": ms_dn, "tflops": flop / ms_dn / 1e9},
+        "up": {"ms": ms_up, "tflops": flop / ms_up / 1e9, "flop": flop, "median_ms": float(np.median(ups)),
+               "launches": n, "timed": "the timed steps' up-projections (timestamps between the launches)"},
+        "down": {"ms": ms_dn, "tflops": flop / ms_dn / 1e9, "median_ms": float(np.median(dns))},
     }
     for b in (x, w_up, w_dn, hid, y):
         g.free(b)
@@ -184,7 +195,7 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20, rotate=0):
     def run(i, w=ws[0]):
         g.matmul(p, x_dt, x, w_dt, w, y_dt, y)
 
-    for i in range(3):
+    for i in range(3 if m <= 64 else iters):  # large GEMMs: past the power management's first transient
         run(i)
     ms = time_graph(g, run, 10, max(1, iters // 10)) if m <= 64 else time_launches(g, run, iters)
     flop = 2.0 * m * n * k

@@ -153,6 +153,14 @@ int we_record_all(we_ctx* ctx, uint64_t tickets[3]);
 /* ---- timing on the compute stream (hipEvents) ---- */
 int we_timer_start(we_ctx* ctx);
 int we_timer_stop(we_ctx* ctx, float* ms);
+/* Timestamps between kernels without a host round trip, for harnesses that time each step of a running sequence (the
+ * per-op timings of profileBlock, src/bench/block.ts:17-95, which the reference takes with submit-and-wait):
+ * we_timer_mark records a timestamp into slot (0 .. WE_TIMER_MARKS - 1) after the work queued so far on the selected
+ * compute stream, without waiting; we_timer_between waits for slot `to` and returns the milliseconds from slot `from`
+ * to it. A slot keeps its last mark. */
+#define WE_TIMER_MARKS 256
+int we_timer_mark(we_ctx* ctx, uint32_t slot);
+int we_timer_between(we_ctx* ctx, uint32_t from, uint32_t to, float* ms);
 
 /* ---- HIP graphs of the compute stream: no counterpart in the reference (WebGPU records a command buffer
  * per submit). For launch-bound loops (decode steps, small GEMMs) and callers that replay a fixed sequence:

@@ -48,7 +48,8 @@ EXPORTS = {
     "we_st_metadata_at": "stMetadataAt", "we_st_read": "stRead", "we_stream_select": "streamSelect",
     "we_stream_fork": "streamFork", "we_stream_join": "streamJoin", "we_buf_download_async": "downloadAsync",
     "we_ticket_wait": "waitTicketAsync", "we_record_all": "recordAll", "we_set_alloc_cap": "setAllocCap",
-    "we_set_poison": "setPoison", "we_set_tuning": "setTuning",
+    "we_set_poison": "setPoison", "we_set_tuning": "setTuning", "we_timer_mark": "timerMark",
+    "we_timer_between": "timerBetween",
 }
 
 

@@ -63,6 +63,7 @@ struct we_ctx {
   bool poison = false;
   std::map<void*, size_t> scratch_sizes;  // bytes of every scratch block (current, other lane's, retired)
   we::Tuning tune;  // kernel-choice switches (we_set_tuning), from the environment at creation
+  std::vector<hipEvent_t> marks;  // timestamp slots (we_timer_mark), created on first use
 };
 
 namespace {
@@ -276,6 +277,8 @@ int we_ctx_destroy(we_ctx* ctx) {
     if (e) (void)hipEventDestroy(e);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+  for (auto& e : ctx->marks)
+    if (e) (void)hipEventDestroy(e);
   if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
   if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
   for (auto st : ctx->lanes)
@@ -713,6 +716,28 @@ int we_timer_stop(we_ctx* ctx, float* ms) {
   HIP_OK(ctx, hipEventRecord(ctx->t1, ctx->compute), "hipEventRecord");
   HIP_OK(ctx, hipEventSynchronize(ctx->t1), "hipEventSynchronize");
   HIP_OK(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1), "hipEventElapsedTime");
+  return WE_OK;
+}
+
+int we_timer_mark(we_ctx* ctx, uint32_t slot) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (ctx->capturing) return fail(ctx, WE_EINVAL, "not allowed while a graph is being captured");
+  if (slot >= WE_TIMER_MARKS) return fail(ctx, WE_EINVAL, "timer slot %u out of range (%d slots)", slot, WE_TIMER_MARKS);
+  if (ctx->marks.empty()) {
+    ctx->marks.assign(WE_TIMER_MARKS, nullptr);
+    for (auto& e : ctx->marks) HIP_OK(ctx, hipEventCreate(&e), "hipEventCreate");
+  }
+  HIP_OK(ctx, hipEventRecord(ctx->marks[slot], ctx->compute), "hipEventRecord");
+  return WE_OK;
+}
+
+int we_timer_between(we_ctx* ctx, uint32_t from, uint32_t to, float* ms) {
+  if (!ctx) return fail(ctx, WE_EINVAL, "context is null");
+  if (!ms) return fail(ctx, WE_EINVAL, "output pointer is null");
+  if (ctx->marks.empty() || from >= WE_TIMER_MARKS || to >= WE_TIMER_MARKS)
+    return fail(ctx, WE_EINVAL, "timer slots %u, %u were not marked", from, to);
+  HIP_OK(ctx, hipEventSynchronize(ctx->marks[to]), "hipEventSynchronize");
+  HIP_OK(ctx, hipEventElapsedTime(ms, ctx->marks[from], ctx->marks[to]), "hipEventElapsedTime");
   return WE_OK;
 }
 

@@ -360,6 +360,28 @@ static napi_value SetPoison(napi_env env, napi_callback_info info) {
   return status(env, ctx, we_set_poison(ctx, on));
 }
 
+/* timerMark(ctx, slot); timerBetween(ctx, from, to) -> ms */
+static napi_value TimerMark(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 2)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t slot = u32_arg(&a, 1);
+  if (a.bad) return NULL;
+  return status(env, ctx, we_timer_mark(ctx, slot));
+}
+
+static napi_value TimerBetween(napi_env env, napi_callback_info info) {
+  args_t a;
+  if (!get_args(env, info, &a, 3)) return NULL;
+  we_ctx* ctx = ptr_arg(&a, 0);
+  uint32_t from = u32_arg(&a, 1), to = u32_arg(&a, 2);
+  if (a.bad) return NULL;
+  float ms = 0.0f;
+  int rc = we_timer_between(ctx, from, to, &ms);
+  if (rc != WE_OK) return status(env, ctx, rc);
+  return num(env, (double)ms);
+}
+
 /* setTuning(ctx, key, value) -> previous value (WE_TUNE_* keys) */
 static napi_value SetTuning(napi_env env, napi_callback_info info) {
   args_t a;
@@ -1212,7 +1234,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       {"sync", Sync},             {"streamSelect", StreamSelect}, {"streamFork", StreamFork}, {"streamJoin", StreamJoin},             {"bufAlloc", BufAlloc},     {"bufFree", BufFree},
       {"upload", Upload},         {"download", Download},     {"copy", Copy},
       {"mark", Mark},             {"release", Release},       {"stats", Stats},
-      {"setAllocCap", SetAllocCap}, {"setPoison", SetPoison}, {"setTuning", SetTuning},
+      {"setAllocCap", SetAllocCap}, {"setPoison", SetPoison}, {"setTuning", SetTuning}, {"timerMark", TimerMark}, {"timerBetween", TimerBetween},
       {"hostAlloc", HostAlloc},   {"hostFree", HostFree},     {"hostWrite", HostWrite}, {"hostSpan", HostSpan}, {"hostRead", HostRead},
       {"streamCopy", StreamCopy}, {"waitTicket", WaitTicket}, {"recordCompute", RecordCompute},
       {"downloadAsync", DownloadAsync}, {"waitTicketAsync", WaitTicketAsync}, {"recordAll", RecordAll},

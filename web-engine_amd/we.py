@@ -31,6 +31,7 @@ F32, F16, BF16, FP8, INT4 = 0, 1, 2, 3, 4
 DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "fp8": FP8, "int4": INT4}
 ELEM_BYTES = {F32: 4, F16: 2, BF16: 2, FP8: 1}
 EPI_ACCUMULATE, EPI_SPLIT_K, EPI_BIAS, EPI_GELU = 1, 2, 4, 8
+TIMER_MARKS = 256  # timestamp slots (WE_TIMER_MARKS)
 # kernel-choice switches (we_set_tuning, WE_TUNE_* of include/we.h)
 TUNE_KEYS = {"gemm_cfg": 0, "gemm_generic": 1, "gemm_splitk": 2, "gemm_reduce_xcd": 3, "attn_path": 4, "int4_path": 5}
 MUL_SWIGLU, MUL_SIGMOID_GATE = 1, 2
@@ -97,6 +98,8 @@ SIGNATURES = {
     "we_set_alloc_cap": (_I, [_P, _U64, _P]),
     "we_set_poison": (_I, [_P, ctypes.c_int]),
     "we_set_tuning": (_I, [_P, ctypes.c_int, ctypes.c_int, _P]),
+    "we_timer_mark": (_I, [_P, _U32]),
+    "we_timer_between": (_I, [_P, _U32, _U32, _P]),
     "we_stream_copy": (_I, [_P, _P, _P, _SZ, _U64, _P]),
     "we_wait_ticket": (_I, [_P, _U64]),
     "we_record_compute": (_I, [_P, _P]),
@@ -381,6 +384,16 @@ class Graph:
     def timer_stop(self):
         ms = ctypes.c_float()
         self.check(self.lib.we_timer_stop(self.ctx, ctypes.byref(ms)))
+        return ms.value
+
+    def timer_mark(self, slot):
+        """Timestamp into `slot` after the work queued so far (no wait)."""
+        self.check(self.lib.we_timer_mark(self.ctx, slot))
+
+    def timer_between(self, a, b):
+        """Milliseconds from timestamp slot a to slot b (waits for b)."""
+        ms = ctypes.c_float()
+        self.check(self.lib.we_timer_between(self.ctx, a, b, ctypes.byref(ms)))
         return ms.value
 
     # ---- raw ops (one dispatch each)
