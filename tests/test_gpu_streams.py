@@ -59,3 +59,30 @@ def test_stream_calls_refused_where_they_cannot_hold(graph):
         g = graph.graph_end()
     graph.graph_destroy(g)
     graph.stream(0)  # selecting the current stream is a no-op
+
+
+def test_timestamp_slots_time_work_in_stream_order(graph):
+    """we_timer_mark records a timestamp on the compute stream without waiting (the block benchmark's per-op timings,
+    src/bench/block.ts:17-95, without a host round trip per op): intervals add up, the interval around queued GEMMs
+    covers them, and slots outside the range or never marked are refused."""
+    rng = np.random.default_rng(5)
+    m, k, n = 256, 3072, 3072
+    mark = graph.mark()
+    xb = graph.buffer(O.bf16_rne(rng.standard_normal(m * k).astype(np.float32)))
+    wb = graph.buffer(_fp8_weights(rng, n, k))
+    yb = graph.buffer(m * n * 2)
+    p = we.matmul_params(m, n, k, 0.02, graph=graph)
+    graph.sync()
+    graph.timer_mark(10)
+    for _ in range(4):
+        graph.matmul(p, we.BF16, xb, we.FP8, wb, we.BF16, yb)
+    graph.timer_mark(11)
+    graph.timer_mark(12)
+    a, b, whole = graph.timer_between(10, 11), graph.timer_between(11, 12), graph.timer_between(10, 12)
+    graph.release(mark)
+    assert a > 0 and b >= 0 and abs(whole - (a + b)) < 1e-3
+    assert b < a  # nothing queued between 11 and 12
+    with pytest.raises(we.WeError, match="out of range"):
+        graph.timer_mark(we.TIMER_MARKS)
+    with pytest.raises(we.WeError):
+        graph.timer_between(10, we.TIMER_MARKS)
