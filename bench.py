@@ -84,6 +84,24 @@ def time_graph(g, fn, per_graph, replays):
     return ms
 
 
+def settle_steps(g, step, group=10, min_ms=40.0, max_ms=400.0, tol=0.01):
+    """Runs untimed steps in groups until the time per step stops drifting (a group within tol of the previous one,
+    after at least min_ms; at most max_ms). Returns the count, the time and the first and last groups' us per step."""
+    total, n, prev, first, last = 0.0, 0, None, None, None
+    while True:
+        ms = time_launches(g, lambda i: step(n + i), group) * group
+        total += ms
+        n += group
+        per = ms / group * 1e3
+        first = per if first is None else first
+        done = prev is not None and abs(per - prev) <= tol * per and total >= min_ms
+        prev = last = per
+        if done or total >= max_ms:
+            break
+    return {"steps": n, "ms": round(total, 2), "first_group_us_per_step": round(first, 1),
+            "last_group_us_per_step": round(last, 1)}
+
+
 def bench_mlp(g, steps, warmup, rng):
     m, h, f = 4096, 3072, 12288
     x = g.buffer(bf16_bits(rng.standard_normal(m * h, dtype=np.float32)))
@@ -104,11 +122,15 @@ def bench_mlp(g, steps, warmup, rng):
         up()
         down()
 
-    # `warmup` untimed steps, then `steps` timed ones with a timestamp before each GEMM and after the last
-    # (events on the compute stream, no host round trip): the line's value is the whole run (first to last
-    # timestamp), and each GEMM's duration inside it is what the roofline reports, from the same launches. (Timing a
-    # GEMM alone, back to back, measures something else: the power management's response to sustained peak load;
-    # measured on MI355X, the up-projection 260 -> 338 us over 12 launches, settling near 290 us.)
+    # The chip's power management answers the first milliseconds of sustained MFMA load from idle with a transient:
+    # measured on MI355X from a cold start, steps 1-3 take 512-528 us, step 7 651 us, and the time decays back to
+    # 490 us by about step 50 (28 ms), where it stays (381 further steps at 487-499 us). So untimed steps run first
+    # until the step time has settled (groups of 10 steps within 1% of the previous group, at least 40 ms, at most
+    # 400 ms); the line reports what that took. Then `warmup` untimed steps, then `steps` timed ones with a timestamp
+    # before each GEMM and after the last (events on the compute stream, no host round trip): the line's value is the
+    # whole run (first to last timestamp), and each GEMM's duration inside it is what the roofline reports, from the
+    # same launches.
+    settle = settle_steps(g, step)
     for _ in range(warmup):
         step()
     n = steps
@@ -126,6 +148,7 @@ def bench_mlp(g, steps, warmup, rng):
     ms_up, ms_dn = float(np.mean(ups)), float(np.mean(dns))
     flop = 2.0 * m * f * h
     res = {
+        "settle": settle,
         "ms_per_step": ms_step,
         "step_tflops": 2 * flop / ms_step / 1e9,
         "up": {"ms": ms_up, "tflops": flop / ms_up / 1e9, "flop": flop, "median_ms": float(np.median(ups)),
@@ -195,11 +218,17 @@ def bench_gemm(g, rng, m, n, k, x_dt, w_dt, y_dt, iters=20, rotate=0):
     def run(i, w=ws[0]):
         g.matmul(p, x_dt, x, w_dt, w, y_dt, y)
 
-    for i in range(3 if m <= 64 else iters):  # large GEMMs: past the power management's first transient
-        run(i)
+    settle = None
+    if m <= 64:
+        for i in range(3):
+            run(i)
+    else:  # large GEMMs: past the power management's start transient (as the MLP steps)
+        settle = settle_steps(g, run)
     ms = time_graph(g, run, 10, max(1, iters // 10)) if m <= 64 else time_launches(g, run, iters)
     flop = 2.0 * m * n * k
     res = {"us": ms * 1e3, "tflops": flop / ms / 1e9}
+    if settle:
+        res["settle_launches"] = settle["steps"]
     if rotate and m <= 64:
         def run_rot(i):
             g.matmul(p, x_dt, x, w_dt, ws[i % rotate], y_dt, y)
@@ -601,6 +630,8 @@ def main():
                        "m": 4096, "hidden": 3072, "mlp": 12288, "weights": "fp8_e4m3fn", "activations": "bf16"}}
     if mlp:
         line.update({"value": mlp["step_tflops"], "ms_per_step": mlp["ms_per_step"]})
+        line["settle"] = dict(mlp["settle"], note="untimed steps before the warmup, run until the step time stopped "
+                                                  "drifting (the power management's start transient)")
         up = mlp["up"]
         traffic, source = measured_traffic("gemm_fp8_up")
         line["roofline"] = {"bound": "mfma", "achieved": up["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
