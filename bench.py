@@ -326,8 +326,7 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
         a, b = xs[i % 2], xs[(i + 1) % 2]
         blk.forward(weights[0], weights[1], a[0], a[1], tvec, rope, b[0], b[1])
 
-    for i in range(8):  # the first forwards run below steady clocks (measured: the first 10 ~12% slower)
-        forward(i, w_res)
+    settle = settle_steps(g, lambda i: forward(i, w_res), group=5)  # past the power management's start transient
     t_comp = time_launches(g, lambda i: forward(i, w_res), iters)
     # profileBlock (src/bench/block.ts:17-95): every step on its own, serial, after the whole-block timing
     ops = blk.profile(w_res[0], w_res[1], xs[0][0], xs[0][1], tvec, rope, xs[1][0], xs[1][1])
@@ -366,7 +365,7 @@ def bench_block(g, rng, layers=16, pinned_sets=4, iters=10):
     flop = 2.0 * (tt + ti) * H * (3 * H + H + 2 * cfg.mlp) + 4.0 * (tt + ti) ** 2 * H
     attn_flop = 4.0 * (tt + ti) ** 2 * H
     return {"tokens": f"{tt} text + {ti} image", "layers_streamed": layers, "flop_per_block": flop,
-            "resident_ms": t_comp, "resident_tflops": flop / t_comp / 1e9,
+            "resident_ms": t_comp, "resident_tflops": flop / t_comp / 1e9, "settle_forwards": settle["steps"],
             "attention_us": attn_ms * 1e3, "attention_tflops": attn_flop / attn_ms / 1e9,
             "weight_bytes_per_block": layout.nbytes, "copy_ms_per_block": t_copy,
             "h2d_gbs": layout.nbytes / t_copy / 1e6, "streamed_ms_per_block": t_stream,

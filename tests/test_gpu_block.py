@@ -285,7 +285,7 @@ def test_double_block_full_shape_sampled_rows_match_the_oracle(graph):
 def test_double_block_overlapped_streams_equal_serial(graph, tune, grouped):
     """The text stream on the second compute stream beside the image stream gives the serial block's outputs bit
     for bit at the full shape (512 + 4096 tokens, hidden 3072, bf16), forward after forward (the text GEMMs'
-    split-K slices use that stream's own scratch). With the output, up and down projections of the two streams
+    split-K slices use that stream's own scratch). With the QKV, output, up and down projections of the two streams
     grouped into one launch each (the default), the text tiles run in the image's tile shape with all of K, so
     the serial block is run with that tile shape and no split-K (gemm_cfg, gemm_splitk) for the
     comparison."""

@@ -150,9 +150,9 @@ class DoubleBlock:
     """The double-stream block at fixed token counts, with its workspace allocated once. With overlap (the
     default) the text stream's steps run on the context's second compute stream, beside the image stream's:
     the two streams meet only in the joint attention, and the text stream's small GEMMs fill workgroup slots
-    the image stream leaves free. With grouped (the default, with overlap) the output, up and down projections
-    of the two streams run as one launch each (we_matmul_group). The result is the same bit for bit as serial
-    calls that use the same tile shapes."""
+    the image stream leaves free. With grouped (the default, with overlap) the QKV, output, up and down
+    projections of the two streams run as one launch each (we_matmul_group), the QKV launch followed by the q / k
+    RMSNorm (+ RoPE) passes. The result is the same bit for bit as serial calls that use the same tile shapes."""
 
     def __init__(self, graph, cfg, txt_tokens, img_tokens, dtype=we.BF16, overlap=True, grouped=True):
         if cfg.heads != cfg.kv_heads or cfg.heads * cfg.head_dim != cfg.hidden:
@@ -167,6 +167,7 @@ class DoubleBlock:
         self.o = graph.buffer(self.tokens * H * e)
         self.overlap = overlap
         self.grouped = grouped and overlap  # the grouped projections use each stream's own buffers
+        self.group_qkv = self.grouped  # the QKV projections grouped as well (then q / k normalized by passes)
         if overlap:  # each stream its own norm output and MLP hidden
             self.h = [graph.buffer(r * H * e) for r in self.rows]
             self.u = [graph.buffer(r * cfg.mlp * e) for r in self.rows]
@@ -257,7 +258,27 @@ class DoubleBlock:
                                  x=self.u[s], w=ws[s].down.buffer, y=outs[s], gate=sl(self.mod[s], 5 * H * 4, H * 4),
                                  residual=self.x1[s]) for s in (0, 1)], dt, we.FP8, dt)
 
-        self._streams(qkv_step)
+        def qkv_grouped():
+            # the two QKV projections share N and K: one launch (we_matmul_group) writes both streams' rows of the
+            # shared [text + image, 3 hidden] buffer; then the per-head RMSNorm of q and k (and RoPE on the image
+            # rows) as passes, in place
+            self._streams(lambda s: g.rmsnorm_mod(self.rows[s], H, cfg.eps, 1.0, dt, xs[s], ws[s].norm1, tvec,
+                                                  ws[s].table, 6 * H, self.mod[s], self.h[s]))
+            g.matmul_group([dict(params=we.matmul_params(self.rows[s], 3 * H, H, ws[s].qkv.scale,
+                                                         y_offset=self.row0[s] * 3 * H, graph=g),
+                                 x=self.h[s], w=ws[s].qkv.buffer, y=self.qkv) for s in (0, 1)], dt, we.FP8, dt)
+            for s in (0, 1):
+                rotate = s == 1
+                cos, sin = (rope_img.cos, rope_img.sin) if rotate else (None, None)
+                for part, norm_w in ((0, ws[s].norm_q), (1, ws[s].norm_k)):
+                    base = sl(self.qkv, (self.row0[s] * 3 * H + part * H) * e, 0)
+                    g.qk_norm_rope(self.rows[s], heads, hd, cfg.eps, 1.0, norm_w, 0 if rotate else self.rows[s], False,
+                                   cos, sin, dt, base, base, x_stride=3 * H, out_stride=3 * H)
+
+        if self.group_qkv:
+            qkv_grouped()
+        else:
+            self._streams(qkv_step)
         g.attention(self.tokens, heads, heads, hd, False, dt, self.qkv, sl(self.qkv, H * e, 0),
                     sl(self.qkv, 2 * H * e, 0), self.o, q_stride=3 * H, k_stride=3 * H, v_stride=3 * H, out_stride=H)
         if self.grouped:

@@ -1140,19 +1140,22 @@ int we_matmul_group(we_ctx* ctx, uint32_t count, const we_matmul_item* items, in
     struct Span {
       uintptr_t lo, hi;
     };
-    auto span = [](const void* p, uint64_t bytes) { return Span{(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; };
+    // the bytes from the first element an operand's rows touch to the last (offset, rows - 1 strides, one row)
+    auto rows_span = [](const void* p, uint64_t off, uint64_t rows, uint64_t stride, uint64_t cols, uint64_t eb) {
+      if (!p || !rows || !cols) return Span{0, 0};
+      return Span{(uintptr_t)p + (uintptr_t)(off * eb), (uintptr_t)p + (uintptr_t)((off + (rows - 1) * stride + cols) * eb)};
+    };
     auto hit = [](Span a, Span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; };
     const uint64_t xb = elem_bytes(x_dtype), wb = elem_bytes(w_dtype), yb = elem_bytes(y_dtype);
     Span out[2], in[2][5];
     for (int i = 0; i < 2; i++) {
       const we_matmul_params* p = items[i].p;
-      const uint64_t y_need = ((uint64_t)p->y_offset + (uint64_t)(p->m - 1) * p->y_stride + p->n) * yb;
-      out[i] = span(items[i].y, y_need);
-      in[i][0] = span(items[i].x, p->k ? ((uint64_t)p->x_offset + (uint64_t)(p->m - 1) * p->x_stride + p->k) * xb : 0);
-      in[i][1] = span(items[i].w, p->k ? ((uint64_t)p->w_offset + (uint64_t)(p->n - 1) * p->w_stride + p->k) * wb : 0);
-      in[i][2] = span(items[i].bias, (flags & WE_EPI_BIAS) ? (uint64_t)p->n * 4 : 0);
-      in[i][3] = span(items[i].gate, items[i].gate ? (uint64_t)p->n * 4 : 0);
-      in[i][4] = span(items[i].residual, items[i].residual ? y_need : 0);
+      out[i] = rows_span(items[i].y, p->y_offset, p->m, p->y_stride, p->n, yb);
+      in[i][0] = rows_span(items[i].x, p->x_offset, p->m, p->x_stride, p->k, xb);
+      in[i][1] = rows_span(items[i].w, p->w_offset, p->n, p->w_stride, p->k, wb);
+      in[i][2] = rows_span((flags & WE_EPI_BIAS) ? items[i].bias : nullptr, 0, 1, 0, p->n, 4);
+      in[i][3] = rows_span(items[i].gate, 0, 1, 0, p->n, 4);
+      in[i][4] = rows_span(items[i].residual, p->y_offset, p->m, p->y_stride, p->n, yb);  // read where y is written
     }
     if (hit(out[0], out[1])) return false;
     for (int i = 0; i < 2; i++)
