@@ -649,7 +649,11 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, uint32_t kv
     if (grp == 0 && t >= 2 && t + 2 < nt) issue(t + 2);
     const int cs = (t % PP_NS) * STAGE, ps = ((t - 1) % PP_NS) * STAGE;
     // causal: the scores of a tile no query of this wave sees are computed and left unused
+    // the wave in its MFMA phase wins issue arbitration over its SIMD's softmax wave (causal 4608 x 24 x 128:
+    // 215 -> 212 us; non-causal unchanged)
+    __builtin_amdgcn_s_setprio(3);
     if (active(t - 1)) attn_mphase16<IS_F16, true, true, true>(vst + ps, kst + cs, qf, pf, o, sacc, c, hf, vl);
+    __builtin_amdgcn_s_setprio(0);
     if (grp == 1 && t + 1 < nt) wait_tile(t + 1);
     barrier();
     if (grp == 1 && t + 3 < nt) issue(t + 3);
