@@ -174,6 +174,15 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
+  // The ping-pong tiles multiply on 16x16x32 MFMAs (more work per watt at the chip's power limit: 4096 x 12288 x 3072
+  // up-projection 245 -> 227 us, same box, against 32x32x16), the other tiles on 32x32x16. Accumulator block (ri, rc)
+  // of a lane holds rows ri * RS + lrow and the 4 columns ccol(rc) + lcol .. + 3 of the wave tile: 32x32 blocks give
+  // lane (l32, h) row l32 and, per block, 4 runs (8 q + 4 h); 16x16 blocks give lane (r16, g) row r16 and one run 4 g.
+  constexpr int RS = PP ? 16 : 32;          // rows of an accumulator block
+  constexpr int RR = WTM / RS;              // accumulator block rows per wave
+  constexpr int TN16 = WTN / 16;            // 16x16 blocks per wave row (ping-pong tiles)
+  constexpr int RC = PP ? TN16 : 4 * TN;    // 4-column runs per row and lane
+  using AccT = std::conditional_t<PP, f32x4, f32x16>;
   constexpr bool B8 = BT == FP8;
   constexpr int WB = B8 ? 1 : 2;                  // weight bytes per value
   constexpr int A_BYTES = BM * 128;               // x: BM rows x 64 k x 2 B
@@ -304,13 +313,27 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       for (int s = 0; s < 4; s++) rdb[s] = (uint32_t)(A_BYTES + (wn * WTN + l32) * 128 + ((sa ^ s) * 16));
     }
   }
+  // 16x16x32 (ping-pong tiles): 2 MFMA steps per 64-k block; step s, lane group g uses the 8 k of logical chunk
+  // 2 g + s of both operands (k 16 g + 8 s ..), so an fp8 weight lane reads the 16 bytes of both steps at once.
+  // x: row wm WTM + 16 i + r16; fp8 weights: row wn WTN + 16 j + r16, whose swizzle (bits 1-4 of the row) depends on
+  // the parity of j; 16-bit weights: per step, as x.
+  const int r16 = lane & 15, g16 = lane >> 4;
+  uint32_t rx16[2], rw16[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    rx16[t] = (uint32_t)((wm * WTM + r16) * 128 + (((2 * g16 + t) ^ swz128(r16)) * 16));
+    if constexpr (B8)
+      rw16[t] = (uint32_t)(A_BYTES + (wn * WTN + 16 * t + r16) * 64 + ((g16 ^ swz64(16 * t + r16)) * 16));
+    else
+      rw16[t] = (uint32_t)(A_BYTES + (wn * WTN + r16) * 128 + (((2 * g16 + t) ^ swz128(r16)) * 16));
+  }
   auto rd = [&](uint32_t off) { return *(const u32x4*)(lds + off); };
 
-  f32x16 acc[TM][TN];
+  AccT acc[RR][PP ? TN16 : TN];
 #pragma unroll
-  for (int i = 0; i < TM; i++)
+  for (int i = 0; i < RR; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+    for (int j = 0; j < (PP ? TN16 : TN); j++) acc[i][j] = AccT{};
 
   u32x4 xf[2][TM];           // x fragments, double-buffered over steps
   u32x4 wr[2][TN];           // fp8: raw 16-B chunks (t = 0, 1); 16-bit: fragments double-buffered over steps
@@ -338,63 +361,66 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     // memory phase of block t: interval 2t or 2t + 1.
     static_assert(NW % 2 == 0 && S >= 2, "ping-pong needs two wave groups");
     const int grp = wave / (NW / 2);
-    u32x4 xb[4][TM];                // x fragments of the 4 MFMA steps of a block
-    u32x4 wb[B8 ? 2 : 4][TN];       // fp8: raw 16-byte chunks (2 steps each); 16-bit: fragments per step
+    u32x4 xb[2][RR];                // x fragments of the 2 MFMA steps of a block
+    u32x4 wb[B8 ? 1 : 2][TN16];     // fp8: raw 16-byte chunks (both steps); 16-bit: fragments per step
     auto pp_barrier = [&]() {
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     };
-    // fp8 with 4 x 2 MFMAs per step (the 128 x 64 wave tile): the weight fragments of the block are unpacked at
-    // the end of the memory phase, which is shorter than the compute phase, so the compute phase issues its 32
-    // MFMAs back to back (2-3% off the 4096 x 12288 x 3072 and 4096 x 3072 x 12288 projections). The 64 x 96
-    // wave tile (2 x 3 MFMAs per step, 24 unpacks) unpacks only its first step there (1.7% off 4096 x 9216 x
-    // 3072) and the other three between its MFMAs: moving two or all four made its memory phase the longer one.
-    constexpr int PRE = !B8 ? 0 : TM >= 4 ? 4 : 1;  // steps unpacked in the memory phase
+    // fp8 with 8 x 4 MFMAs per step (the 128 x 64 wave tile): the weight fragments of the block are unpacked at the
+    // end of the memory phase, which is shorter than the compute phase, so the compute phase issues its MFMAs back
+    // to back (2-3% off the 4096 x 12288 x 3072 and 4096 x 3072 x 12288 projections). The 64 x 96 wave tile (4 x 6
+    // MFMAs per step) unpacks only its first step there (1.7% off 4096 x 9216 x 3072) and the second between its
+    // MFMAs: unpacking more there made its memory phase the longer one.
+    constexpr int PRE = !B8 ? 0 : RR >= 8 ? 2 : 1;  // steps unpacked in the memory phase
     constexpr bool PRE_CVT = PRE > 0;
-    u32x4 wcv[PRE_CVT ? PRE : 1][TN];
+    u32x4 wcv[PRE_CVT ? PRE : 1][TN16];
+    auto unpack = [&](const u32x4& r, int q) {
+      const u32x2 lo = cvt_fp8x4<IS_F16>(r[2 * q]), hi = cvt_fp8x4<IS_F16>(r[2 * q + 1]);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    };
     auto memory_block = [&](uint32_t st_off) {
 #pragma unroll
-      for (int q = 0; q < 4; q++) read_x(st_off, q, xb[q]);
+      for (int q = 0; q < 2; q++)
 #pragma unroll
-      for (int q = 0; q < (B8 ? 2 : 4); q++) read_w(st_off, q, wb[q]);
+        for (int i = 0; i < RR; i++) xb[q][i] = rd(st_off + rx16[q] + i * 16 * 128);
+#pragma unroll
+      for (int q = 0; q < (B8 ? 1 : 2); q++)
+#pragma unroll
+        for (int j = 0; j < TN16; j++)
+          wb[q][j] = B8 ? rd(st_off + rw16[j & 1] + (j >> 1) * 32 * 64) : rd(st_off + rw16[q] + j * 16 * 128);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if constexpr (PRE_CVT) {
 #pragma unroll
         for (int q = 0; q < PRE; q++)
 #pragma unroll
-          for (int j = 0; j < TN; j++) {
-            const u32x4 r = wb[q >> 1][j];
-            const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
-            wcv[q][j] = u32x4{lo.x, lo.y, hi.x, hi.y};
-          }
+          for (int j = 0; j < TN16; j++) wcv[q][j] = unpack(wb[0][j], q);
       }
     };
-    // LD: issue this wave's L loads of the block at kb into stage st between the MFMAs (L / 4 per step)
+    // LD: issue this wave's L loads of the block at kb into stage st between the MFMAs (half of them per step)
     auto compute_block = [&](bool ld, uint32_t kb, int st) {
-      static_for<0, 4>([&](auto Q) {
+      static_for<0, 2>([&](auto Q) {
         constexpr int q = decltype(Q)::value;
         if (LM && ld) {  // wave-uniform
-          constexpr int PER = (L + 3) / 4, Q0 = q * PER, Q1 = Q0 + PER < L ? Q0 + PER : L;
+          constexpr int PER = (L + 1) / 2, Q0 = q * PER, Q1 = Q0 + PER < L ? Q0 + PER : L;
           static_for<Q0, Q1>([&](auto QQ) { issue_one(QQ, kb, st); });
         }
-        u32x4 w[TN];
+        u32x4 w[TN16];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
+        for (int j = 0; j < TN16; j++) {
           if constexpr (PRE_CVT && q < PRE) {
             w[j] = wcv[q < PRE ? q : 0][j];
           } else if constexpr (B8) {
-            const u32x4 r = wb[q >> 1][j];
-            const u32x2 lo = cvt_fp8x4<IS_F16>(r[(q & 1) * 2]), hi = cvt_fp8x4<IS_F16>(r[(q & 1) * 2 + 1]);
-            w[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            w[j] = unpack(wb[0][j], q);
           } else {
             w[j] = wb[q][j];
           }
         }
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = 0; i < RR; i++)
 #pragma unroll
-          for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(w[j], xb[q][i], acc[i][j]);
+          for (int j = 0; j < TN16; j++) acc[i][j] = mfma_16x16x32<IS_F16>(w[j], xb[q][i], acc[i][j]);
       });
     };
     // own loads of block t + 1 complete; blocks issued after it (up to S - 2 of them) may be in flight
@@ -513,65 +539,106 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     // wave's tile with the shader's decoding of every byte (0x7f / 0xff -> +-480).
     float probe = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int i = 0; i < RR; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+      for (int j = 0; j < (PP ? TN16 : TN); j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) probe += acc[i][j][v] * 0.0f;
+        for (int v = 0; v < (PP ? 4 : 16); v++) probe += acc[i][j][v] * 0.0f;
     if (__ballot(probe != probe) != 0) {
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int i = 0; i < RR; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
-      for (uint32_t k0 = k_begin; k0 < k_end; k0 += 16) {
-        const uint32_t kk = k0 + 8 * h;  // 8 k per lane half; k_end - k0 >= 16 (multiples of 16)
-        const uint32_t kkw = kk >= a.kwrap2 ? kk - a.kwrap2 : kk >= a.kwrap ? kk - a.kwrap : kk;  // weights' k
-        u32x4 xr[TM];
-        u32x4 wv[TN];
+        for (int j = 0; j < (PP ? TN16 : TN); j++) acc[i][j] = AccT{};
+      if constexpr (PP) {
+        // 16x16x32 steps of 32 k: lane group g takes k0 + 8 g; the last step of a slice may hold only 16 k
+        for (uint32_t k0 = k_begin; k0 < k_end; k0 += 32) {
+          const uint32_t kk = k0 + 8 * g16;
+          const bool in = kk < k_end;
+          const uint32_t kkw = kk >= a.kwrap2 ? kk - a.kwrap2 : kk >= a.kwrap ? kk - a.kwrap : kk;  // weights' k
+          u32x4 xr[RR];
+          u32x4 wv[TN16];
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
-          const uint32_t row = row0 + wm * WTM + i * 32 + l32;
-          const uint32_t o = row < a.m ? (row * a.x_stride + kk) * 2 : kInvalid;
-          xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+          for (int i = 0; i < RR; i++) {
+            const uint32_t row = row0 + wm * WTM + i * 16 + r16;
+            const uint32_t o = row < a.m && in ? (row * a.x_stride + kk) * 2 : kInvalid;
+            xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+          }
+#pragma unroll
+          for (int j = 0; j < TN16; j++) {
+            const uint32_t col = col0 + wn * WTN + j * 16 + r16;
+            const uint32_t o = col < a.n && in ? col * a.w_stride + kkw : kInvalid;
+            const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
+            const u32x2 lo = fp8x4_to_16<IS_F16>(raw.x), hi = fp8x4_to_16<IS_F16>(raw.y);
+            wv[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          }
+#pragma unroll
+          for (int i = 0; i < RR; i++)
+#pragma unroll
+            for (int j = 0; j < TN16; j++) acc[i][j] = mfma_16x16x32<IS_F16>(wv[j], xr[i], acc[i][j]);
         }
+      } else {
+        for (uint32_t k0 = k_begin; k0 < k_end; k0 += 16) {
+          const uint32_t kk = k0 + 8 * h;  // 8 k per lane half; k_end - k0 >= 16 (multiples of 16)
+          const uint32_t kkw = kk >= a.kwrap2 ? kk - a.kwrap2 : kk >= a.kwrap ? kk - a.kwrap : kk;  // weights' k
+          u32x4 xr[TM];
+          u32x4 wv[TN];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-          const uint32_t col = col0 + wn * WTN + j * 32 + l32;
-          const uint32_t o = col < a.n ? col * a.w_stride + kkw : kInvalid;
-          const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
-          const u32x2 lo = fp8x4_to_16<IS_F16>(raw.x), hi = fp8x4_to_16<IS_F16>(raw.y);
-          wv[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          for (int i = 0; i < TM; i++) {
+            const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+            const uint32_t o = row < a.m ? (row * a.x_stride + kk) * 2 : kInvalid;
+            xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+          }
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            const uint32_t col = col0 + wn * WTN + j * 32 + l32;
+            const uint32_t o = col < a.n ? col * a.w_stride + kkw : kInvalid;
+            const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
+            const u32x2 lo = fp8x4_to_16<IS_F16>(raw.x), hi = fp8x4_to_16<IS_F16>(raw.y);
+            wv[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          }
+#pragma unroll
+          for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(wv[j], xr[i], acc[i][j]);
         }
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int j = 0; j < TN; j++) acc[i][j] = mfma_32x32x16<IS_F16>(wv[j], xr[i], acc[i][j]);
       }
     }
   }
+
+  // the accumulators as runs of 4 consecutive columns: block row ri (row ri * RS + lrow of the wave tile), run rc
+  // (columns ccol(rc) + lcol .. + 3)
+  const int lrow = PP ? r16 : l32, lcol = PP ? 4 * g16 : 4 * h;
+  auto ccol = [](int rc) { return PP ? rc * 16 : (rc >> 2) * 32 + 8 * (rc & 3); };
+  auto av = [&](int ri, int rc) -> f32x4 {
+    if constexpr (PP) {
+      return acc[ri][rc];
+    } else {
+      const int j = rc >> 2, q = rc & 3;
+      return f32x4{acc[ri][j][4 * q], acc[ri][j][4 * q + 1], acc[ri][j][4 * q + 2], acc[ri][j][4 * q + 3]};
+    }
+  };
 
   if (a.rsplits > 1) {
     // ---- split-K slice: raw sums (no scale) to the partial-sum plane of this slice
     const size_t plane = (size_t)a.m * a.n;
     const bool vec = (a.n & 3u) == 0u;
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-      const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+    for (int i = 0; i < RR; i++) {
+      const uint32_t row = row0 + wm * WTM + i * RS + lrow;
       if (row >= a.m) continue;
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+      for (int rc = 0; rc < RC; rc++) {
+        const uint32_t c0 = col0 + wn * WTN + ccol(rc) + lcol;
+        float* p = a.part + z * plane + (size_t)row * a.n + c0;
+        const f32x4 v = av(i, rc);
+        if (vec && c0 + 3 < a.n) {
+          *(f32x4*)p = v;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const uint32_t c0 = col0 + wn * WTN + j * 32 + 8 * q + 4 * h;
-          float* p = a.part + z * plane + (size_t)row * a.n + c0;
-          if (vec && c0 + 3 < a.n) {
-            *(f32x4*)p = f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-              if (c0 + e < a.n) p[e] = acc[i][j][4 * q + e];
-          }
+          for (int e = 0; e < 4; e++)
+            if (c0 + e < a.n) p[e] = v[e];
         }
+      }
     }
     return;
   }
@@ -652,8 +719,7 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     }
   }
 
-  // ---- epilogue: lane (l32, h) holds row l32 of each 32-row sub-tile and, for q = 0..3, the columns
-  // 8q + 4h .. 8q + 4h + 3 of each 32-column sub-tile (accumulator entries 4q .. 4q + 3)
+  // ---- epilogue over the runs of 4 columns (av, ccol, lcol, lrow above)
   const bool accum = (a.flags & WE_EPI_ACCUMULATE_BIT) != 0;
   const bool has_bias = (a.flags & WE_EPI_BIAS_BIT) != 0;
   const bool gelu = (a.flags & WE_EPI_GELU_BIT) != 0;
@@ -672,61 +738,59 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       constexpr int MD = decltype(MODE)::value;
       constexpr bool GT = MD == 1;
       const void* other = MD == 1 ? addend : aux;  // the operand read beside the accumulators
-      f32x4 gv[TN][4];  // the lane's gate values, the same for every row
+      f32x4 gv[RC];  // the lane's gate values, the same for every row
       if constexpr (GT) {
 #pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-          for (int q = 0; q < 4; q++) gv[j][q] = *(const f32x4*)(a.gate + wcol0 + 4 * h + j * 32 + 8 * q);
+        for (int rc = 0; rc < RC; rc++) gv[rc] = *(const f32x4*)(a.gate + wcol0 + lcol + ccol(rc));
       }
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const size_t yrow = (size_t)a.y_offset + (zrow + wrow0 + i * 32 + l32) * (size_t)a.y_stride + wcol0 + 4 * h;
+      for (int i = 0; i < RR; i++) {
+        const size_t yrow = (size_t)a.y_offset + (zrow + wrow0 + i * RS + lrow) * (size_t)a.y_stride + wcol0 + lcol;
         if constexpr (YT == F32) {
           float* p = (float*)a.y + yrow;
           const float* r0 = MD ? (const float*)other + yrow : nullptr;
 #pragma unroll
-          for (int j = 0; j < TN; j++)
+          for (int rc = 0; rc < RC; rc++) {
+            const f32x4 v = av(i, rc);
+            f32x4 r;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              f32x4 r;
-#pragma unroll
-              for (int e = 0; e < 4; e++) {
-                const float t = acc[i][j][4 * q + e] * a.scale;
-                r[e] = decltype(GELU)::value ? gelu_tanh(t) : t;
-              }
-              if constexpr (GT) r = *(const f32x4*)(r0 + j * 32 + 8 * q) + gv[j][q] * r;
-              if constexpr (MD >= 2) {
-                const f32x4 ax = *(const f32x4*)(r0 + j * 32 + 8 * q);
-#pragma unroll
-                for (int e = 0; e < 4; e++) r[e] = mul_epilogue(MD - 1, ax[e], r[e]);
-              }
-              *(f32x4*)(p + j * 32 + 8 * q) = r;
+            for (int e = 0; e < 4; e++) {
+              const float t = v[e] * a.scale;
+              r[e] = decltype(GELU)::value ? gelu_tanh(t) : t;
             }
+            if constexpr (GT) r = *(const f32x4*)(r0 + ccol(rc)) + gv[rc] * r;
+            if constexpr (MD >= 2) {
+              const f32x4 ax = *(const f32x4*)(r0 + ccol(rc));
+#pragma unroll
+              for (int e = 0; e < 4; e++) r[e] = mul_epilogue(MD - 1, ax[e], r[e]);
+            }
+            *(f32x4*)(p + ccol(rc)) = r;
+          }
         } else if (PP && MD == 0 && a.store16) {
-          // Whole rows through LDS. In the MFMA layout one store instruction covers 32 rows with 16 bytes each;
-          // staged 32 rows at a time in the wave's own LDS region (every wave is past its last fragment read:
-          // the ping-pong loop ends on a barrier that follows the other group's last memory phase), the
-          // stores become 16 bytes per lane over whole row segments. Measured: 3% off the 4096 x 12288 x 3072
-          // up-projection. Rows are padded by 16 bytes, which puts the 32 rows of a write on distinct banks.
+          // Whole rows through LDS. In the MFMA layout one store instruction covers 16 rows with 32 bytes each (4
+          // lanes of 8 bytes per row); staged RS rows at a time in the wave's own LDS region (every wave is past
+          // its last fragment read: the ping-pong loop ends on a barrier that follows the other group's last
+          // memory phase), the stores become 16 bytes per lane over whole row segments. Measured with 32x32 blocks:
+          // 3% off the 4096 x 12288 x 3072 up-projection. Rows are padded by 16 bytes, which puts the rows of a
+          // write on distinct banks.
           constexpr int P = WTN * 2 + 16, CPR = WTN / 8;  // row pitch in bytes, 16-byte chunks per row
+          static_assert((RS * CPR) % 64 == 0, "whole rounds of 64 lanes");
           char* reg = lds + wave * (32 * P);
           const std::integral_constant<bool, YT == F16> tag;
 #pragma unroll
-          for (int j = 0; j < TN; j++)
+          for (int rc = 0; rc < RC; rc++) {
+            const f32x4 v = av(i, rc);
+            float t[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              float t[4];
-#pragma unroll
-              for (int e = 0; e < 4; e++) {
-                t[e] = acc[i][j][4 * q + e] * a.scale;
-                if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
-              }
-              *(u32x2*)(reg + l32 * P + j * 64 + q * 16 + h * 8) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
+            for (int e = 0; e < 4; e++) {
+              t[e] = v[e] * a.scale;
+              if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
             }
-          uint16_t* yb = (uint16_t*)a.y + (size_t)a.y_offset + (zrow + wrow0 + i * 32) * (size_t)a.y_stride + wcol0;
+            *(u32x2*)(reg + lrow * P + (ccol(rc) + lcol) * 2) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
+          }
+          uint16_t* yb = (uint16_t*)a.y + (size_t)a.y_offset + (zrow + wrow0 + i * RS) * (size_t)a.y_stride + wcol0;
 #pragma unroll
-          for (int s = 0; s < CPR / 2; s++) {  // 32 rows x CPR chunks = CPR / 2 rounds of 64 lanes
+          for (int s = 0; s < RS * CPR / 64; s++) {  // RS rows x CPR chunks in rounds of 64 lanes
             const int idx = s * 64 + lane, r = idx / CPR, c = idx % CPR;
             *(u32x4*)(yb + (size_t)r * a.y_stride + c * 8) = *(const u32x4*)(reg + r * P + c * 16);
           }
@@ -735,24 +799,23 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
           const uint16_t* r0 = MD ? (const uint16_t*)other + yrow : nullptr;
           const std::integral_constant<bool, YT == F16> tag;
 #pragma unroll
-          for (int j = 0; j < TN; j++)
+          for (int rc = 0; rc < RC; rc++) {
+            const f32x4 v = av(i, rc);
+            float t[4];
+            u32x2 old = {0u, 0u};
+            if constexpr (MD != 0) old = *(const u32x2*)(r0 + ccol(rc));
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              float t[4];
-              u32x2 old = {0u, 0u};
-              if constexpr (MD != 0) old = *(const u32x2*)(r0 + j * 32 + 8 * q);
-#pragma unroll
-              for (int e = 0; e < 4; e++) {
-                t[e] = acc[i][j][4 * q + e] * a.scale;
-                if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
-                if constexpr (MD != 0) {
-                  const uint32_t hb = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
-                  const float o = YT == BF16 ? bf16_to_f32((uint16_t)hb) : f16_to_f32((uint16_t)hb);
-                  t[e] = GT ? o + gv[j][q][e] * t[e] : mul_epilogue(MD - 1, o, t[e]);
-                }
+            for (int e = 0; e < 4; e++) {
+              t[e] = v[e] * a.scale;
+              if constexpr (decltype(GELU)::value) t[e] = gelu_tanh(t[e]);
+              if constexpr (MD != 0) {
+                const uint32_t hb = ((e < 2 ? old.x : old.y) >> (16 * (e & 1))) & 0xffffu;
+                const float o = YT == BF16 ? bf16_to_f32((uint16_t)hb) : f16_to_f32((uint16_t)hb);
+                t[e] = GT ? o + gv[rc][e] * t[e] : mul_epilogue(MD - 1, o, t[e]);
               }
-              *(u32x2*)(p + j * 32 + 8 * q) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
             }
+            *(u32x2*)(p + ccol(rc)) = u32x2{pack2(t[0], t[1], tag), pack2(t[2], t[3], tag)};
+          }
         }
       }
     };
@@ -771,19 +834,19 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     return;
   }
 #pragma unroll
-  for (int i = 0; i < TM; i++) {
-    const uint32_t row = row0 + wm * WTM + i * 32 + l32;
+  for (int i = 0; i < RR; i++) {
+    const uint32_t row = row0 + wm * WTM + i * RS + lrow;
     if (row >= a.m) continue;
     const size_t yrow = (size_t)a.y_offset + (zrow + row) * (size_t)a.y_stride;
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t c0 = col0 + wn * WTN + j * 32 + 8 * q + 4 * h;
+    for (int rc = 0; rc < RC; rc++) {
+      {
+        const uint32_t c0 = col0 + wn * WTN + ccol(rc) + lcol;
+        const f32x4 av4 = av(i, rc);
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          float t = acc[i][j][4 * q + e] * a.scale;
+          float t = av4[e] * a.scale;
           if (has_bias) t += a.bias[c0 + e < a.n ? c0 + e : 0];
           if (gelu) t = gelu_tanh(t);
           if (a.gate) t *= a.gate[c0 + e < a.n ? c0 + e : 0];
