@@ -1,6 +1,7 @@
 // Fast path of the gfx950 GEMM for the hot dtypes: 16-bit activations (bf16 or f16) times fp8 e4m3fn or
-// 16-bit weights, fp32 accumulation on MFMA 32x32x16, y = x . W^T * scale (+ bias, gelu, accumulate,
-// split-K) with the semantics of matmulWgsl (src/kernels/matmul.ts:118-178).
+// 16-bit weights, fp32 accumulation on MFMA (16x16x32 in the ping-pong tiles, 32x32x16 in the others),
+// y = x . W^T * scale (+ bias, gelu, accumulate, split-K) with the semantics of matmulWgsl
+// (src/kernels/matmul.ts:118-178).
 //
 // Structure (one workgroup per BM x BN output tile, 64 k per pipeline stage, S stages in LDS):
 //  * Operands move HBM -> LDS with direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): each load
@@ -175,7 +176,8 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   // The ping-pong tiles multiply on 16x16x32 MFMAs (more work per watt at the chip's power limit: 4096 x 12288 x 3072
-  // up-projection 245 -> 227 us, same box, against 32x32x16), the other tiles on 32x32x16. Accumulator block (ri, rc)
+  // up-projection 245 -> 232 us, down-projection 235 -> 224 us, bf16 4096 x 9216 x 3072 200 -> 186 us, same box,
+  // against 32x32x16), the other tiles on 32x32x16. Accumulator block (ri, rc)
   // of a lane holds rows ri * RS + lrow and the 4 columns ccol(rc) + lcol .. + 3 of the wave tile: 32x32 blocks give
   // lane (l32, h) row l32 and, per block, 4 runs (8 q + 4 h); 16x16 blocks give lane (r16, g) row r16 and one run 4 g.
   constexpr int RS = PP ? 16 : 32;          // rows of an accumulator block
