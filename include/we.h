@@ -324,9 +324,10 @@ int we_dequant_int4(we_ctx* ctx, const uint32_t* words, const uint16_t* scales, 
  * F32 / F16 / I8 as the reference: workgroups of 64 threads, each thread `iters` iterations of 64 operations
  * (8 independent chains of fma / packed-f16 fma / int8 dot4); F32 uses scalar FMAs. MFMA_BF16: workgroups of
  * 256 threads, each wave 8 independent chains of v_mfma_f32_32x32x16_bf16 per iteration (4096 FLOP per thread
- * per iteration) on small constant operands: the ceiling of the matmul's MFMA loop. MFMA_BF16_DATA: the same loop
- * on operands with the fp8-weight GEMM's bit statistics (random bf16 activations, weights decoded from random
- * e4m3fn codes, rotated every MFMA): the ceiling at the power those data draw. out: u32 [workgroups x threads]
+ * per iteration) on small constant operands: the ceiling of the matmul's MFMA loop. MFMA_BF16_DATA: the same work
+ * on v_mfma_f32_16x16x32_bf16 (the large GEMM tiles' shape) on operands with the fp8-weight GEMM's bit statistics
+ * (random bf16 activations, weights decoded from random e4m3fn codes, rotated every MFMA): the ceiling at the power
+ * those data draw. out: u32 [workgroups x threads]
  * receives each thread's folded result; *ops (may be NULL) the operation count of the dispatch. No counterpart in
  * the reference for the two MFMA kinds (src/bench/peak.ts times the shader ALUs only). */
 #define WE_PEAK_F32 0

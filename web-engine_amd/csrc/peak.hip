@@ -9,12 +9,14 @@
 //   I8:  8 chains x dot4 of int8 (v_dot4_i32_i8, 4 multiply-adds = 8 ops);
 //   MFMA_BF16: per wave 8 chains of v_mfma_f32_32x32x16_bf16 (32768 FLOP each) per iteration, i.e. 4096 FLOP
 //        per thread per iteration, on small constant operands;
-//   MFMA_BF16_DATA: the same loop on operands with the fp8-weight GEMM's bit statistics: A as its activations
+//   MFMA_BF16_DATA: the same work on v_mfma_f32_16x16x32_bf16 (the shape of the GEMM's ping-pong tiles; two per
+//        32x32x16 of the loop above) on operands with the fp8-weight GEMM's bit statistics: A as its activations
 //        (bf16 of N(0,1)-like magnitude, every mantissa bit random), B as its weights (the bf16 images of random
 //        finite e4m3fn codes, decoded by the hardware converter), 8 operand pairs per lane rotated so that
 //        consecutive MFMAs of a chain see different data. The chip runs at its power limit under the GEMM, and
-//        the power of an MFMA grows with the bits that toggle in its operands: this is the ceiling of the
-//        matmul's MFMA loop on the data it is measured with.
+//        the power of an MFMA grows with the bits that toggle in its operands (and with the accumulator bits it
+//        moves: 32x32x16 reaches about 10% less here): this is the ceiling of the matmul's MFMA loop on the data
+//        it is measured with.
 // The chains start from the thread id so no value is a compile-time constant, and every result is folded
 // into out[thread] so nothing is removed. b = 0.5 and c = 0.25 keep the float chains exact (and finite).
 #include "common.h"
@@ -136,29 +138,35 @@ __global__ void __launch_bounds__(256) peak_mfma_bf16_data(uint32_t iters, uint3
       rb[j][e] = __builtin_bit_cast(uint32_t, lo);
       rb[j][e + 1] = __builtin_bit_cast(uint32_t, hi);
     }
-  f32x16_p acc[PEAK_CHAINS];
+  f32x4 acc[PEAK_CHAINS];
 #pragma unroll
-  for (int j = 0; j < PEAK_CHAINS; j++) acc[j] = f32x16_p{};
+  for (int j = 0; j < PEAK_CHAINS; j++) acc[j] = f32x4{};
   uint32_t i = 0;
-  // groups of 8 iterations: in sub-iteration s chain j multiplies A[j] with B[(j + s) % 8]
+  // groups of 8 iterations: in sub-iteration s, half r, chain j multiplies A[j] with B[(j + s + r) % 8] (two
+  // 16x16x32 MFMAs per chain and iteration: the 32768 FLOP of one 32x32x16)
   for (; i + PEAK_CHAINS <= iters; i += PEAK_CHAINS)
 #pragma unroll
     for (int s8 = 0; s8 < PEAK_CHAINS; s8++)
 #pragma unroll
-      for (int j = 0; j < PEAK_CHAINS; j++)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ra[j]),
-                                                         __builtin_bit_cast(bf16x8, rb[(j + s8) % PEAK_CHAINS]), acc[j],
-                                                         0, 0, 0);
+      for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int j = 0; j < PEAK_CHAINS; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ra[j]),
+                                                           __builtin_bit_cast(bf16x8, rb[(j + s8 + r) % PEAK_CHAINS]),
+                                                           acc[j], 0, 0, 0);
   for (; i < iters; i++)
 #pragma unroll
-    for (int j = 0; j < PEAK_CHAINS; j++)
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ra[j]), __builtin_bit_cast(bf16x8, rb[j]),
-                                                       acc[j], 0, 0, 0);
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int j = 0; j < PEAK_CHAINS; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ra[j]),
+                                                         __builtin_bit_cast(bf16x8, rb[(j + r) % PEAK_CHAINS]), acc[j], 0,
+                                                         0, 0);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < PEAK_CHAINS; j++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) s += acc[j][v];
+    for (int v = 0; v < 4; v++) s += acc[j][v];
   out[id] = __float_as_uint(s);
 }
 
