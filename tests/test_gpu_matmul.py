@@ -724,3 +724,74 @@ def test_f32_activations_on_the_fast_path(graph, tune, m, n, k, w_dt, flags):
     tune(gemm_generic=1)
     general = run(graph, p, x, we.F32, w_store, w_dt, we.F32, flags=flags, bias=bias, y_init=y0)
     assert O.rel_error(got, general) < 4e-6
+
+
+# ---- the ping-pong tiles (16x16x32 accumulator layout) through every epilogue ----
+
+PP_CASES = {  # x dtype, weight dtype, y dtype, epilogue
+    "plain_bf16": (we.BF16, we.FP8, we.BF16, "plain"), "plain_bf16_weights": (we.BF16, we.BF16, we.BF16, "plain"),
+    "gelu_bf16": (we.BF16, we.FP8, we.BF16, "gelu"), "bias_gelu_f32": (we.BF16, we.FP8, we.F32, "bias_gelu"),
+    "gated_bf16": (we.BF16, we.FP8, we.BF16, "gated"), "gated_f32_f16x": (we.F16, we.FP8, we.F32, "gated"),
+    "swiglu_bf16": (we.BF16, we.FP8, we.BF16, "swiglu"), "sigmoid_gate_f16": (we.F16, we.F16, we.F16, "sigmoid"),
+    "accumulate_f32": (we.BF16, we.FP8, we.F32, "accumulate"), "split_partials": (we.BF16, we.FP8, we.F32, "partials"),
+    "reduce_pass_bf16": (we.BF16, we.FP8, we.BF16, "reduce"),
+}
+
+
+@pytest.mark.parametrize("shape", ["whole", "ragged"])
+@pytest.mark.parametrize("cfg", [0, 5])
+@pytest.mark.parametrize("case", list(PP_CASES))
+def test_pingpong_tiles_every_epilogue(graph, tune, cfg, shape, case):
+    """The ping-pong tiles (gemm_cfg 0: 256 x 256, 5: 256 x 192; 16x16x32 MFMAs, whose accumulator blocks hold one
+    run of 4 columns per lane) through every epilogue, on whole tiles (the per-row fast paths, the LDS-staged
+    16-bit stores) and ragged ones (the per-value path, a partial last K block): against the oracle's product
+    followed by the reference's epilogue formulas (bias and GELU src/kernels/elementwise.ts:25-29, gatedAdd :52-58,
+    swiglu :38-43, sigmoidGate :45-50, accumulate and split-K partials src/kernels/matmul.ts:159-175)."""
+    x_dt, w_dt, y_dt, epi = PP_CASES[case]
+    m, n, k = (512, 768, 256) if shape == "whole" else (300, 520, 208)
+    if epi == "reduce":  # the split-K reduce plan needs K >= 512
+        k += 256 if shape == "whole" else 320
+    rng = np.random.default_rng(cfg * 100 + len(case) + (7 if shape == "whole" else 0))
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    w_store, w_oracle, ow = make_weights(rng, n, k, w_dt)
+    scale = 0.05 if w_dt == we.FP8 else 1.0
+    tune(gemm_cfg=cfg, gemm_splitk=2 if epi == "reduce" else 0)
+    split = 2 if epi == "partials" else 1
+    p = we.matmul_params(m, n, k, scale, k_split=split, graph=graph)
+    flags = {"gelu": we.EPI_GELU, "bias_gelu": we.EPI_BIAS | we.EPI_GELU, "accumulate": we.EPI_ACCUMULATE,
+             "partials": we.EPI_SPLIT_K}.get(epi, 0)
+    bias = rng.uniform(-.5, .5, n).astype(np.float32) if flags & we.EPI_BIAS else None
+    gate = rng.uniform(-1.5, 1.5, n).astype(np.float32) if epi == "gated" else None
+    other_store, other = _store(rng.standard_normal(m * n), y_dt) if epi in ("gated", "swiglu", "sigmoid",
+                                                                               "accumulate") else (None, None)
+    mark = graph.mark()
+    xb, wb = graph.buffer(x_store), graph.buffer(w_store)
+    yb = graph.buffer(other_store) if epi == "accumulate" else graph.buffer(m * split * n * we.ELEM_BYTES[y_dt])
+    bb = graph.buffer(bias) if bias is not None else None
+    kw = {}
+    if epi == "gated":
+        kw = {"gate": graph.buffer(gate), "residual": graph.buffer(other_store)}
+    elif epi in ("swiglu", "sigmoid"):
+        kw = {"mul": we.MUL_SWIGLU if epi == "swiglu" else we.MUL_SIGMOID_GATE, "aux": graph.buffer(other_store)}
+    graph.matmul(p, x_dt, xb, w_dt, wb, y_dt, yb, bias=bb, flags=flags, **kw)
+    got = decode(graph.read(yb), y_dt)
+    graph.release(mark)
+    if epi == "partials":
+        want = O.matmul(O.matmul_params(m, n, k, scale, k_split=split), ox, x_oracle, ow, w_oracle, split=True)
+        full = O.matmul(O.matmul_params(m, n, k, scale), ox, x_oracle, ow, w_oracle)
+        assert np.abs(got - want).max() < TOL_F32_OUT * np.abs(full).max(), (cfg, shape)
+        return
+    v = O.matmul(O.matmul_params(m, n, k, scale), ox, x_oracle, ow, w_oracle)
+    if bias is not None:
+        v = v + np.tile(bias.astype(np.float64), m)
+    if flags & we.EPI_GELU:
+        v = np.vectorize(O.lib.or_gelu_tanh)(v)
+    if epi == "gated":
+        v = other + np.tile(gate.astype(np.float64), m) * v
+    elif epi == "swiglu":
+        v = other * _sigmoid(other) * v
+    elif epi == "sigmoid":
+        v = other * _sigmoid(v)
+    elif epi == "accumulate":
+        v = other + v
+    assert O.rel_error(got, v) < TOL[y_dt], (cfg, shape, case)
