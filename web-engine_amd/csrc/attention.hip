@@ -6,15 +6,17 @@
 // token's, so q, k and v can be column slices of one fused QKV projection output.
 //
 // Work split: a wave owns 32 queries of one head and walks the keys in tiles of 64 shared through LDS with
-// the other waves of its workgroup. Three kernels:
+// the other waves of its workgroup. Four kernels:
 //   * attn16_kernel / attn32_kernel: any head dim up to 128; 4 waves (128 queries), tiles staged through
 //     registers.
-//   * attn_pp_kernel (head dim 128, 16-bit, the default there): 8 waves (256 queries); K and V^T tiles
+//   * attn_pp16_kernel (head dim 128, 16-bit, the default there): 8 waves (256 queries); K and V tiles
 //     reach a 4-stage LDS ring by direct-to-LDS loads; the two waves sharing a SIMD alternate MFMA and
-//     softmax phases between workgroup barriers (ping-pong).
-//   * attn_dma_kernel (WE_ATTN_PATH=ring): the same ring with a 3-stage depth and one phase per tile.
-// For 16-bit operands at head dim 128 the three run the same per-tile arithmetic in the same order, so their
-// outputs agree bit for bit.
+//     softmax phases between workgroup barriers (ping-pong); 16x16x32 MFMAs.
+//   * attn_pp_kernel (WE_ATTN_PATH=mfma32): the same ping-pong on 32x32x16 MFMAs.
+//   * attn_dma_kernel (WE_ATTN_PATH=ring): the ring with a 3-stage depth and one phase per tile.
+// For 16-bit operands at head dim 128 the 32x32x16 kernels run the same per-tile arithmetic in the same order,
+// so their outputs agree bit for bit; the 16x16x32 kernel sums the same products in another order inside each
+// MFMA.
 //
 // 16-bit kernel (bf16 or f16 operands, fp32 accumulation, 32x32x16 MFMA):
 //   * S^T = K Q^T: the MFMA's A operand is a K tile row (a key), B is the wave's Q held in registers. In the
@@ -687,6 +689,329 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, uint32_t kv
   attn_store16<DP, IS_F16>(o[0], l[0], qi[0], h, hf, a);
 }
 
+// ------------------------------------------------------------------------------------ 16-bit, ping-pong, 16x16x32
+// The ping-pong kernel's work split, LDS ring, loads and schedule with the products on 16x16x32 MFMAs, which draw
+// less power per multiply-add than 32x32x16 (the chip runs attention at its power limit: random inputs take 273 us
+// at the block shape where all-zero ones take 244 us). A wave's 32 queries are two blocks of 16; lane (c16, g):
+// c16 = lane & 15, g = lane >> 4.
+//   S^T block (kb, qb) = K rows 16 kb .. 16 kb + 15 of the tile times Q^T of query block qb (A = K, the lane's key
+//   row 16 kb + c16 and dims 8 g .. of each 32-dim step; B = Q, query 16 qb + c16): the lane holds the scores of
+//   keys 16 kb + 4 g + e (e = 0..3) for query 16 qb + c16.
+//   P V^T step ks covers keys 32 ks .. 32 ks + 31 with k slot group g <-> keys 32 ks + 4 g + e and 32 ks + 16 + 4 g
+//   + e: exactly the scores the lane holds for kb = 2 ks and 2 ks + 1, so P stays in the lane. The V^T fragments
+//   are gathered from the key-major V tile by ds_read_b64_tr_b16 in that key order (two reads per fragment).
+//   O^T block (db, qb): the lane holds dims 16 db + 4 g + e of query 16 qb + c16.
+// The running max and sum are per query; a query's four lane groups share them (the max is reduced across the
+// groups every tile, the sum only at the end).
+
+struct Vtr16 {
+  uint32_t base;  // byte offset of the lane's first row and 8-byte half, before the chunk term
+  uint32_t xk;    // the XOR swizzle key of the lane's rows (vswz16)
+  uint32_t cc;    // the lane's 16-byte chunk inside a 16-dim block
+};
+
+// This kernel's V tile puts 16-byte chunk c of key row r at c ^ vswz16(r). A transposing read of a 16-lane group
+// touches rows 4 g + q (q = 0..3) at chunks 2 db and 2 db + 1: with the K tile's swizzle (r & 15) rows 4 g and
+// 4 g + 1 put one of those chunks on the same banks; 2 (r & 7) sends the 4 rows (and the other group of the
+// 32-lane half, rows + 4) to 16 distinct chunk positions.
+__device__ __forceinline__ int vswz16(int r) { return 2 * (r & 7); }
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane 4 q + a' addresses key kq + q of dims d0 + 4 a' .. + 3, and
+// lane 4 a + b receives keys kq .. kq + 3 of dim d0 + 4 a + b (measured on gfx950). With kq = 4 g (then 16 + 4 g)
+// and d0 = 16 db, lane (c16, g) gathers dim 16 db + c16 of the keys of its P fragment.
+__device__ __forceinline__ Vtr16 vtr16_lane(int lane) {
+  const int g = lane >> 4, q = (lane & 15) >> 2, ap = lane & 3;
+  Vtr16 v;
+  const int kr = 4 * g + q;  // the row inside 16 (rows + 16 and + 32 ks have the same swizzle)
+  v.xk = (uint32_t)vswz16(kr);
+  v.base = (uint32_t)kr * 256u + (uint32_t)(ap & 1) * 8u;
+  v.cc = (uint32_t)(ap >> 1);
+  return v;
+}
+
+template <int DB, int KS>
+__device__ __forceinline__ u32x4 vtr16_frag(const char* vt, const Vtr16& v) {
+  const char* t = vt + KS * 32 * 256 + v.base + ((((uint32_t)(2 * DB) + v.cc) ^ v.xk) << 4);
+  const attn_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_v4s*)t);
+  const attn_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_v4s*)(t + 16 * 256));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
+}
+
+// max / sum over the four lane groups of a query (lanes c16, c16 + 16, c16 + 32, c16 + 48)
+__device__ __forceinline__ float quads_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float quads_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// M phase: O^T += V^T P^T of the previous tile (PV), then S^T = K Q^T of this tile (SC): 32 fragment reads, each
+// feeding the two query blocks' MFMAs, pipelined PP_LA reads ahead. PV fragment p: ks = p / 8, db = p % 8 (an O
+// block is hit every 8 fragments); SC fragment q: step q / 4, kb = q % 4 (an S block every 4).
+template <bool IS_F16, bool PV, bool SC>
+__device__ __forceinline__ void attn_mphase_q16(const char* vt, const char* ks, const u32x4 (&qf)[2][4],
+                                                const u32x4 (&pf)[2][2], f32x4 (&o)[8][2], f32x4 (&sacc)[4][2],
+                                                int c16, int g, const Vtr16& vl) {
+  constexpr int N = (PV ? 16 : 0) + (SC ? 16 : 0);
+  constexpr auto is_pv = [](int i) { return PV && (!SC || i % 2 == 0); };
+  constexpr auto idx = [](int i) { return PV && SC ? i / 2 : i; };
+  auto frag = [&](auto I) -> u32x4 {
+    constexpr int i = I;
+    if constexpr (is_pv(i)) {
+      constexpr int pi = idx(i);
+      return vtr16_frag<pi % 8, pi / 8>(vt, vl);
+    } else {
+      constexpr int qi = idx(i), st = qi / 4, kb = qi % 4;
+      return *(const u32x4*)(ks + (16 * kb + c16) * 256 + (((4 * st + g) ^ c16) << 4));
+    }
+  };
+  if constexpr (SC) {
+    static_for<0, 4>([&](auto KB) {
+      sacc[KB][0] = f32x4{};
+      sacc[KB][1] = f32x4{};
+    });
+  }
+  u32x4 f[PP_LA + 1];
+  static_for<0, PP_LA>([&](auto I) {
+    if constexpr (I < N) f[I] = frag(I);
+  });
+  static_for<0, N>([&](auto I) {
+    constexpr int i = I;
+    if constexpr (i + PP_LA < N) f[(i + PP_LA) % (PP_LA + 1)] = frag(std::integral_constant<int, i + PP_LA>{});
+    if constexpr (is_pv(i)) {
+      constexpr int pi = idx(i), ksi = pi / 8, db = pi % 8;
+      o[db][0] = mfma_16x16x32<IS_F16>(f[i % (PP_LA + 1)], pf[ksi][0], o[db][0]);
+      o[db][1] = mfma_16x16x32<IS_F16>(f[i % (PP_LA + 1)], pf[ksi][1], o[db][1]);
+    } else {
+      constexpr int qi = idx(i), st = qi / 4, kb = qi % 4;
+      sacc[kb][0] = mfma_16x16x32<IS_F16>(f[i % (PP_LA + 1)], qf[0][st], sacc[kb][0]);
+      sacc[kb][1] = mfma_16x16x32<IS_F16>(f[i % (PP_LA + 1)], qf[1][st], sacc[kb][1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// The online softmax of one tile for the wave's two query blocks (the lazy rescale of attn_softmax16: the running
+// max moves, and O and the sums are rescaled, only when some query's max would rise by more than 8 in log2 units).
+// Whether some query's max rises that far is whether some lane's own 16 scores do (a query's max is the max of its
+// four lanes'), so the common step votes on the lanes' maxima and reduces a query's max across its lane groups only
+// when it moves. FAST: if it would move, nothing changes and the call returns false.
+template <bool IS_F16, bool FAST = false>
+__device__ __forceinline__ bool attn_softmax_q16(f32x4 (&sacc)[4][2], u32x4 (&pf)[2][2], f32x4 (&o)[8][2],
+                                                 float (&m)[2], float (&l)[2], uint32_t k0, uint32_t qw, int c16,
+                                                 int g, const AttnArgs& a) {
+  // the mask, in place and behind one wave-uniform branch: only the last tile and (causal) the tiles that cross
+  // the wave's queries hold keys to drop; masking twice (a FAST call that returns false, then the full call) is
+  // the same as once
+  if (__builtin_expect((k0 + ATT_BN > a.tokens) || (a.causal && k0 + ATT_BN - 1 > qw), 0)) {
+    static_for<0, 2>([&](auto QB) {
+      // key k0 + 4 g + c stays when c < lim: below the sequence end and (causal) at most the query
+      const uint32_t query = qw + 16 * QB + (uint32_t)c16;
+      const uint32_t end = a.causal ? min(a.tokens, query + 1) : a.tokens;
+      const int lim = (int)end - (int)(k0 + 4 * (uint32_t)g);
+      static_for<0, 4>([&](auto KB) {
+        static_for<0, 4>([&](auto E) {
+          constexpr int kb = KB, qb = QB, e = E;
+          sacc[kb][qb][e] = 16 * kb + e < lim ? sacc[kb][qb][e] : -__builtin_inff();
+        });
+      });
+    });
+  }
+  float lmax[2];
+  bool grow = false;
+  static_for<0, 2>([&](auto QB) {
+    constexpr int qb = QB;
+    float t = fmaxf(fmaxf(sacc[0][qb][0], sacc[0][qb][1]), sacc[0][qb][2]);
+    static_for<3, 16>([&](auto I) { t = fmaxf(t, sacc[I / 4][qb][I % 4]); });
+    // in log2 units: rounding is monotone, so max(x) * scale is exactly max(x * scale)
+    lmax[qb] = t * a.scale_log2;
+    grow |= lmax[qb] > m[qb] + 8.0f;
+  });
+  const bool rescale = __any(grow);
+  if constexpr (FAST) {
+    if (rescale) return false;
+  }
+  float mref[2] = {m[0], m[1]};
+  if (rescale) {  // wave-uniform: every lane takes part in the cross-lane reduction
+    static_for<0, 2>([&](auto QB) { mref[QB] = fmaxf(m[QB], quads_max(lmax[QB])); });
+  }
+  static_for<0, 2>([&](auto QB) {
+    constexpr int qb = QB;
+    const float ms = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
+    float ps = 0.0f;
+    float p[16];
+    static_for<0, 16>([&](auto I) {
+      p[I] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[I / 4][qb][I % 4], a.scale_log2, -ms));
+      ps += p[I];
+    });
+    const auto tag = std::integral_constant<bool, IS_F16>{};
+    static_for<0, 2>([&](auto KS) {
+      constexpr int k2 = KS;  // scores of kb = 2 k2 (k slots 0-3) and 2 k2 + 1 (slots 4-7)
+      pf[k2][qb] = u32x4{pack2(p[8 * k2], p[8 * k2 + 1], tag), pack2(p[8 * k2 + 2], p[8 * k2 + 3], tag),
+                         pack2(p[8 * k2 + 4], p[8 * k2 + 5], tag), pack2(p[8 * k2 + 6], p[8 * k2 + 7], tag)};
+    });
+    if constexpr (FAST) {
+      l[qb] += ps;
+    } else {
+      // alpha = 1 unless the max moved; O is multiplied on every tile (a branch around it copies all of O)
+      const float alpha = rescale ? __builtin_amdgcn_exp2f(m[qb] - ms) : 1.0f;
+      l[qb] = __builtin_fmaf(l[qb], alpha, ps);
+      m[qb] = mref[qb];
+      static_for<0, 8>([&](auto D) { o[D][qb] *= alpha; });
+    }
+  });
+  return true;
+}
+
+template <bool IS_F16, bool CAUSAL>
+__global__ void __launch_bounds__(512, 1) attn_pp16_kernel(AttnArgs a, uint32_t kv_heads) {
+  constexpr int DP = 128, NW = 8, IPW = 2;
+  constexpr int KS_BYTES = ATT_BN * DP * 2;  // 16 KB
+  constexpr int STAGE = 2 * KS_BYTES;        // K + V
+  __shared__ __attribute__((aligned(1024))) char lds[PP_NS * STAGE];
+
+  uint32_t qblk, h;
+  block_coords(a, qblk, h);
+  const uint32_t g = h / a.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int c16 = lane & 15, lg = lane >> 4;
+  const uint32_t q0 = qblk * DMA_BM;
+  const uint32_t qw = q0 + 32 * wave;
+  const uint16_t* Qp = (const uint16_t*)a.q;
+
+  // B operand of S^T: query block qb, step st holds dims 32 st + 8 g .. + 7 of query qw + 16 qb + c16
+  u32x4 qf[2][4];
+  static_for<0, 2>([&](auto QB) {
+    const uint32_t qi = qw + 16 * QB + (uint32_t)c16;
+    static_for<0, 4>([&](auto ST) {
+      qf[QB][ST] = u32x4{0, 0, 0, 0};
+      if (qi < a.tokens) qf[QB][ST] = *(const u32x4*)(Qp + (size_t)qi * a.qs + (size_t)h * DP + 32 * ST + 8 * lg);
+    });
+  });
+
+  const uint32_t kv_end = CAUSAL ? min(a.tokens, q0 + DMA_BM) : a.tokens;
+  const int nt = (int)((kv_end + ATT_BN - 1) / ATT_BN);
+  const uint32_t k_bytes = ((a.tokens - 1) * a.ks + kv_heads * DP) * 2;
+  const uint32_t v_bytes = ((a.tokens - 1) * a.vs + kv_heads * DP) * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.k, (short)0, (int)k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)a.v, (short)0, (int)v_bytes, 0x00020000);
+  // the tiles' loads: as attn_pp_kernel (instruction j fills K or V rows 4 j .. 4 j + 3; wave w issues j = w + 8 u),
+  // the V rows with this kernel's swizzle
+  auto issue = [&](int t) {
+    const uint32_t k0 = (uint32_t)t * ATT_BN;
+    char* base = lds + (t % PP_NS) * STAGE;
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ (row & 15);
+      const uint32_t key = k0 + row;
+      dma16(rk, base + j * 1024, key < a.tokens ? (key * a.ks + g * DP + logical * 8) * 2 : kAttInvalid);
+    }
+#pragma unroll
+    for (int u = 0; u < IPW; u++) {
+      const int j = wave + NW * u;
+      const int row = 4 * j + (lane >> 4), phys = lane & 15, logical = phys ^ vswz16(row);
+      const uint32_t key = k0 + row;
+      dma16(rv, base + KS_BYTES + j * 1024, key < a.tokens ? (key * a.vs + g * DP + logical * 8) * 2 : kAttInvalid);
+    }
+  };
+  const Vtr16 vl = vtr16_lane(lane);
+  auto wait_tile = [&](int t) {
+    const int ahead = min(nt - 1, max(PP_NS - 1, t + 1)) - t;
+    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * IPW) : "memory");
+    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * IPW) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * IPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto active = [&](int t) { return !CAUSAL || (uint32_t)t * ATT_BN <= qw + 31; };
+  const char* kst = lds;
+  const char* vst = lds + KS_BYTES;
+
+  f32x4 o[8][2];
+  static_for<0, 8>([&](auto D) {
+    o[D][0] = f32x4{};
+    o[D][1] = f32x4{};
+  });
+  float m[2] = {-__builtin_inff(), -__builtin_inff()}, l[2] = {0.0f, 0.0f};
+  f32x4 sacc[4][2];
+  u32x4 pf[2][2];
+  for (int t = 0; t < PP_NS; t++)
+    if (t < nt) issue(t);
+#pragma unroll
+  for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+    for (int ss = 0; ss < 4; ss++) asm volatile("" ::"v"(qf[qq][ss]));
+  wait_tile(0);
+  barrier();
+  if (grp == 1) barrier();  // group 1 runs one phase behind group 0
+  if (active(0)) attn_mphase_q16<IS_F16, false, true>(nullptr, kst, qf, pf, o, sacc, c16, lg, vl);
+  if (grp == 1 && nt > 1) wait_tile(1);
+  barrier();
+  if (active(0)) attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, 0u, qw, c16, lg, a);
+  if (grp == 0 && nt > 1) wait_tile(1);
+  barrier();
+  auto m_half = [&](int t) {
+    if (grp == 0 && t >= 2 && t + 2 < nt) issue(t + 2);
+    const int cs = (t % PP_NS) * STAGE, ps = ((t - 1) % PP_NS) * STAGE;
+    // the wave in its MFMA phase wins issue arbitration over its SIMD's softmax wave
+    __builtin_amdgcn_s_setprio(3);
+    if (active(t - 1)) attn_mphase_q16<IS_F16, true, true>(vst + ps, kst + cs, qf, pf, o, sacc, c16, lg, vl);
+    __builtin_amdgcn_s_setprio(0);
+    if (grp == 1 && t + 1 < nt) wait_tile(t + 1);
+    barrier();
+    if (grp == 1 && t + 3 < nt) issue(t + 3);
+  };
+  auto v_end = [&](int t) {
+    if (grp == 0 && t + 1 < nt) wait_tile(t + 1);
+    barrier();
+  };
+  int t = 1;
+  for (; t < nt; t++) {
+    m_half(t);
+    if (active(t) && !attn_softmax_q16<IS_F16, true>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a)) break;
+    v_end(t);
+  }
+  if (t < nt) {
+    attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a);
+    v_end(t);
+    for (t++; t < nt; t++) {
+      m_half(t);
+      if (active(t)) attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a);
+      v_end(t);
+    }
+  }
+  if (active(nt - 1))
+    attn_mphase_q16<IS_F16, true, false>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c16, lg, vl);
+  if (grp == 0) barrier();  // both groups pass the same number of barriers
+  // O = O^T / l: lane (c16, g) stores dims 16 db + 4 g .. + 3 of its two queries
+  static_for<0, 2>([&](auto QB) {
+    const float inv = 1.0f / quads_sum(l[QB]);
+    const uint32_t qi = qw + 16 * QB + (uint32_t)c16;
+    if (qi < a.tokens) {
+      uint16_t* O = (uint16_t*)a.o + (size_t)qi * a.os + (size_t)h * DP;
+      const auto tag = std::integral_constant<bool, IS_F16>{};
+      static_for<0, 8>([&](auto D) {
+        const f32x4 v = o[D][QB];
+        *(u32x2*)(O + 16 * D + 4 * lg) = u32x2{pack2(v[0] * inv, v[1] * inv, tag), pack2(v[2] * inv, v[3] * inv, tag)};
+      });
+    }
+  });
+}
+
 // ------------------------------------------------------------------------------------ f32 kernel
 template <int DP>
 __global__ void __launch_bounds__(ATT_NT, 1) attn32_kernel(AttnArgs a) {
@@ -867,9 +1192,13 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
       if (e != hipSuccess) return e;
       if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
       else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
-    } else {
+    } else if (L.path == 3) {  // the ping-pong kernel on 32x32x16 MFMAs
       const auto kern = L.dtype == F16 ? (L.causal ? attn_pp_kernel<true, true> : attn_pp_kernel<true, false>)
                                        : (L.causal ? attn_pp_kernel<false, true> : attn_pp_kernel<false, false>);
+      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
+    } else {
+      const auto kern = L.dtype == F16 ? (L.causal ? attn_pp16_kernel<true, true> : attn_pp16_kernel<true, false>)
+                                       : (L.causal ? attn_pp16_kernel<false, true> : attn_pp16_kernel<false, false>);
       hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
     }
     return hipGetLastError();

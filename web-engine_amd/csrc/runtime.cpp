@@ -198,7 +198,7 @@ int ticket_valid(we_ctx* ctx, uint64_t t) {
 namespace we {
 // The switches as the WE_* environment variables give them (the values of sweeps and tests that pin a kernel):
 // WE_GEMM_CFG=<id>, WE_GEMM_PATH=generic, WE_GEMM_SPLITK=off|<slices>, WE_GEMM_REDUCE_XCD=off,
-// WE_ATTN_PATH=registers|ring, WE_INT4_PATH=generic|shared|pipe. Unset or unknown values keep the defaults.
+// WE_ATTN_PATH=registers|ring|mfma32, WE_INT4_PATH=generic|shared|pipe. Unset or unknown values keep the defaults.
 Tuning tuning_from_env() {
   Tuning t;
   auto env = [](const char* name) -> const char* {
@@ -212,7 +212,8 @@ Tuning tuning_from_env() {
     t.gemm_splitk = strcmp(v, "off") == 0 ? 0 : n > 0 ? (int)n : -1;
   }
   if (const char* v = env("WE_GEMM_REDUCE_XCD")) t.gemm_reduce_xcd = strcmp(v, "off") != 0;
-  if (const char* v = env("WE_ATTN_PATH")) t.attn_path = strcmp(v, "registers") == 0 ? 1 : strcmp(v, "ring") == 0 ? 2 : 0;
+  if (const char* v = env("WE_ATTN_PATH"))
+    t.attn_path = strcmp(v, "registers") == 0 ? 1 : strcmp(v, "ring") == 0 ? 2 : strcmp(v, "mfma32") == 0 ? 3 : 0;
   if (const char* v = env("WE_INT4_PATH"))
     t.int4_path = strcmp(v, "generic") == 0 ? 1 : strcmp(v, "shared") == 0 ? 2 : strcmp(v, "pipe") == 0 ? 3 : 0;
   return t;
@@ -299,7 +300,7 @@ int we_set_tuning(we_ctx* ctx, int key, int value, int* previous) {
     case WE_TUNE_GEMM_GENERIC: slot = &ctx->tune.gemm_generic, lo = 0, hi = 1; break;
     case WE_TUNE_GEMM_SPLITK: slot = &ctx->tune.gemm_splitk, lo = -1, hi = 1 << 16; break;
     case WE_TUNE_GEMM_REDUCE_XCD: slot = &ctx->tune.gemm_reduce_xcd, lo = 0, hi = 1; break;
-    case WE_TUNE_ATTN_PATH: slot = &ctx->tune.attn_path, lo = 0, hi = 2; break;
+    case WE_TUNE_ATTN_PATH: slot = &ctx->tune.attn_path, lo = 0, hi = 3; break;
     case WE_TUNE_INT4_PATH: slot = &ctx->tune.int4_path, lo = 0, hi = 3; break;
     default: return fail(ctx, WE_EINVAL, "unknown tuning key %d", key);
   }
