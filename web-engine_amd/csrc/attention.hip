@@ -800,9 +800,12 @@ __device__ __forceinline__ void attn_mphase_q16(const char* vt, const char* ks, 
 
 // The online softmax of one tile for the wave's two query blocks (the lazy rescale of attn_softmax16: the running
 // max moves, and O and the sums are rescaled, only when some query's max would rise by more than 8 in log2 units).
-// Whether some query's max rises that far is whether some lane's own 16 scores do (a query's max is the max of its
-// four lanes'), so the common step votes on the lanes' maxima and reduces a query's max across its lane groups only
-// when it moves. FAST: if it would move, nothing changes and the call returns false.
+// FAST (the common step): p = exp2(s * scale - m) against the running max as it is, and the call returns false,
+// changing nothing, when some lane's sum of p over its 16 scores of a query exceeds 2^8. Every accepted p is then at
+// most 2^8, which is all the lazy rescale asks for; a rejected tile takes the full step, whose p equal FAST's
+// where its max does not move. Full step: whether some query's max rises by more than 8 is whether some lane's own
+// 16 scores do (a query's max is the max of its four lanes'), so it votes on the lanes' maxima and reduces a
+// query's max across its lane groups only when it moves.
 template <bool IS_F16, bool FAST = false>
 __device__ __forceinline__ bool attn_softmax_q16(f32x4 (&sacc)[4][2], u32x4 (&pf)[2][2], f32x4 (&o)[8][2],
                                                  float (&m)[2], float (&l)[2], uint32_t k0, uint32_t qw, int c16,
@@ -824,50 +827,60 @@ __device__ __forceinline__ bool attn_softmax_q16(f32x4 (&sacc)[4][2], u32x4 (&pf
       });
     });
   }
-  float lmax[2];
-  bool grow = false;
-  static_for<0, 2>([&](auto QB) {
+  const auto tag = std::integral_constant<bool, IS_F16>{};
+  // p of query block qb against the reference max ms, packed to the operand type; returns the lane's sum
+  auto exps = [&](auto QB, float ms) -> float {
     constexpr int qb = QB;
-    float t = fmaxf(fmaxf(sacc[0][qb][0], sacc[0][qb][1]), sacc[0][qb][2]);
-    static_for<3, 16>([&](auto I) { t = fmaxf(t, sacc[I / 4][qb][I % 4]); });
-    // in log2 units: rounding is monotone, so max(x) * scale is exactly max(x * scale)
-    lmax[qb] = t * a.scale_log2;
-    grow |= lmax[qb] > m[qb] + 8.0f;
-  });
-  const bool rescale = __any(grow);
-  if constexpr (FAST) {
-    if (rescale) return false;
-  }
-  float mref[2] = {m[0], m[1]};
-  if (rescale) {  // wave-uniform: every lane takes part in the cross-lane reduction
-    static_for<0, 2>([&](auto QB) { mref[QB] = fmaxf(m[QB], quads_max(lmax[QB])); });
-  }
-  static_for<0, 2>([&](auto QB) {
-    constexpr int qb = QB;
-    const float ms = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
     float ps = 0.0f;
     float p[16];
     static_for<0, 16>([&](auto I) {
       p[I] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[I / 4][qb][I % 4], a.scale_log2, -ms));
       ps += p[I];
     });
-    const auto tag = std::integral_constant<bool, IS_F16>{};
     static_for<0, 2>([&](auto KS) {
       constexpr int k2 = KS;  // scores of kb = 2 k2 (k slots 0-3) and 2 k2 + 1 (slots 4-7)
       pf[k2][qb] = u32x4{pack2(p[8 * k2], p[8 * k2 + 1], tag), pack2(p[8 * k2 + 2], p[8 * k2 + 3], tag),
                          pack2(p[8 * k2 + 4], p[8 * k2 + 5], tag), pack2(p[8 * k2 + 6], p[8 * k2 + 7], tag)};
     });
-    if constexpr (FAST) {
-      l[qb] += ps;
-    } else {
-      // alpha = 1 unless the max moved; O is multiplied on every tile (a branch around it copies all of O)
+    return ps;
+  };
+  if constexpr (FAST) {
+    // m is finite here: the first tile takes the full step and holds a key of every query
+    const float ps0 = exps(std::integral_constant<int, 0>{}, m[0]);
+    const float ps1 = exps(std::integral_constant<int, 1>{}, m[1]);
+    // also rejects inf and NaN sums (a score far above the max)
+    if (__any(!(ps0 <= 256.0f) | !(ps1 <= 256.0f))) return false;
+    l[0] += ps0;
+    l[1] += ps1;
+    return true;
+  } else {
+    float lmax[2];
+    bool grow = false;
+    static_for<0, 2>([&](auto QB) {
+      constexpr int qb = QB;
+      float t = fmaxf(fmaxf(sacc[0][qb][0], sacc[0][qb][1]), sacc[0][qb][2]);
+      static_for<3, 16>([&](auto I) { t = fmaxf(t, sacc[I / 4][qb][I % 4]); });
+      // in log2 units: rounding is monotone, so max(x) * scale is exactly max(x * scale)
+      lmax[qb] = t * a.scale_log2;
+      grow |= lmax[qb] > m[qb] + 8.0f;
+    });
+    const bool rescale = __any(grow);
+    float mref[2] = {m[0], m[1]};
+    if (rescale) {  // wave-uniform: every lane takes part in the cross-lane reduction
+      static_for<0, 2>([&](auto QB) { mref[QB] = fmaxf(m[QB], quads_max(lmax[QB])); });
+    }
+    static_for<0, 2>([&](auto QB) {
+      constexpr int qb = QB;
+      const float ms = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
+      const float ps = exps(QB, ms);
+      // alpha = 1 unless the max moved; O is multiplied on every full step (a branch around it copies all of O)
       const float alpha = rescale ? __builtin_amdgcn_exp2f(m[qb] - ms) : 1.0f;
       l[qb] = __builtin_fmaf(l[qb], alpha, ps);
       m[qb] = mref[qb];
       static_for<0, 8>([&](auto D) { o[D][qb] *= alpha; });
-    }
-  });
-  return true;
+    });
+    return true;
+  }
 }
 
 template <bool IS_F16, bool CAUSAL>
@@ -979,20 +992,12 @@ __global__ void __launch_bounds__(512, 1) attn_pp16_kernel(AttnArgs a, uint32_t 
     if (grp == 0 && t + 1 < nt) wait_tile(t + 1);
     barrier();
   };
-  int t = 1;
-  for (; t < nt; t++) {
+  for (int t = 1; t < nt; t++) {
     m_half(t);
-    if (active(t) && !attn_softmax_q16<IS_F16, true>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a)) break;
+    // the common step leaves O alone; a tile that moves a max takes the full step
+    if (active(t) && !attn_softmax_q16<IS_F16, true>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a))
+      attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a);
     v_end(t);
-  }
-  if (t < nt) {
-    attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a);
-    v_end(t);
-    for (t++; t < nt; t++) {
-      m_half(t);
-      if (active(t)) attn_softmax_q16<IS_F16>(sacc, pf, o, m, l, (uint32_t)t * ATT_BN, qw, c16, lg, a);
-      v_end(t);
-    }
   }
   if (active(nt - 1))
     attn_mphase_q16<IS_F16, true, false>(vst + ((nt - 1) % PP_NS) * STAGE, nullptr, qf, pf, o, sacc, c16, lg, vl);
