@@ -100,7 +100,7 @@ int we_set_poison(we_ctx* ctx, int on);
  * variants from TUNE_CONFIGS (src/kernels/matmul-tuned.ts:13-125); here the variants are built in and a switch pins
  * one, for tile sweeps, measurements and tests. A context starts from the environment as it is at we_ctx_create
  * (WE_GEMM_CFG=<id>, WE_GEMM_PATH=generic, WE_GEMM_SPLITK=off|<slices>, WE_GEMM_REDUCE_XCD=off,
- * WE_ATTN_PATH=registers|ring|mfma32, WE_INT4_PATH=generic|shared|pipe); launches read the context, never the environment.
+ * WE_ATTN_PATH=registers|ring|mfma16, WE_INT4_PATH=generic|shared|pipe); launches read the context, never the environment.
  * we_set_tuning sets one key (WE_EINVAL for an unknown key or a value out of range) and returns the old value in
  * `previous` (may be NULL). */
 #define WE_TUNE_GEMM_CFG 0        /* fast-GEMM tile: 0 256x256, 1 256x128, 2 128x128, 3 64x64, 4 32x64, 5 256x192; -1 by shape */
@@ -108,7 +108,7 @@ int we_set_poison(we_ctx* ctx, int on);
 #define WE_TUNE_GEMM_SPLITK 2     /* -1: split-K plan by shape, 0: off, n > 0: n slices */
 #define WE_TUNE_GEMM_REDUCE_XCD 3 /* 1: the split-K reduce reads each tile on its XCD where that pays, 0: never */
 #define WE_TUNE_ATTN_PATH 4       /* 0: default, 1: register-staged kernel, 2: DMA ring with a V^T pre-pass,
-                                     3: ping-pong kernel on 32x32x16 MFMAs */
+                                     3: ping-pong kernel on 16x16x32 MFMAs */
 #define WE_TUNE_INT4_PATH 5       /* 0: by shape, 1: general kernel, 2: shared-x kernel, 3: LDS-ring decode kernel */
 int we_set_tuning(we_ctx* ctx, int key, int value, int* previous);
 

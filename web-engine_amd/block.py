@@ -286,12 +286,13 @@ class DoubleBlock:
         else:
             self._streams(out_step)
 
-    def profile(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img, reps=5):
+    def profile(self, w_txt, w_img, x_txt, x_img, tvec, rope_img, out_txt, out_img, reps=5, warm=None):
         """Where the block's time goes (profileBlock, src/bench/block.ts:17-95): the steps of forward() in its
         order, each run on its own on compute stream 0 (`reps` back-to-back calls between HIP events, after one
-        untimed call), per stream, without the overlap and grouping of forward(). Every step rewrites its outputs
-        from inputs it does not write, so repeating it changes nothing. Returns [{name, kind, us}], kind one of
-        linear / attention / other as in the reference."""
+        untimed call, or after warm(step) where given: a caller's untimed run-up, e.g. until the clocks settle),
+        per stream, without the overlap and grouping of forward(). Every step rewrites its outputs from inputs it
+        does not write, so repeating it changes nothing. Returns [{name, kind, us}], kind one of linear /
+        attention / other as in the reference."""
         g, cfg, dt = self.graph, self.cfg, self.dtype
         H, hd, heads, e = cfg.hidden, cfg.head_dim, cfg.heads, we.ELEM_BYTES[dt]
         sl = we.Graph.slice
@@ -332,7 +333,10 @@ class DoubleBlock:
                      outs[s], gate=sl(mod, 5 * H * 4, H * 4), residual=self.x1[s]))]
         out = []
         for name, kind, fn in steps:
-            fn()
+            if warm is None:
+                fn()
+            else:
+                warm(fn)
             g.sync()
             g.timer_start()
             for _ in range(reps):

@@ -9,10 +9,11 @@
 // the other waves of its workgroup. Four kernels:
 //   * attn16_kernel / attn32_kernel: any head dim up to 128; 4 waves (128 queries), tiles staged through
 //     registers.
-//   * attn_pp16_kernel (head dim 128, 16-bit, the default there): 8 waves (256 queries); K and V tiles
+//   * attn_pp_kernel (head dim 128, 16-bit, the default there): 8 waves (256 queries); K and V tiles
 //     reach a 4-stage LDS ring by direct-to-LDS loads; the two waves sharing a SIMD alternate MFMA and
-//     softmax phases between workgroup barriers (ping-pong); 16x16x32 MFMAs.
-//   * attn_pp_kernel (WE_ATTN_PATH=mfma32): the same ping-pong on 32x32x16 MFMAs.
+//     softmax phases between workgroup barriers (ping-pong); 32x32x16 MFMAs.
+//   * attn_pp16_kernel (WE_ATTN_PATH=mfma16): the same ping-pong on 16x16x32 MFMAs. Faster while the chip has
+//     power to spare (a single call after idle), slower at the power limit a run of blocks holds it at.
 //   * attn_dma_kernel (WE_ATTN_PATH=ring): the ring with a 3-stage depth and one phase per tile.
 // For 16-bit operands at head dim 128 the 32x32x16 kernels run the same per-tile arithmetic in the same order,
 // so their outputs agree bit for bit; the 16x16x32 kernel sums the same products in another order inside each
@@ -1197,13 +1198,13 @@ hipError_t attention_launch(const AttnLaunch& L, hipStream_t s) {
       if (e != hipSuccess) return e;
       if (L.dtype == F16) hipLaunchKernelGGL((attn_dma_kernel<true, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
       else hipLaunchKernelGGL((attn_dma_kernel<false, 1>), grid, dim3(512), 0, s, a, (const uint16_t*)vt, tp, L.kv_heads);
-    } else if (L.path == 3) {  // the ping-pong kernel on 32x32x16 MFMAs
-      const auto kern = L.dtype == F16 ? (L.causal ? attn_pp_kernel<true, true> : attn_pp_kernel<true, false>)
-                                       : (L.causal ? attn_pp_kernel<false, true> : attn_pp_kernel<false, false>);
-      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
-    } else {
+    } else if (L.path == 3) {  // the ping-pong kernel on 16x16x32 MFMAs
       const auto kern = L.dtype == F16 ? (L.causal ? attn_pp16_kernel<true, true> : attn_pp16_kernel<true, false>)
                                        : (L.causal ? attn_pp16_kernel<false, true> : attn_pp16_kernel<false, false>);
+      hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
+    } else {
+      const auto kern = L.dtype == F16 ? (L.causal ? attn_pp_kernel<true, true> : attn_pp_kernel<true, false>)
+                                       : (L.causal ? attn_pp_kernel<false, true> : attn_pp_kernel<false, false>);
       hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, a, L.kv_heads);
     }
     return hipGetLastError();

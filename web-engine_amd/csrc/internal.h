@@ -28,7 +28,7 @@ struct Tuning {
   int gemm_splitk = -1;     // -1: split-K plan by shape, 0: off, n > 0: n slices
   int gemm_reduce_xcd = 1;  // 1: the split-K reduce reads each tile on its XCD where that pays, 0: never
   int attn_path = 0;        // 0: default kernel, 1: register-staged kernel, 2: DMA ring with the V^T pre-pass,
-                            // 3: ping-pong kernel on 32x32x16 MFMAs
+                            // 3: ping-pong kernel on 16x16x32 MFMAs
   int int4_path = 0;        // 0: by shape, 1: general kernel, 2: shared-x kernel, 3: LDS-ring decode kernel
 };
 Tuning tuning_from_env();

@@ -198,7 +198,7 @@ int ticket_valid(we_ctx* ctx, uint64_t t) {
 namespace we {
 // The switches as the WE_* environment variables give them (the values of sweeps and tests that pin a kernel):
 // WE_GEMM_CFG=<id>, WE_GEMM_PATH=generic, WE_GEMM_SPLITK=off|<slices>, WE_GEMM_REDUCE_XCD=off,
-// WE_ATTN_PATH=registers|ring|mfma32, WE_INT4_PATH=generic|shared|pipe. Unset or unknown values keep the defaults.
+// WE_ATTN_PATH=registers|ring|mfma16, WE_INT4_PATH=generic|shared|pipe. Unset or unknown values keep the defaults.
 Tuning tuning_from_env() {
   Tuning t;
   auto env = [](const char* name) -> const char* {
@@ -213,7 +213,7 @@ Tuning tuning_from_env() {
   }
   if (const char* v = env("WE_GEMM_REDUCE_XCD")) t.gemm_reduce_xcd = strcmp(v, "off") != 0;
   if (const char* v = env("WE_ATTN_PATH"))
-    t.attn_path = strcmp(v, "registers") == 0 ? 1 : strcmp(v, "ring") == 0 ? 2 : strcmp(v, "mfma32") == 0 ? 3 : 0;
+    t.attn_path = strcmp(v, "registers") == 0 ? 1 : strcmp(v, "ring") == 0 ? 2 : strcmp(v, "mfma16") == 0 ? 3 : 0;
   if (const char* v = env("WE_INT4_PATH"))
     t.int4_path = strcmp(v, "generic") == 0 ? 1 : strcmp(v, "shared") == 0 ? 2 : strcmp(v, "pipe") == 0 ? 3 : 0;
   return t;
