@@ -691,10 +691,10 @@ __global__ void __launch_bounds__(512, 1) attn_pp_kernel(AttnArgs a, uint32_t kv
 }
 
 // ------------------------------------------------------------------------------------ 16-bit, ping-pong, 16x16x32
-// The ping-pong kernel's work split, LDS ring, loads and schedule with the products on 16x16x32 MFMAs, which draw
-// less power per multiply-add than 32x32x16 (the chip runs attention at its power limit: random inputs take 273 us
-// at the block shape where all-zero ones take 244 us). A wave's 32 queries are two blocks of 16; lane (c16, g):
-// c16 = lane & 15, g = lane >> 4.
+// The ping-pong kernel's work split, LDS ring, loads and schedule with the products on 16x16x32 MFMAs. Measured at
+// the block shape (4608 tokens, 24 heads): alone after settling 250 us against 267 us for attn_pp_kernel, but after
+// 20 block forwards (the power limit a run of blocks holds the chip at) 303-311 against 283-288 us, so it is not the
+// default. A wave's 32 queries are two blocks of 16; lane (c16, g): c16 = lane & 15, g = lane >> 4.
 //   S^T block (kb, qb) = K rows 16 kb .. 16 kb + 15 of the tile times Q^T of query block qb (A = K, the lane's key
 //   row 16 kb + c16 and dims 8 g .. of each 32-dim step; B = Q, query 16 qb + c16): the lane holds the scores of
 //   keys 16 kb + 4 g + e (e = 0..3) for query 16 qb + c16.
