@@ -51,6 +51,7 @@ struct Int4Args {
 namespace {
 constexpr uint32_t kInvalid = 0x80000000u;
 constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kCpolNt = 2;  // buffer-load cache policy: nt (non-temporal)
 }  // namespace
 
 // v_and_or_b32 with the mask in a VGPR and the constant in an SGPR (one instruction; the compiler
@@ -296,6 +297,16 @@ __device__ __forceinline__ u32x4 interleave8(u32x4 v) {
 }
 
 
+// dma16 with the non-temporal cache policy, for weights read once per call (the shared-x kernel's weight pieces:
+// M = 8 12.85-13.44 -> 12.47-12.77 us, M = 16 13.69-13.96 -> 13.42-13.54 us, alternating processes, same box; x and
+// the scales, which every workgroup reads, keep the default policy)
+__device__ __forceinline__ void dma16_nt(const __amdgpu_buffer_rsrc_t& r, void* dst, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"((uint32_t)(uintptr_t)(lds_ptr_t*)dst), "v"(voff), "s"(r)
+               : "memory");
+}
+
 template <int XT>
 __global__ void __launch_bounds__(256) int4_gemv_pipe_kernel(Int4Args a) {
   constexpr bool IS_F16 = XT == F16;
@@ -522,7 +533,7 @@ __global__ void __launch_bounds__(64 * TILES * WPT) int4_gemv_shared_kernel(Int4
     for (int j = 0; j < LPC; j++) {
       const int first = j * NT + wave * 64;
       if (first < XP) dma16(rx, slot + first * 16, c + blk[j] < nblk ? src[j] + c * 128 : kInvalid);
-      else if (first < PIECES) dma16(rw, slot + first * 16, c + blk[j] < nblk ? src[j] + c * 32 : kInvalid);
+      else if (first < PIECES) dma16_nt(rw, slot + first * 16, c + blk[j] < nblk ? src[j] + c * 32 : kInvalid);
       else dma16(rw, ring + SK_NBUF * SLOT, kInvalid);  // a spare: zeros into the pad, counted like the others
     }
   };
@@ -669,13 +680,15 @@ __global__ void __launch_bounds__(256) int4_gemv_direct_kernel(Int4Args a) {
       sh[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < 16 * ng ? (n0 * ng + i) * 2 : kInvalid, 0, 0);
     }
   }
-  // the weights: all of the lane's pieces at once (pieces past the row read as zeros and are skipped below)
+  // the weights: all of the lane's pieces at once (pieces past the row read as zeros and are skipped below).
+  // Non-temporal (cache policy nt): every weight byte is read once per call (M = 1 decode shape: 9.54-10.0 ->
+  // 9.20-9.30 us, alternating processes, same box)
   u32x4 wv[NP];
 #pragma unroll
   for (int j = 0; j < NP; j++) {
     const uint32_t pc = (uint32_t)(l16 + 16 * j);
     const uint32_t o = row < a.n && pc < npc ? row * (a.k / 2) + pc * 16 : kInvalid;
-    wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+    wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, kCpolNt));
   }
 #pragma unroll
   for (int j = 0; j < 2; j++) {
