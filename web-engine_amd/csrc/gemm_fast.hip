@@ -43,6 +43,7 @@ constexpr int BK = 64;
 
 constexpr uint32_t kInvalid = 0x80000000u;  // a byte offset past every extent: the load returns 0
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kCpolNt = 2;                  // buffer-load cache policy: nt (non-temporal)
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
@@ -278,6 +279,12 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
     if (j == 0) kb8 = c * 16 / WB;
   }
 
+  // With one row of tiles (M <= BM) every weight byte is read once per call: its loads take the non-temporal cache
+  // policy (64 x 3072 x 3072 with the weights streamed from HBM: 11.24 -> 10.78 us; with the weights left in the
+  // caches between calls 9.28 -> 9.37 us). Where M-tiles share the weights it costs L2 reuse (the 4096 x 12288 x 3072
+  // up-projection 232 -> 244 us). Not in the ping-pong tiles, whose memory phase the branch reorders (the
+  // up-projection 232 -> 241-246 us with it).
+  const bool w_once = !PP && a.tiles_m == 1;
   // load q (0 .. L - 1) of this wave's share of the 64-k block starting at kb, into stage st
   auto issue_one = [&](auto Q, uint32_t kb, int st) {
     constexpr int q = decltype(Q)::value;
@@ -291,8 +298,13 @@ __global__ void __launch_bounds__(WAVES_M* WAVES_N * 64) gemm_lds_kernel(FastArg
       constexpr int j = q - A_PW;
       const uint32_t o = (full || kb + kb8 < k_end) ? offb[j] : kInvalid;
       const uint32_t kbw = kb >= a.kwrap2 ? kb - a.kwrap2 : kb >= a.kwrap ? kb - a.kwrap : kb;  // weights' k
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t*)(base + A_BYTES + (lw + j * NL) * 1024), 16, o,
-                                               (int)(kbw * WB), 0, 0);
+      lds_ptr_t* dst = (lds_ptr_t*)(base + A_BYTES + (lw + j * NL) * 1024);
+      if constexpr (!PP) {
+        if (w_once) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, o, (int)(kbw * WB), 0, kCpolNt);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, o, (int)(kbw * WB), 0, 0);
+      } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, o, (int)(kbw * WB), 0, 0);
+      }
     }
   };
   // issue this wave's share of the loads of the 64-k block starting at kb into stage st
