@@ -1,7 +1,7 @@
 """HIP graphs of the compute stream (we_graph_begin / end / launch / destroy).
 
-A graph captures split-K fp8 GEMM (two kernels), the int4 decode GEMV, bf16 attention (V^T pre-pass + DMA
-kernel), RMSNorm and an elementwise op. It is replayed several times; before each replay the inputs are
+A graph captures split-K fp8 GEMM (two kernels), the int4 decode GEMV, bf16 attention (the ping-pong kernel),
+RMSNorm and an elementwise op. It is replayed several times; before each replay the inputs are
 rewritten (eager uploads, a sync), and every replay's outputs must equal, bit for bit, the same calls run
 eagerly on the same inputs.
 """
