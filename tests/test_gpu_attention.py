@@ -171,3 +171,29 @@ def test_dma_ring_path_equals_register_path(graph, tune, tokens, heads, kv_heads
     rows = (0, min(tokens, 16))
     want = O.attention(qv, kv, vv, tokens, heads, kv_heads, 128, causal, rows=rows)
     assert O.rel_error(pp16.reshape(tokens, -1)[rows[0]:rows[1]].ravel(), want) < 1e-2
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 63, 255, 256])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [we.BF16, we.F32])
+def test_tiny_and_block_edge_token_counts(graph, tokens, causal, dtype):
+    """Token counts at the edges of the kernels' work units: one and two tokens (a single key tile, most rows of
+    the workgroup past the end), one short of a key tile, and one short of / exactly a 256-query block. Head dim
+    128, 2 query heads over 1 kv head; every output against the oracle. f32 takes the reference test's inputs
+    (one LCG stream, uniform in [-2, 2]), which its 1e-5 bar is set for; 16-bit takes normal inputs."""
+    heads, kv_heads, dim = 2, 1, 128
+    sizes = [tokens * heads * dim, tokens * kv_heads * dim, tokens * kv_heads * dim]
+    shape = we.AttentionShape(tokens, heads, kv_heads, dim, causal=causal)
+    if dtype == we.F32:
+        q32, k32, v32 = lcg_random(tokens * 2 + causal + 1, sizes)
+        got = run(graph, q32, k32, v32, shape, dtype)
+        want = O.attention(q32, k32, v32, tokens, heads, kv_heads, dim, causal)
+        assert np.abs(got - want).max() < 1e-5
+    else:
+        rng = np.random.default_rng(tokens * 2 + causal)
+        q32, k32 = (rng.standard_normal(n).astype(np.float32) * 2 for n in sizes[:2])
+        v32 = rng.standard_normal(sizes[2]).astype(np.float32)
+        (q, qv), (k, kv), (v, vv) = (to16(x, dtype) for x in (q32, k32, v32))
+        got = run(graph, q, k, v, shape, dtype)
+        want = O.attention(qv, kv, vv, tokens, heads, kv_heads, dim, causal)
+        assert O.rel_error(got, want) < 1e-2
