@@ -151,3 +151,15 @@ def test_f32_activations_keep_every_mantissa_bit(graph):
     assert np.array_equal(want, exact)
     got = run(graph, m, n, k, group, words, scales, x.ravel(), we.F32, we.F32)
     assert np.array_equal(got, exact), np.abs(got - exact).max()
+
+
+@pytest.mark.parametrize("m,n,k,group", [(1, 1, 64, 64), (1, 3, 128, 64), (2, 1, 64, 64), (16, 1, 128, 128),
+                                         (17, 2, 64, 64), (1, 17, 192, 64)])
+def test_tiny_shapes(graph, m, n, k, group):
+    """One or a few output columns (most of the kernels' 16-row work units past N), a single scale group, and M
+    on both sides of the shared-x kernel's range."""
+    rng = np.random.default_rng(m * 10 + n + k)
+    words, scales, x, ox = make(rng, m, n, k, group)
+    got = run(graph, m, n, k, group, words, scales, x, we.F16, we.F32)
+    want = O.matmul(O.matmul_params(m, n, k, 1.0), ox, x, O.INT4, words, scales=scales, group=group)
+    assert O.rel_error(got, want) < 1e-5

@@ -795,3 +795,23 @@ def test_pingpong_tiles_every_epilogue(graph, tune, cfg, shape, case):
     elif epi == "accumulate":
         v = other + v
     assert O.rel_error(got, v) < TOL[y_dt], (cfg, shape, case)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 4), (1, 1, 64), (2, 3, 8), (5, 1, 68), (1, 7, 260), (3, 2, 128), (9, 1, 192)])
+@pytest.mark.parametrize("w_dt,x_dt", [(we.FP8, we.BF16), (we.FP8, we.F32), (we.BF16, we.F16)])
+def test_tiny_shapes(graph, m, n, k, w_dt, x_dt):
+    """Shapes far below every tile: one output column, one row, K of a single vec4 (the reference's smallest
+    unit, matmulParams' K % 4 rule) and K one vec4 past a 64-k block. f32 output against the oracle."""
+    rng = np.random.default_rng(m * 100 + n * 10 + k)
+    x_store, x_oracle, ox = encode_act(rng.standard_normal(m * k).astype(np.float32), x_dt)
+    if w_dt == we.FP8:
+        w = rng.integers(0, 254, n * k).astype(np.uint8)
+        w = (w + (w >= 0x7F)).astype(np.uint8)
+        ow = O.FP8
+    else:
+        w = O.bf16_rne(rng.standard_normal(n * k).astype(np.float32))
+        ow = O.BF16
+    p = we.matmul_params(m, n, k, 0.5, graph=graph)
+    got = run(graph, p, x_store, x_dt, w, w_dt, we.F32)
+    want = O.matmul(O.matmul_params(m, n, k, 0.5), ox, x_oracle, ow, w)
+    assert O.rel_error(got, want) < TOL_F32_OUT
