@@ -73,8 +73,9 @@ struct GemmLaunch {
   // planes): k runs over all planes and the weights are read at k mod k_wrap. Fast path only (k_wrap % 64 == 0).
   uint32_t k_wrap;
   // split-K for small M: K in rsplits slices of rkc, partial sums in scratch (rsplits * m * n f32), then a
-  // reduce pass that runs the epilogue
+  // reduce pass that runs the epilogue; rcfg: the tile configuration the slices were sized for (-1: by shape)
   uint32_t rsplits, rkc;
+  int rcfg;
   void* scratch;
 };
 hipError_t gemm_launch(const GemmLaunch& L, hipStream_t stream);
@@ -88,6 +89,7 @@ hipError_t gemm_fast_launch_pair(const GemmLaunch& A, const GemmLaunch& B, hipSt
 struct GemmReducePlan {
   uint32_t rsplits, rkc;
   size_t scratch_bytes;
+  int rcfg;  // the tile configuration the slices are sized for, -1: the launch picks by shape
 };
 GemmReducePlan gemm_reduce_plan(const GemmLaunch& L, uint32_t force_splits = 0);  // force_splits: sweeps
 // The straight-line fast path; hipErrorNotSupported when the operands do not qualify.

@@ -951,6 +951,7 @@ void fill_gemm(we::GemmLaunch& L, const we::Tuning& t, const we_matmul_params* p
   L.generic = t.gemm_generic;
   L.reduce_xcd = t.gemm_reduce_xcd;
   L.rsplits = 1;
+  L.rcfg = -1;
   L.rkc = L.k;
   L.scratch = nullptr;
 }
@@ -1047,7 +1048,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
     qk_fused = we::gemm_qk_fusable(L);
     if (!qk_fused) L.qk_cols = L.q_cols = 0;  // the plain GEMM, then the q/k pass below
   }
-  we::GemmReducePlan rp{1, L.k, 0};
+  we::GemmReducePlan rp{1, L.k, 0, -1};
   if (ctx->tune.gemm_splitk != 0) {  // 0: split-K off; n > 0: n slices (sweeps)
     const uint32_t force = ctx->tune.gemm_splitk > 0 ? (uint32_t)ctx->tune.gemm_splitk : 0u;
     rp = we::gemm_reduce_plan(L, force);
@@ -1064,6 +1065,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
       L.scratch = (char*)ctx->scratch + plane_bytes;
       L.rsplits = rp.rsplits;
       L.rkc = rp.rkc;
+      L.rcfg = rp.rcfg;
     }
   } else {
     if (rp.rsplits > 1) {
@@ -1083,6 +1085,7 @@ int matmul_impl(we_ctx* ctx, const we_matmul_params* p, int x_dtype, const void*
       }
       L.rsplits = rp.rsplits;
       L.rkc = rp.rkc;
+      L.rcfg = rp.rcfg;
     }
   }
   hipError_t e = we::gemm_launch(L, ctx->compute);
